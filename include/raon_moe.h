@@ -1,0 +1,169 @@
+/*
+ * raon_moe.h -- C ABI of librmoe.so, the MI355X (gfx950) quantized-MoE hot path.
+ *
+ * The library replaces the device side of raon-npu's NPU backend for the q4nx
+ * mixture-of-experts path.  Every entry point below names the reference
+ * interface it stands in for (paths inside the reference tree).  The Python
+ * host mirror (raon-npu_amd/backend.py, class GpuBackend) binds these entry
+ * points with ctypes and keeps the reference's Backend method signatures.
+ *
+ * Conventions
+ *  - Every function returns an int status (RMOE_OK on success).  No C++
+ *    exception crosses the ABI.  rmoe_last_error() returns the message of the
+ *    last failure on the calling thread.
+ *  - bf16 values are uint16_t bit patterns; fp32 values are float.
+ *  - "Host" entry points take host pointers, borrow them for the call only,
+ *    and are synchronous.  "_dev" entry points take device pointers and a
+ *    hipStream_t passed as void* (NULL = the context's stream); they are
+ *    asynchronous and never allocate, so they can be captured in a HIP graph.
+ *  - Device memory (weights, scratch) is owned by the context.  A context is
+ *    not thread-safe: calls that overlap on one context race on its scratch.
+ *
+ * Weight format at the boundary is the reference's q4nx pack_gemv layout
+ * (quant/q4nx.py:335-393); per-expert bundles are the concatenations of
+ * kernels/moe/pack.py:136-224 (expert e at offset e * expert_bytes; gate rows
+ * then up rows in one [2I, H] matrix; down [H, Ipad]).  Uploads re-lay the
+ * bytes on the device into the library's own tile layout.
+ */
+#ifndef RAON_MOE_H
+#define RAON_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes; the Python mirror maps them to the reference's exception types. */
+#define RMOE_OK 0
+#define RMOE_EINVAL 1   /* ValueError: shape/dtype/contract violation (npu/backend.py:4864-4897) */
+#define RMOE_ENOTFOUND 2 /* KeyError: unknown weight or layer (npu/backend.py:3609)               */
+#define RMOE_EDEVICE 3  /* RuntimeError: HIP/device failure (npu/backend.py:1429-1437)            */
+#define RMOE_ENOMEM 4   /* RuntimeError: device allocation failed                                 */
+
+/* Activations (host/backend.py:47-62 SiTU-GLU; kernels/moe/reference.py:127-180 SwiGLU). */
+#define RMOE_ACT_SITU 0
+#define RMOE_ACT_SWIGLU 1
+
+/* Router score functions (host/raon.py:1233-1234 sigmoid; softmax for BASELINE configs). */
+#define RMOE_SCORE_SIGMOID 0
+#define RMOE_SCORE_SOFTMAX 1
+
+typedef struct rmoe_ctx rmoe_ctx;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* rmoe_last_error(void);
+
+/* Library version string. */
+const char* rmoe_version(void);
+
+/* Context lifetime.  Replaces NpuBackend.__init__ device set-up (npu/backend.py:2404-2521)
+ * and the XRT device/runner it opens. */
+int rmoe_create(int device, rmoe_ctx** out);
+int rmoe_destroy(rmoe_ctx* ctx);
+/* Wait for all work queued on the context's stream (run.wait(), npu/backend.py:2236-2244). */
+int rmoe_synchronize(rmoe_ctx* ctx);
+/* The context's HIP stream, as void*. */
+void* rmoe_stream(rmoe_ctx* ctx);
+
+/* ---------------------------------------------------------------- q4nx matrices --
+ * Dense q4nx matrices ("bundles" of npu/backend.py:360-392, e.g. dense_gu) served by
+ * rmoe_linear.  M % 128 == 0 and K % 256 == 0 (quant/q4nx.py:358-366).          */
+
+/* Upload pack_gemv bytes of an [M, K] matrix; returns a handle.  Replaces the bundle
+ * upload of NpuBackend.preload / _get_weight_tensor (npu/backend.py:3265). */
+int rmoe_matrix_upload(rmoe_ctx* ctx, const void* pack_gemv_bytes, size_t nbytes, int M, int K, int* handle);
+/* Allocate an [M, K] matrix and fill it by quantizing fp32 device weights w_dev [M, K]
+ * row-major on the device (quant/q4nx.py:127-200, bit-exact). */
+int rmoe_matrix_quantize_dev(rmoe_ctx* ctx, const float* w_dev, int M, int K, int* handle, void* stream);
+/* Read a matrix back as pack_gemv bytes (inverse re-layout; used for round trips). */
+int rmoe_matrix_download(rmoe_ctx* ctx, int handle, void* pack_gemv_bytes, size_t nbytes);
+int rmoe_matrix_free(rmoe_ctx* ctx, int handle);
+int rmoe_matrix_shape(rmoe_ctx* ctx, int handle, int* M, int* K);
+
+/* y[T, M] = RTNE_bf16(x[T, K] @ W^T), fp32 accumulation.  Replaces NpuBackend.linear /
+ * _execute_gemv for a q4nx bundle (npu/backend.py:3569-3721, 3908-4021) and
+ * Backend.linear_batch (host/backend.py:71-74).  K_in <= K: columns past K_in are zero
+ * padding (comp.padded_k > comp.orig_k, npu/backend.py:3680-3684). */
+int rmoe_linear(rmoe_ctx* ctx, int handle, const uint16_t* x, int T, int K_in, uint16_t* y);
+int rmoe_linear_dev(rmoe_ctx* ctx, int handle, const void* x_dev, int T, void* y_dev, void* stream);
+/* Size the scratch that rmoe_linear_dev needs for up to T tokens on this matrix. */
+int rmoe_reserve_linear(rmoe_ctx* ctx, int handle, int T);
+
+/* --------------------------------------------------------------- MoE layers --
+ * One MoE layer: n_routed experts + n_shared (0 or 1) shared expert, hidden H,
+ * intermediate I (down input padded to Ipad = ceil(I/256)*256), router [n_routed, H].
+ * H % 256 == 0, (2I) % 128 == 0, I % 64 == 0 (kernels/moe/pack.py:40-87). */
+int rmoe_layer_create(rmoe_ctx* ctx, int layer, int hidden, int inter, int n_routed, int n_shared, int top_k);
+/* Size the context scratch so that the "_dev" entry points of this layer accept up to
+ * max_tokens tokens (they never allocate).  Replaces NpuBackend._prepared_buffer set-up. */
+int rmoe_reserve(rmoe_ctx* ctx, int layer, int max_tokens);
+/* Expert bundles in kernels/moe/pack.py geometry: (n_routed + n_shared) experts back to back.
+ * gate_up: expert_bytes = 2I*H*5/8; down: H*Ipad*5/8.  Replaces moe_b1/moe_b2 uploads. */
+int rmoe_layer_upload_experts(rmoe_ctx* ctx, int layer, const void* gate_up, size_t gu_nbytes,
+                              const void* down, size_t dn_nbytes);
+/* Quantize one expert from fp32 device weights (gate_up [2I, H], down [H, I] row-major;
+ * the down input columns past I are zero-padded to Ipad).  Bit-exact quant/q4nx.py:127-200. */
+int rmoe_layer_quantize_expert_dev(rmoe_ctx* ctx, int layer, int expert, const float* gate_up_dev,
+                                   const float* down_dev, void* stream);
+/* Read one expert back as pack_gemv bytes (round trips, oracle cross-checks). */
+int rmoe_layer_download_expert(rmoe_ctx* ctx, int layer, int expert, void* gate_up, size_t gu_nbytes,
+                               void* down, size_t dn_nbytes);
+/* Router of the layer (host/raon.py:1224-1247): weight bf16 [n_routed, H]; bias fp32
+ * [n_routed] or NULL (selection-only e_score_correction_bias); score RMOE_SCORE_*;
+ * renormalize 0/1; scaling = routed_scaling_factor. */
+int rmoe_layer_set_router(rmoe_ctx* ctx, int layer, const uint16_t* weight, const float* bias,
+                          int score, int renormalize, float scaling);
+int rmoe_layer_set_router_dev(rmoe_ctx* ctx, int layer, const void* weight_dev, const float* bias_host,
+                              int score, int renormalize, float scaling);
+int rmoe_layer_free(rmoe_ctx* ctx, int layer);
+
+/* Router + top-k for T tokens (RaonModel._route_token, host/raon.py:1224-1247).
+ * top_ids int32 [T, k], weights fp32 [T, k], logits fp32 [T, n_routed] (may be NULL).
+ * Top-k ties keep the lower expert id first. */
+int rmoe_route(rmoe_ctx* ctx, int layer, const uint16_t* x, int T, int32_t* top_ids, float* weights,
+               float* logits);
+
+/* Routed experts for one token: Backend.moe_experts (host/backend.py:98-117,466-510;
+ * npu/backend.py:5029-5322).  Ascending-expert-id fp32 combine, RTNE.  act RMOE_ACT_*. */
+int rmoe_moe_experts(rmoe_ctx* ctx, int layer, const uint16_t* x, const int32_t* top_ids,
+                     const float* top_weights, int k, int act, float gate_beta, float value_beta,
+                     uint16_t* out);
+
+/* Router + routed + shared expert + combine for one decode token, all on the device:
+ * RaonModel._moe_token (host/raon.py:1288-1330) with the router moved onto the GPU.
+ * out = RTNE(f32(routed) + f32(shared)); with residual != 0 also adds x:
+ * out = RTNE(f32(x) + f32(out)).  top_ids/top_weights (device, may be NULL) receive
+ * the routing of the token. */
+int rmoe_moe_decode_dev(rmoe_ctx* ctx, int layer, const void* x_dev, void* out_dev, int residual,
+                        int act, float gate_beta, float value_beta, void* top_ids_dev,
+                        void* top_weights_dev, void* stream);
+int rmoe_moe_decode(rmoe_ctx* ctx, int layer, const uint16_t* x, uint16_t* out, int residual,
+                    int act, float gate_beta, float value_beta, int32_t* top_ids, float* top_weights);
+
+/* Dispatch permutation (kernels/moe_grouped/planner.py:76-108 flattened): top_ids int32
+ * [T, k] -> order int32 [T*k] (assignment index t*k + r at each expert-sorted position;
+ * ascending expert, then token, then route) and offsets int32 [n_experts + 1]. */
+int rmoe_dispatch(rmoe_ctx* ctx, const int32_t* top_ids, int T, int k, int n_experts, int32_t* order,
+                  int32_t* offsets);
+
+/* Grouped prefill MoE: NpuBackend.moe_experts_grouped (npu/backend.py:4845-4979).
+ * x [T, H], top_ids [T, k] (distinct per token, 0..n_routed-1), top_weights fp32 [T, k],
+ * shared_gu [T, 2I] -> routed [T, H] and shared_down [T, H]. */
+int rmoe_moe_experts_grouped(rmoe_ctx* ctx, int layer, const uint16_t* x, int T, const int32_t* top_ids,
+                             const float* top_weights, const uint16_t* shared_gu, int act, float gate_beta,
+                             float value_beta, uint16_t* routed, uint16_t* shared_down);
+
+/* Full prefill MoE layer on the device (host/raon.py:1565-1602 grouped branch): router,
+ * dispatch, grouped gate/up + activation, grouped down, ordered combine, shared expert.
+ * out [T, H] = RTNE(f32(routed) + f32(shared_down)) (+ x when residual != 0). */
+int rmoe_moe_prefill_dev(rmoe_ctx* ctx, int layer, const void* x_dev, int T, void* out_dev, int residual,
+                         int act, float gate_beta, float value_beta, void* top_ids_dev,
+                         void* top_weights_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RAON_MOE_H */

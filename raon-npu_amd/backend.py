@@ -1,0 +1,289 @@
+"""GpuBackend: the MI355X drop-in for the MoE side of raon-npu's NPU backend.
+
+``RaonModel`` (host/raon.py) and ``Engine`` (serve/engine.py) drive a backend
+through the ``Backend`` interface of ``host/backend.py:65-204`` plus the NPU
+extras ``moe_experts_grouped``/``preload``/``set_step`` (npu/backend.py:4845,
+3265, 2805).  This class keeps those method names, argument meanings, dtypes
+and exception types for the q4nx MoE path:
+
+* ``linear`` / ``linear_batch``  -- q4nx bundle GEMV (npu/backend.py:3569-3721)
+* ``moe_experts``                -- routed experts of one token (host/backend.py:98-117)
+* ``moe_experts_grouped``        -- grouped prefill (npu/backend.py:4845-4979)
+* ``moe_prestart_shared`` & co.  -- overlap hooks, no-ops here (results never depend on them)
+* ``prefill_shared_precompute`` / ``prefill_grouped_moe`` flags (npu/backend.py:2523-2547)
+
+Weights are registered from the reference's q4nx byte layouts (``pack_gemv``
+bundles); the device re-lays them at upload.  The attention-side methods of
+the reference ``Backend`` (RDA, MLA) are outside the MoE hot path and raise
+``NotImplementedError``.
+"""
+
+from __future__ import annotations
+
+import time
+from collections import defaultdict
+from dataclasses import dataclass
+
+import numpy as np
+
+from .device import Context, Matrix, MoeLayer, act_code
+from .geometry import MoeGeometry
+
+
+def _f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bits, RNE, NaN -> 0x7FC0 (host/weights.py:104-115): input conversion only."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    u = a.view(np.uint32)
+    out = ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+    nan = np.isnan(a)
+    if nan.any():
+        out[nan] = 0x7FC0
+    return out
+
+
+def _bf16_to_f32(u: np.ndarray) -> np.ndarray:
+    return (np.asarray(u, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+@dataclass
+class _Component:
+    """A named projection served by a row slice of a bundle (npu/backend.py:360-392)."""
+
+    bundle: str
+    row_start: int
+    row_end: int
+    orig_k: int
+
+
+class GpuBackend:
+    """MoE hot path of the raon-npu backend on one MI355X (gfx950)."""
+
+    _TIMING_KEYS = ("linear_gpu", "moe_gpu", "moe_grouped_gpu", "moe_host", "route_gpu")
+
+    def __init__(self, device: int = 0, *, activation: str | None = None):
+        self.ctx = Context(device)
+        self.activation = activation  # "swiglu" forces SwiGLU; None follows the betas
+        self._bundles: dict[str, Matrix] = {}
+        self._components: dict[str, _Component] = {}
+        self._layers: dict[int, MoeLayer] = {}
+        self._step_id = 0
+        self._bundle_cache: dict[str, tuple[int, int, np.ndarray]] = {}
+        self._cached_inputs: dict[str, np.ndarray] = {}
+        self.prefill_shared_precompute: bool = True
+        self.prefill_grouped_moe: bool = True
+        self.timings: dict[str, float] = {}
+        self.call_counts: dict[str, int] = defaultdict(int)
+        self.reset_timings()
+
+    # ----------------------------------------------------------- bookkeeping --
+    def reset_timings(self) -> None:
+        self.timings = {k: 0.0 for k in self._TIMING_KEYS}
+        self.call_counts = defaultdict(int)
+
+    def _add_timing(self, key: str, dt: float, count: int = 1) -> None:
+        self.timings[key] = self.timings.get(key, 0.0) + dt
+        self.call_counts[key] += count
+
+    def set_step(self, step: int) -> None:
+        """Token step id for the bundle-reuse rule (npu/backend.py:2805)."""
+        self._step_id = int(step)
+
+    def preload(self, num_layers: int | None = None) -> None:
+        """Weights are resident from registration on; nothing to stage (npu/backend.py:3265)."""
+        return None
+
+    def reset(self) -> None:
+        """MoE is stateless; clears only the per-step bundle cache."""
+        self._bundle_cache.clear()
+        self._cached_inputs.clear()
+
+    # ---------------------------------------------------------- registration --
+    def register_bundle(self, bundle: str, packed: bytes | np.ndarray, M: int, K: int) -> None:
+        """Upload one q4nx bundle (pack_gemv bytes of an [M, K] matrix)."""
+        self._bundles[bundle] = self.ctx.upload_matrix(packed, M, K)
+
+    def register_component(self, name: str, bundle: str, row_start: int, row_end: int, orig_k: int | None = None) -> None:
+        """Serve weight ``name`` as rows ``[row_start, row_end)`` of ``bundle``."""
+        mat = self._bundles[bundle]
+        if not 0 <= row_start < row_end <= mat.M:
+            raise ValueError(f"rows [{row_start}, {row_end}) outside bundle {bundle!r} with {mat.M} rows")
+        self._components[name] = _Component(bundle, row_start, row_end, orig_k or mat.K)
+
+    def register_moe_layer(self, layer: int, geom: MoeGeometry, gate_up: bytes | np.ndarray, down: bytes | np.ndarray,
+                           router_weight: np.ndarray | None = None, router_bias: np.ndarray | None = None,
+                           score: str = "softmax", renormalize: bool = True, scaling: float = 1.0) -> MoeLayer:
+        """Upload one layer's expert bundles (kernels/moe/pack.py geometry) and optional router."""
+        lyr = self.ctx.create_layer(layer, geom)
+        lyr.upload_experts(gate_up, down)
+        if router_weight is not None:
+            lyr.set_router(router_weight, router_bias, score, renormalize, scaling)
+        self._layers[int(layer)] = lyr
+        return lyr
+
+    def layer(self, layer: int) -> MoeLayer:
+        try:
+            return self._layers[int(layer)]
+        except KeyError:
+            raise ValueError(f"layer {layer} is not an exported MoE layer") from None
+
+    def __contains__(self, name: str) -> bool:
+        return name in self._components or name in self._bundles
+
+    # ---------------------------------------------------------------- linear --
+    def _resolve(self, name: str) -> tuple[Matrix, _Component]:
+        comp = self._components.get(name)
+        if comp is None:
+            if name in self._bundles:
+                m = self._bundles[name]
+                return m, _Component(name, 0, m.M, m.K)
+            raise KeyError(f"Weight parameter '{name}' not found in GPU bundle map")
+        return self._bundles[comp.bundle], comp
+
+    def linear(self, name: str, x: np.ndarray) -> np.ndarray:
+        """``y = x @ W^T`` over a q4nx bundle row slice (npu/backend.py:3569-3721).
+
+        bf16 (uint16) input gives bf16 output.  fp32 input is rounded to bf16 for
+        the GEMV and the bf16 result is returned as fp32, as the NPU path does.
+        Reuse rule: a bundle computed for the same step and the same input object
+        is sliced from the cache (npu/backend.py:3652-3663).
+        """
+        t0 = time.perf_counter()
+        is_f32 = x.dtype == np.float32
+        xu = _f32_to_bf16(x) if is_f32 else np.asarray(x, dtype=np.uint16)
+        mat, comp = self._resolve(name)
+        if xu.shape[-1] != comp.orig_k:
+            raise ValueError(f"{name}: input width {xu.shape[-1]} != {comp.orig_k}")
+        cached = self._bundle_cache.get(comp.bundle)
+        if cached is not None and cached[0] == self._step_id and cached[1] == id(x) and self._cached_inputs.get(comp.bundle) is x:
+            y_full = cached[2]
+        else:
+            y_full = mat.linear(xu)
+            self._bundle_cache[comp.bundle] = (self._step_id, id(x), y_full)
+            self._cached_inputs[comp.bundle] = x
+        out = y_full[..., comp.row_start : comp.row_end].copy()
+        self._add_timing("linear_gpu", time.perf_counter() - t0)
+        return _bf16_to_f32(out) if is_f32 else out
+
+    def linear_batch(self, name: str, x: np.ndarray) -> np.ndarray:
+        """``[T, K]`` -> ``[T, M]``, byte-identical to stacked ``linear`` (host/backend.py:71-74)."""
+        xa = np.asarray(x)
+        if xa.ndim != 2:
+            raise ValueError("linear_batch expects [T, K]")
+        mat, comp = self._resolve(name)
+        if xa.shape[1] != comp.orig_k:
+            raise ValueError(f"{name}: input width {xa.shape[1]} != {comp.orig_k}")
+        t0 = time.perf_counter()
+        y = mat.linear(np.asarray(xa, dtype=np.uint16))[:, comp.row_start : comp.row_end].copy()
+        self._add_timing("linear_gpu", time.perf_counter() - t0)
+        return y
+
+    # overlap hooks (host/backend.py:119-155): results never depend on them
+    def moe_prestart_shared(self, layer: int, x: np.ndarray) -> None:
+        return None
+
+    def moe_abort_prestart_shared(self) -> None:
+        return None
+
+    def prefetch_linears(self, items) -> None:
+        return None
+
+    def linear_start(self, name: str, x: np.ndarray) -> object:
+        return (name, x)
+
+    def linear_finish(self, pending: object) -> np.ndarray:
+        name, x = pending
+        return self.linear(name, x)
+
+    def linear_abort(self, pending: object) -> None:
+        return None
+
+    # ------------------------------------------------------------------- MoE --
+    def _act(self, gate_beta, value_beta):
+        if self.activation == "swiglu":
+            return None, None
+        return gate_beta, value_beta
+
+    def moe_experts(self, layer: int, x: np.ndarray, top_ids: np.ndarray, top_weights: np.ndarray,
+                    gate_beta: float | None = 4.0, value_beta: float | None = 25.0,
+                    shared_gu: np.ndarray | None = None) -> np.ndarray:
+        """Weighted sum of the routed experts for one token (host/backend.py:466-510).
+
+        Experts are combined in ascending id in fp32 and rounded to bf16 once.
+        ``shared_gu`` is validated like npu/backend.py:5046-5055 and otherwise
+        ignored: the shared expert is not part of this sum.
+        """
+        lyr = self.layer(layer)
+        if shared_gu is not None:
+            if not isinstance(shared_gu, np.ndarray) or shared_gu.dtype != np.uint16 or shared_gu.shape != (2 * lyr.geom.inter,):
+                raise ValueError(f"shared_gu must be a [{2 * lyr.geom.inter}] uint16 ndarray")
+        xu = _f32_to_bf16(x) if x.dtype == np.float32 else np.asarray(x, dtype=np.uint16)
+        t0 = time.perf_counter()
+        gb, vb = self._act(gate_beta, value_beta)
+        out = lyr.moe_experts(xu.reshape(-1)[: lyr.geom.hidden], np.asarray(top_ids), np.asarray(top_weights, np.float32), gb, vb)
+        self._add_timing("moe_gpu", time.perf_counter() - t0)
+        return out
+
+    def moe_experts_grouped(self, layer: int, x: np.ndarray, top_ids: np.ndarray, top_weights: np.ndarray,
+                            shared_gu: np.ndarray, gate_beta: float | None = 4.0,
+                            value_beta: float | None = 25.0) -> tuple[np.ndarray, np.ndarray]:
+        """Grouped routed sums and shared down rows for ``T`` tokens (npu/backend.py:4845-4979).
+
+        Validation follows npu/backend.py:4864-4897 with the layer's geometry.
+        """
+        if not isinstance(layer, (int, np.integer)):
+            raise ValueError("layer must be an integer")
+        lyr = self.layer(int(layer))
+        g = lyr.geom
+        if not isinstance(x, np.ndarray) or x.dtype != np.uint16 or x.ndim != 2:
+            raise ValueError(f"x must be a [T, {g.hidden}] uint16 ndarray")
+        if x.shape[0] < 1 or x.shape[1] != g.hidden:
+            raise ValueError(f"x must be a [T, {g.hidden}] uint16 ndarray with T >= 1")
+        T = x.shape[0]
+        if (not isinstance(top_ids, np.ndarray) or not np.issubdtype(top_ids.dtype, np.integer)
+                or top_ids.shape != (T, g.top_k)):
+            raise ValueError(f"top_ids must be an integer ndarray with shape [T, {g.top_k}]")
+        if np.any(top_ids < 0) or np.any(top_ids >= g.n_routed):
+            raise ValueError(f"top_ids values must be in 0..{g.n_routed - 1}")
+        s = np.sort(top_ids, axis=1)
+        if np.any(s[:, 1:] == s[:, :-1]):
+            raise ValueError(f"each token must route to {g.top_k} distinct experts")
+        if (not isinstance(top_weights, np.ndarray) or top_weights.dtype != np.float32
+                or top_weights.shape != (T, g.top_k)):
+            raise ValueError(f"top_weights must be a float32 ndarray with shape [T, {g.top_k}]")
+        if (not isinstance(shared_gu, np.ndarray) or shared_gu.dtype != np.uint16
+                or shared_gu.shape != (T, 2 * g.inter)):
+            raise ValueError(f"shared_gu must be a [T, {2 * g.inter}] uint16 ndarray")
+        t0 = time.perf_counter()
+        gb, vb = self._act(gate_beta, value_beta)
+        routed, sdown = lyr.moe_experts_grouped(x, top_ids, top_weights, shared_gu, gb, vb)
+        self._add_timing("moe_grouped_gpu", time.perf_counter() - t0, count=T)
+        return routed, sdown
+
+    def route(self, layer: int, x: np.ndarray):
+        """Device router for ``[T, H]`` or ``[H]`` tokens -> (top int32, weights f32, logits f32)."""
+        t0 = time.perf_counter()
+        out = self.layer(layer).route(np.asarray(x, dtype=np.uint16))
+        self._add_timing("route_gpu", time.perf_counter() - t0)
+        return out
+
+    # ------------------------------------------------ outside the MoE hot path --
+    def rda_update(self, *a, **k):
+        raise NotImplementedError("RDA recurrence is outside the MoE hot path served by GpuBackend")
+
+    def mla_attend(self, *a, **k):
+        raise NotImplementedError("MLA attention is outside the MoE hot path served by GpuBackend")
+
+    def mla_attend_chunk(self, *a, **k):
+        raise NotImplementedError("MLA attention is outside the MoE hot path served by GpuBackend")
+
+    def set_rda_state(self, *a, **k):
+        raise NotImplementedError("RDA state is outside the MoE hot path served by GpuBackend")
+
+    def get_rda_state(self, *a, **k):
+        raise NotImplementedError("RDA state is outside the MoE hot path served by GpuBackend")
+
+    def set_mla_cache(self, *a, **k):
+        raise NotImplementedError("MLA cache is outside the MoE hot path served by GpuBackend")
+
+    def get_mla_cache(self, *a, **k):
+        raise NotImplementedError("MLA cache is outside the MoE hot path served by GpuBackend")

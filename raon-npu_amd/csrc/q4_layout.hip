@@ -1,0 +1,212 @@
+// q4nx format kernels: pack_gemv <-> device tile layout, and the device quantizer.
+//
+// pack_gemv layout: quant/q4nx.py:335-393 (32x256 blocks of 5,120 B, block order
+// ((slice*k_blocks + kb)*4 + r), scales/mins [group][row], codes in
+// (half, group, col, row16) order with two rows per byte).  The device tile layout
+// is described in rmoe_internal.h.
+#include "rmoe_internal.h"
+
+namespace rmoe {
+namespace {
+
+// Position of (row r, group g) inside a pack_gemv buffer.
+struct PackPos {
+  size_t base;  // block byte offset
+  int r32, half, r16, gg;
+};
+
+__device__ __forceinline__ PackPos pack_pos(int r, int g, int K) {
+  const int kblocks = K / 256;
+  const int slice = r / 128, rw = (r % 128) / 32, r32 = r % 32;
+  const int kb = g / 8, gg = g % 8;
+  PackPos p;
+  p.base = ((size_t)(slice * kblocks + kb) * 4 + rw) * 5120;
+  p.r32 = r32;
+  p.half = r32 / 16;
+  p.r16 = r32 % 16;
+  p.gg = gg;
+  return p;
+}
+
+// Column c (0..31) of a group -> (dword, nibble) inside the lane's 16 bytes.
+__device__ __forceinline__ int tile_nibble_index(int c) {
+  const int d = c >> 3, w = c & 7;
+  const int q = (w & 1) ? (w >> 1) + 4 : (w >> 1);
+  return d * 8 + q;  // nibble index 0..31 over the 4 dwords
+}
+
+// Thread = (tile, j, lane): gathers row (64*rt + lane), group (4*kt + j).
+__global__ void relayout_in_kernel(const uint8_t* __restrict__ packed, uint8_t* __restrict__ tiles, int M, int K) {
+  const int G = K / 32, nkt = K / 128;
+  const size_t n = (size_t)M * G;
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n) return;
+  const int lane = idx & 63;
+  const size_t rest = idx >> 6;
+  const int j = rest & 3;
+  const size_t tile = rest >> 2;
+  const int rt = (int)(tile / nkt), kt = (int)(tile % nkt);
+  const int r = rt * 64 + lane, g = kt * 4 + j;
+  const PackPos p = pack_pos(r, g, K);
+  const uint16_t* sm = reinterpret_cast<const uint16_t*>(packed + p.base);
+  const uint32_t scale = sm[p.gg * 32 + p.r32];
+  const uint32_t mn = sm[256 + p.gg * 32 + p.r32];
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+  const uint8_t* cbase = packed + p.base + 1024 + (size_t)((p.half * 8 + p.gg) * 32) * 8 + (p.r16 >> 1);
+  const int shift = (p.r16 & 1) ? 4 : 0;
+#pragma unroll 8
+  for (int c = 0; c < 32; ++c) {
+    const uint32_t code = (cbase[c * 8] >> shift) & 15u;
+    const int ni = tile_nibble_index(c);
+    w[ni >> 3] |= code << (4 * (ni & 7));
+  }
+  uint8_t* t = tiles + tile * kTileBytes;
+  *reinterpret_cast<uint4*>(t + j * 1024 + lane * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+  *reinterpret_cast<uint32_t*>(t + kCodeBytes + lane * 16 + j * 4) = scale | (mn << 16);
+}
+
+// Thread = (row pair, group): writes both rows' nibbles (one byte per column).
+__global__ void relayout_out_kernel(const uint8_t* __restrict__ tiles, uint8_t* __restrict__ packed, int M, int K) {
+  const int G = K / 32, nkt = K / 128;
+  const size_t n = (size_t)(M / 2) * G;
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n) return;
+  const int g = (int)(idx % G);
+  const int r0 = (int)(idx / G) * 2;
+  const int kt = g / 4, j = g % 4;
+  uint32_t w[2][4];
+  uint32_t smv[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int r = r0 + h;
+    const uint8_t* t = tiles + ((size_t)(r / 64) * nkt + kt) * kTileBytes;
+    const uint4 c = *reinterpret_cast<const uint4*>(t + j * 1024 + (r % 64) * 16);
+    w[h][0] = c.x; w[h][1] = c.y; w[h][2] = c.z; w[h][3] = c.w;
+    smv[h] = *reinterpret_cast<const uint32_t*>(t + kCodeBytes + (r % 64) * 16 + j * 4);
+  }
+  const PackPos p = pack_pos(r0, g, K);
+  uint16_t* sm = reinterpret_cast<uint16_t*>(packed + p.base);
+  sm[p.gg * 32 + p.r32] = (uint16_t)(smv[0] & 0xffffu);
+  sm[p.gg * 32 + p.r32 + 1] = (uint16_t)(smv[1] & 0xffffu);
+  sm[256 + p.gg * 32 + p.r32] = (uint16_t)(smv[0] >> 16);
+  sm[256 + p.gg * 32 + p.r32 + 1] = (uint16_t)(smv[1] >> 16);
+  uint8_t* cbase = packed + p.base + 1024 + (size_t)((p.half * 8 + p.gg) * 32) * 8 + (p.r16 >> 1);
+#pragma unroll 8
+  for (int c = 0; c < 32; ++c) {
+    const int ni = tile_nibble_index(c);
+    const uint32_t lo = (w[0][ni >> 3] >> (4 * (ni & 7))) & 15u;
+    const uint32_t hi = (w[1][ni >> 3] >> (4 * (ni & 7))) & 15u;
+    cbase[c * 8] = (uint8_t)(lo | (hi << 4));
+  }
+}
+
+// ------------------------------------------------------------------ quantizer --
+// Bit-exact restatement of quant/q4nx.py:127-200 per (row, group), in float64 where
+// the reference uses float64.
+__device__ __forceinline__ float bits_f(uint32_t u) { return __uint_as_float(u); }
+
+__device__ __forceinline__ float bf16_floor_f32(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t bump = ((u >> 31) && (u & 0xffffu)) ? 1u : 0u;
+  return bits_f(((u >> 16) + bump) << 16);
+}
+
+__device__ __forceinline__ float bf16_ceil_f64(double x) {
+  float f = __double2float_rn(x);
+  if ((double)f < x) f = nextafterf(f, __builtin_inff());
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t bump = (!(u >> 31) && (u & 0xffffu)) ? 1u : 0u;
+  return bits_f(((u >> 16) + bump) << 16);
+}
+
+__device__ __forceinline__ float bf16_next_up(float x) {
+  uint32_t h = __float_as_uint(x) >> 16;
+  if (h == 0x8000u) h = 0u;
+  uint32_t nx;
+  if (h == 0u) nx = 1u;
+  else if (h & 0x8000u) nx = (h == 0x8001u) ? 0u : h - 1u;
+  else nx = h + 1u;
+  return bits_f(nx << 16);
+}
+
+__global__ void quantize_kernel(const float* __restrict__ w, int M, int K, int ld, int k_valid,
+                                uint8_t* __restrict__ tiles, int* __restrict__ err) {
+  const int G = K / 32, nkt = K / 128;
+  const size_t n = (size_t)M * G;
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n) return;
+  const int lane = idx & 63;
+  const size_t rest = idx >> 6;
+  const int j = rest & 3;
+  const size_t tile = rest >> 2;
+  const int rt = (int)(tile / nkt), kt = (int)(tile % nkt);
+  const int r = rt * 64 + lane, g = kt * 4 + j;
+  const float* row = w + (size_t)r * ld;
+  float v[32];
+  bool finite = true;
+#pragma unroll
+  for (int c = 0; c < 32; ++c) {
+    const int col = g * 32 + c;
+    v[c] = col < k_valid ? row[col] : 0.f;
+    finite = finite && isfinite(v[c]);
+  }
+  if (!finite) atomicOr(err, 1);
+  float lo = v[0], hi = v[0];
+#pragma unroll
+  for (int c = 1; c < 32; ++c) {
+    lo = fminf(lo, v[c]);
+    hi = fmaxf(hi, v[c]);
+  }
+  const float minq = bf16_floor_f32(lo);
+  const double min64 = (double)minq, hi64 = (double)hi;
+  const double span = hi64 - min64;
+  float sc = bf16_ceil_f64(span / 15.0);
+  for (int it = 0; it < 64; ++it) {
+    if (!isfinite(sc)) break;
+    if (min64 + 15.0 * (double)sc >= hi64) break;
+    sc = bf16_next_up(sc);
+  }
+  const bool flat = span == 0.0;
+  if (flat) sc = 0.f;
+  if (!isfinite(minq) || !isfinite(sc)) atomicOr(err, 2);
+  const double div = flat ? 1.0 : (double)sc;
+  uint32_t words[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int c = 0; c < 32; ++c) {
+    double q = rint(((double)v[c] - min64) / div);
+    q = q < 0.0 ? 0.0 : (q > 15.0 ? 15.0 : q);
+    const uint32_t code = flat ? 0u : (uint32_t)q;
+    const int ni = tile_nibble_index(c);
+    words[ni >> 3] |= code << (4 * (ni & 7));
+  }
+  uint8_t* t = tiles + tile * kTileBytes;
+  *reinterpret_cast<uint4*>(t + j * 1024 + lane * 16) = make_uint4(words[0], words[1], words[2], words[3]);
+  const uint32_t sb = __float_as_uint(sc) >> 16, mb = __float_as_uint(minq) >> 16;
+  *reinterpret_cast<uint32_t*>(t + kCodeBytes + lane * 16 + j * 4) = sb | (mb << 16);
+}
+
+}  // namespace
+
+hipError_t launch_relayout_in(const uint8_t* packed, uint8_t* tiles, int M, int K, hipStream_t st) {
+  const size_t n = (size_t)M * (K / 32);
+  const unsigned blocks = (unsigned)((n + 255) / 256);
+  hipLaunchKernelGGL(relayout_in_kernel, dim3(blocks), dim3(256), 0, st, packed, tiles, M, K);
+  return hipGetLastError();
+}
+
+hipError_t launch_relayout_out(const uint8_t* tiles, uint8_t* packed, int M, int K, hipStream_t st) {
+  const size_t n = (size_t)(M / 2) * (K / 32);
+  const unsigned blocks = (unsigned)((n + 255) / 256);
+  hipLaunchKernelGGL(relayout_out_kernel, dim3(blocks), dim3(256), 0, st, tiles, packed, M, K);
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize(const float* w, int M, int K, int ld, int k_valid, uint8_t* tiles, int* err,
+                           hipStream_t st) {
+  const size_t n = (size_t)M * (K / 32);
+  const unsigned blocks = (unsigned)((n + 255) / 256);
+  hipLaunchKernelGGL(quantize_kernel, dim3(blocks), dim3(256), 0, st, w, M, K, ld, k_valid, tiles, err);
+  return hipGetLastError();
+}
+
+}  // namespace rmoe

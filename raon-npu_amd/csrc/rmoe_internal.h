@@ -1,0 +1,220 @@
+// Internal definitions shared by the librmoe HIP sources (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+// ---------------------------------------------------------------- tile layout --
+// The device copy of a q4nx matrix [M, K] is a grid of tiles of 64 rows x 128
+// columns (4 groups of 32 columns).  Tile (rt, kt) sits at byte offset
+// (rt * (K/128) + kt) * 5120, so a 64-row band is contiguous over K.
+// Inside a tile:
+//   bytes [0, 4096):   codes, 4 sub-blocks j (group 4*kt + j) of 64 lanes x 16 B;
+//                      lane L holds the 32 codes of row 64*rt + L for that group.
+//                      In dword d (columns 8d..8d+7 of the group) nibble q (bits
+//                      4q..4q+3) holds column 8d + 2q for q < 4 and column
+//                      8d + 2(q-4) + 1 for q >= 4, so one shift+mask yields the
+//                      bf16 pair for columns (8d+2q, 8d+2q+1).
+//   bytes [4096, 5120): per lane L 16 B: for j = 0..3 a dword (scale bf16 | min bf16 << 16)
+//                      of row 64*rt + L, group 4*kt + j.
+// 5,120 bytes hold 8,192 weights: 5 bits per weight, as in pack_gemv.
+namespace rmoe {
+
+constexpr int kTileRows = 64;
+constexpr int kTileCols = 128;
+constexpr int kTileBytes = 5120;
+constexpr int kGroup = 32;
+constexpr int kCodeBytes = 4096;
+
+inline size_t matrix_bytes(int M, int K) { return (size_t)M * (size_t)K * 5 / 8; }
+
+// ------------------------------------------------------------- device helpers --
+__device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// float32 -> bf16 bits, round to nearest even, every NaN -> 0x7FC0 (quant/q4nx.py:32-44).
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7FC0u;
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Round a float32 onto the bf16 grid (RNE), returned as float32.
+__device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte load of streamed (read-once) weight bytes: non-temporal hint.
+__device__ __forceinline__ uint4 load_stream16(const uint8_t* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// acc += a.lo*b.lo + a.hi*b.hi with bf16 pairs packed in dwords (v_dot2c_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), acc,
+                                         false);
+}
+
+// Codes of one dword -> four bf16 pairs with values 1 + n/16 (n in 0..15, exact).
+// Pair q covers nibbles q and q+4, i.e. columns (8d+2q, 8d+2q+1).
+__device__ __forceinline__ void unpack_codes(uint32_t v, uint32_t& p0, uint32_t& p1, uint32_t& p2, uint32_t& p3) {
+  const uint32_t mask = 0x00780078u, one = 0x3F803F80u;
+  p0 = ((v << 3) & mask) | one;
+  p1 = ((v >> 1) & mask) | one;
+  p2 = ((v >> 5) & mask) | one;
+  p3 = ((v >> 9) & mask) | one;
+}
+
+// Partial dot of one group: D' = sum_c (1 + n_c/16) * x_c over 32 columns, x as 16
+// bf16-pair dwords.  The group's contribution is then
+//   scale*D + min*S = 16*scale*D' + (min - 16*scale)*S,   S = sum_c x_c,
+// since D' = S + D/16.
+__device__ __forceinline__ float group_dot(const uint4 codes, const uint32_t* __restrict__ xw) {
+  float d = 0.f;
+  const uint32_t cw[4] = {codes.x, codes.y, codes.z, codes.w};
+#pragma unroll
+  for (int dd = 0; dd < 4; ++dd) {
+    uint32_t p0, p1, p2, p3;
+    unpack_codes(cw[dd], p0, p1, p2, p3);
+    const uint4 xv = *reinterpret_cast<const uint4*>(xw + 4 * dd);
+    d = dot2_bf16(p0, xv.x, d);
+    d = dot2_bf16(p1, xv.y, d);
+    d = dot2_bf16(p2, xv.z, d);
+    d = dot2_bf16(p3, xv.w, d);
+  }
+  return d;
+}
+
+// y += scale*D + min*S for one group given D' (see group_dot) and S.
+__device__ __forceinline__ float group_apply(uint32_t sm, float dprime, float s_sum, float y) {
+  const float scale = bf16_to_f32(sm & 0xffffu);
+  const float mn = bf16_to_f32(sm >> 16);
+  const float a = 16.f * scale;
+  const float b = mn - a;
+  return fmaf(a, dprime, fmaf(b, s_sum, y));
+}
+
+// Activations, in the operation order of the oracle (fp32).
+// SiTU-GLU (host/backend.py:47-62): gb*tanh(g/gb)*sigmoid(g) * vb*tanh(v/vb).
+__device__ __forceinline__ float act_situ(float g, float v, float gb, float vb) {
+  const float sig = 1.0f / (1.0f + expf(-g));
+  const float t1 = gb * tanhf(g / gb) * sig;
+  const float t2 = vb * tanhf(v / vb);
+  return t1 * t2;
+}
+// SiLU-GLU (kernels/moe/reference.py:160-171): g*sigmoid(g)*u, overflow-free sigmoid.
+__device__ __forceinline__ float act_swiglu(float g, float u) {
+  const float e = expf(-fabsf(g));
+  const float sig = g >= 0.f ? 1.0f / (1.0f + e) : e / (1.0f + e);
+  return (g * sig) * u;
+}
+__device__ __forceinline__ float act_apply(int act, float g, float u, float gb, float vb) {
+  return act == 1 ? act_swiglu(g, u) : act_situ(g, u, gb, vb);
+}
+
+// Wave-wide (64 lanes) sum.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+}  // namespace rmoe
+
+// ------------------------------------------------------------------- context --
+struct RmoeMatrix {
+  uint8_t* tiles = nullptr;  // device, tile layout
+  int M = 0, K = 0;
+};
+
+struct RmoeLayer {
+  int H = 0, I = 0, Ipad = 0, n_routed = 0, n_shared = 0, top_k = 0;
+  size_t gu_bytes = 0, dn_bytes = 0;  // per expert
+  uint8_t* gu = nullptr;              // (n_routed + n_shared) experts, tile layout
+  uint8_t* dn = nullptr;
+  uint16_t* router_w = nullptr;  // [n_routed, H] bf16
+  float* router_bias = nullptr;  // [n_routed] or null
+  bool has_router = false;
+  int score = 1, renorm = 1;
+  float scaling = 1.f;
+};
+
+// Device scratch of a context.  Sized by host entry points (which may allocate);
+// "_dev" entry points only check that it is large enough.
+struct RmoeScratch {
+  void* base = nullptr;
+  size_t bytes = 0;
+  // decode
+  float* part = nullptr;        // fp32 partial sums
+  size_t part_floats = 0;
+  unsigned* counters = nullptr;  // zero between launches
+  size_t n_counters = 0;
+  uint16_t* h = nullptr;         // activations [slots, Ipad] / [A, Ipad]
+  size_t h_elems = 0;
+  uint16_t* dout = nullptr;      // expert outputs [slots, H] / [A, H]
+  size_t dout_elems = 0;
+  int32_t* ids = nullptr;        // routing ids
+  float* wts = nullptr;          // routing weights
+  float* logits = nullptr;
+  size_t route_elems = 0;        // capacity of ids/wts (entries)
+  size_t logit_elems = 0;
+  int32_t* order = nullptr;      // dispatch
+  int32_t* inv = nullptr;
+  int32_t* offsets = nullptr;
+  int32_t* chunk_counts = nullptr;
+  size_t order_elems = 0, offset_elems = 0, chunk_elems = 0;
+  int* err = nullptr;            // device error flag
+  uint8_t* staging = nullptr;    // upload staging
+  size_t staging_bytes = 0;
+  int max_tokens = 0;
+};
+
+struct rmoe_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::map<int, RmoeMatrix> mats;
+  int next_handle = 1;
+  std::map<int, RmoeLayer> layers;
+  RmoeScratch s;
+};
+
+// ------------------------------------------------------- kernel launch wrappers --
+// Each returns hipSuccess or the launch error; shapes are validated by the caller.
+namespace rmoe {
+
+hipError_t launch_relayout_in(const uint8_t* packed, uint8_t* tiles, int M, int K, hipStream_t st);
+hipError_t launch_relayout_out(const uint8_t* tiles, uint8_t* packed, int M, int K, hipStream_t st);
+hipError_t launch_quantize(const float* w, int M, int K, int ld, int k_valid, uint8_t* tiles, int* err,
+                           hipStream_t st);
+
+hipError_t launch_linear(const uint8_t* tiles, int M, int K, const uint16_t* x, int T, uint16_t* y, RmoeScratch& s,
+                         hipStream_t st);
+
+hipError_t launch_route(const RmoeLayer& L, const uint16_t* x, int T, int32_t* ids, float* wts, float* logits,
+                        RmoeScratch& s, hipStream_t st);
+
+// Decode MoE: slots = k routed (+ shared); ids/wts on device ([k]); x [H].
+// out_routed (may be null) gets RTNE of the routed sum; out gets the full combine
+// (routed + shared, + x when residual).
+hipError_t launch_moe_decode(const RmoeLayer& L, const uint16_t* x, const int32_t* ids, const float* wts, int k,
+                             bool with_shared, int act, float gb, float vb, bool residual, uint16_t* out,
+                             uint16_t* out_routed, RmoeScratch& s, hipStream_t st);
+
+hipError_t launch_dispatch(const int32_t* ids, int T, int k, int n_experts, int32_t* order, int32_t* inv,
+                           int32_t* offsets, RmoeScratch& s, hipStream_t st);
+
+hipError_t launch_moe_grouped(const RmoeLayer& L, const uint16_t* x, int T, const int32_t* ids, const float* wts,
+                              const uint16_t* shared_gu, bool shared_from_x, int act, float gb, float vb,
+                              bool residual, uint16_t* routed, uint16_t* shared_down, uint16_t* out,
+                              RmoeScratch& s, hipStream_t st);
+
+// Scratch requirements (bytes) for the launch wrappers above.
+size_t decode_scratch_floats(const RmoeLayer& L);
+size_t decode_scratch_counters(const RmoeLayer& L);
+
+}  // namespace rmoe

@@ -1,0 +1,267 @@
+"""Thin object layer over the C ABI: a device context, q4nx matrices and MoE layers.
+
+Host-array methods take and return NumPy arrays (bf16 as uint16); ``*_dev`` methods
+take torch tensors that already live on the GPU and queue work on a stream without
+allocating (they are what the benchmark times and what a HIP graph captures).
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from ._lib import ACT_SITU, ACT_SWIGLU, SCORE_SIGMOID, SCORE_SOFTMAX, call, ptr
+from .geometry import MoeGeometry
+
+
+def act_code(gate_beta, value_beta) -> tuple[int, float, float]:
+    """SwiGLU when ``gate_beta is None`` (kernels/moe/reference.py:151-171 convention), else SiTU."""
+    if gate_beta is None or value_beta is None:
+        if (gate_beta is None) != (value_beta is None):
+            raise ValueError("gate_beta and value_beta must be provided together")
+        return ACT_SWIGLU, 0.0, 0.0
+    return ACT_SITU, float(gate_beta), float(value_beta)
+
+
+def _u16(a, name: str) -> np.ndarray:
+    arr = np.ascontiguousarray(a)
+    if arr.dtype != np.uint16:
+        raise ValueError(f"{name} must be uint16 (bf16 bits), got {arr.dtype}")
+    return arr
+
+
+def _check_dev(t, shape: tuple, dtype_name: str, name: str):
+    """A device tensor must have exactly the shape/dtype the kernel indexes (no OOB on the GPU)."""
+    if not hasattr(t, "data_ptr") or not getattr(t, "is_cuda", False):
+        raise ValueError(f"{name} must be a GPU tensor")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    if str(t.dtype).split(".")[-1] != dtype_name:
+        raise ValueError(f"{name} must be {dtype_name}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _stream_ptr(stream) -> int | None:
+    if stream is None:
+        return None
+    if hasattr(stream, "cuda_stream"):
+        return stream.cuda_stream
+    return int(stream)
+
+
+class Context:
+    """One device context (``rmoe_create``); owns weights and scratch on one GPU."""
+
+    def __init__(self, device: int = 0):
+        lib = _lib.load()
+        h = C.c_void_p()
+        _lib.check(lib.rmoe_create(int(device), C.byref(h)))
+        self._h = h
+        self.device = int(device)
+
+    @property
+    def handle(self):
+        return self._h
+
+    @property
+    def stream(self) -> int:
+        return _lib.load().rmoe_stream(self._h)
+
+    def close(self):
+        if self._h is not None and self._h.value:
+            _lib.load().rmoe_destroy(self._h)
+        self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def synchronize(self):
+        call("rmoe_synchronize", self._h)
+
+    # ------------------------------------------------------------ matrices --
+    def upload_matrix(self, packed: bytes | np.ndarray, M: int, K: int) -> "Matrix":
+        buf = np.frombuffer(packed, dtype=np.uint8) if isinstance(packed, (bytes, bytearray)) else np.ascontiguousarray(packed, dtype=np.uint8)
+        h = C.c_int()
+        call("rmoe_matrix_upload", self._h, ptr(buf), buf.size, int(M), int(K), C.byref(h))
+        return Matrix(self, h.value, M, K)
+
+    def quantize_matrix(self, w_dev, M: int, K: int, stream=None) -> "Matrix":
+        """Quantize an fp32 torch tensor [M, K] on the device (bit-exact quant/q4nx.py:127-200)."""
+        _check_dev(w_dev, (M, K), "float32", "w")
+        h = C.c_int()
+        call("rmoe_matrix_quantize_dev", self._h, ptr(w_dev), int(M), int(K), C.byref(h), _stream_ptr(stream))
+        return Matrix(self, h.value, M, K)
+
+    # ------------------------------------------------------------ layers --
+    def create_layer(self, layer: int, geom: MoeGeometry) -> "MoeLayer":
+        call("rmoe_layer_create", self._h, int(layer), geom.hidden, geom.inter, geom.n_routed, geom.n_shared, geom.top_k)
+        return MoeLayer(self, int(layer), geom)
+
+    def dispatch(self, top_ids, n_experts: int) -> tuple[np.ndarray, np.ndarray]:
+        ids = np.ascontiguousarray(top_ids, dtype=np.int32)
+        if ids.ndim != 2:
+            raise ValueError("top_ids must have shape [tokens, routes]")
+        order = np.empty(ids.size, dtype=np.int32)
+        offsets = np.empty(n_experts + 1, dtype=np.int32)
+        call("rmoe_dispatch", self._h, ptr(ids), ids.shape[0], ids.shape[1], int(n_experts), ptr(order), ptr(offsets))
+        return order, offsets
+
+
+class Matrix:
+    """A q4nx matrix resident on the device (tile layout)."""
+
+    def __init__(self, ctx: Context, handle: int, M: int, K: int):
+        self.ctx, self.handle, self.M, self.K = ctx, handle, int(M), int(K)
+
+    def download(self) -> bytes:
+        out = np.empty(self.M * self.K * 5 // 8, dtype=np.uint8)
+        call("rmoe_matrix_download", self.ctx.handle, self.handle, ptr(out), out.size)
+        return out.tobytes()
+
+    def linear(self, x: np.ndarray) -> np.ndarray:
+        """bf16 ``x[..., K_in]`` (K_in <= K, zero padded) -> bf16 ``[..., M]``."""
+        xa = _u16(x, "x")
+        lead = xa.shape[:-1]
+        rows = xa.reshape(-1, xa.shape[-1])
+        y = np.empty((rows.shape[0], self.M), dtype=np.uint16)
+        if rows.shape[0]:
+            call("rmoe_linear", self.ctx.handle, self.handle, ptr(rows), rows.shape[0], rows.shape[1], ptr(y))
+        return y.reshape(*lead, self.M)
+
+    def reserve(self, T: int):
+        call("rmoe_reserve_linear", self.ctx.handle, self.handle, int(T))
+
+    def linear_dev(self, x_dev, T: int, y_dev, stream=None):
+        _check_dev(x_dev, (T, self.K), "int16", "x")
+        _check_dev(y_dev, (T, self.M), "int16", "y")
+        call("rmoe_linear_dev", self.ctx.handle, self.handle, ptr(x_dev), int(T), ptr(y_dev), _stream_ptr(stream))
+
+    def free(self):
+        call("rmoe_matrix_free", self.ctx.handle, self.handle)
+
+
+class MoeLayer:
+    """One MoE layer (experts + router) resident on the device."""
+
+    def __init__(self, ctx: Context, layer: int, geom: MoeGeometry):
+        self.ctx, self.layer, self.geom = ctx, layer, geom
+        self.has_router = False
+
+    def upload_experts(self, gate_up: bytes | np.ndarray, down: bytes | np.ndarray):
+        gu = np.frombuffer(gate_up, np.uint8) if isinstance(gate_up, (bytes, bytearray)) else np.ascontiguousarray(gate_up, np.uint8)
+        dn = np.frombuffer(down, np.uint8) if isinstance(down, (bytes, bytearray)) else np.ascontiguousarray(down, np.uint8)
+        call("rmoe_layer_upload_experts", self.ctx.handle, self.layer, ptr(gu), gu.size, ptr(dn), dn.size)
+
+    def quantize_expert(self, expert: int, gate_up_dev, down_dev, stream=None):
+        g = self.geom
+        _check_dev(gate_up_dev, (2 * g.inter, g.hidden), "float32", "gate_up")
+        _check_dev(down_dev, (g.hidden, g.inter), "float32", "down")
+        call("rmoe_layer_quantize_expert_dev", self.ctx.handle, self.layer, int(expert), ptr(gate_up_dev),
+             ptr(down_dev), _stream_ptr(stream))
+
+    def download_expert(self, expert: int) -> tuple[bytes, bytes]:
+        gu = np.empty(self.geom.gu_bytes, np.uint8)
+        dn = np.empty(self.geom.dn_bytes, np.uint8)
+        call("rmoe_layer_download_expert", self.ctx.handle, self.layer, int(expert), ptr(gu), gu.size, ptr(dn), dn.size)
+        return gu.tobytes(), dn.tobytes()
+
+    def set_router(self, weight_bf16, bias=None, score: str = "softmax", renormalize: bool = True, scaling: float = 1.0):
+        code = {"sigmoid": SCORE_SIGMOID, "softmax": SCORE_SOFTMAX}[score]
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        if b is not None and b.shape != (self.geom.n_routed,):
+            raise ValueError(f"router bias must be [{self.geom.n_routed}]")
+        if hasattr(weight_bf16, "data_ptr"):
+            dt = str(weight_bf16.dtype).split(".")[-1]
+            _check_dev(weight_bf16, (self.geom.n_routed, self.geom.hidden), dt if dt in ("bfloat16", "int16") else "bfloat16",
+                       "router weight")
+            call("rmoe_layer_set_router_dev", self.ctx.handle, self.layer, ptr(weight_bf16), ptr(b), code,
+                 int(bool(renormalize)), float(scaling))
+        else:
+            w = _u16(weight_bf16, "router weight")
+            if w.shape != (self.geom.n_routed, self.geom.hidden):
+                raise ValueError(f"router weight must be [{self.geom.n_routed}, {self.geom.hidden}]")
+            call("rmoe_layer_set_router", self.ctx.handle, self.layer, ptr(w), ptr(b), code, int(bool(renormalize)),
+                 float(scaling))
+        self.has_router = True
+
+    def reserve(self, max_tokens: int):
+        call("rmoe_reserve", self.ctx.handle, self.layer, int(max_tokens))
+
+    def route(self, x: np.ndarray):
+        xa = _u16(x, "x").reshape(-1, self.geom.hidden)
+        T, k, E = xa.shape[0], self.geom.top_k, self.geom.n_routed
+        ids = np.empty((T, k), np.int32)
+        wts = np.empty((T, k), np.float32)
+        logits = np.empty((T, E), np.float32)
+        call("rmoe_route", self.ctx.handle, self.layer, ptr(xa), T, ptr(ids), ptr(wts), ptr(logits))
+        return ids, wts, logits
+
+    def moe_experts(self, x, top_ids, top_weights, gate_beta=4.0, value_beta=25.0) -> np.ndarray:
+        xa = _u16(x, "x").reshape(-1)
+        ids = np.ascontiguousarray(top_ids, dtype=np.int32).reshape(-1)
+        w = np.ascontiguousarray(top_weights, dtype=np.float32).reshape(-1)
+        if ids.size != w.size:
+            raise ValueError("top_ids and top_weights must have the same length")
+        act, gb, vb = act_code(gate_beta, value_beta)
+        out = np.empty(self.geom.hidden, np.uint16)
+        call("rmoe_moe_experts", self.ctx.handle, self.layer, ptr(xa), ptr(ids), ptr(w), ids.size, act, gb, vb, ptr(out))
+        return out
+
+    def moe_decode(self, x, residual: bool = False, gate_beta=None, value_beta=None):
+        """Router + routed + shared + combine for one token; returns (out, top_ids, weights)."""
+        xa = _u16(x, "x").reshape(-1)
+        act, gb, vb = act_code(gate_beta, value_beta)
+        out = np.empty(self.geom.hidden, np.uint16)
+        ids = np.empty(self.geom.top_k, np.int32)
+        w = np.empty(self.geom.top_k, np.float32)
+        call("rmoe_moe_decode", self.ctx.handle, self.layer, ptr(xa), ptr(out), int(bool(residual)), act, gb, vb,
+             ptr(ids), ptr(w))
+        return out, ids, w
+
+    def moe_decode_dev(self, x_dev, out_dev, residual: bool = False, gate_beta=None, value_beta=None,
+                       ids_dev=None, wts_dev=None, stream=None):
+        act, gb, vb = act_code(gate_beta, value_beta)
+        g = self.geom
+        _check_dev(x_dev, (g.hidden,), "int16", "x")
+        _check_dev(out_dev, (g.hidden,), "int16", "out")
+        if ids_dev is not None:
+            _check_dev(ids_dev, (g.top_k,), "int32", "ids")
+        if wts_dev is not None:
+            _check_dev(wts_dev, (g.top_k,), "float32", "wts")
+        call("rmoe_moe_decode_dev", self.ctx.handle, self.layer, ptr(x_dev), ptr(out_dev), int(bool(residual)), act,
+             gb, vb, ptr(ids_dev), ptr(wts_dev), _stream_ptr(stream))
+
+    def moe_experts_grouped(self, x, top_ids, top_weights, shared_gu, gate_beta=4.0, value_beta=25.0):
+        xa = _u16(x, "x")
+        T = xa.shape[0]
+        ids = np.ascontiguousarray(top_ids, dtype=np.int32)
+        w = np.ascontiguousarray(top_weights, dtype=np.float32)
+        sgu = _u16(shared_gu, "shared_gu")
+        act, gb, vb = act_code(gate_beta, value_beta)
+        routed = np.empty((T, self.geom.hidden), np.uint16)
+        sdown = np.empty((T, self.geom.hidden), np.uint16)
+        call("rmoe_moe_experts_grouped", self.ctx.handle, self.layer, ptr(xa), T, ptr(ids), ptr(w), ptr(sgu), act, gb,
+             vb, ptr(routed), ptr(sdown))
+        return routed, sdown
+
+    def moe_prefill_dev(self, x_dev, T: int, out_dev, residual: bool = False, gate_beta=None, value_beta=None,
+                        ids_dev=None, wts_dev=None, stream=None):
+        act, gb, vb = act_code(gate_beta, value_beta)
+        g = self.geom
+        _check_dev(x_dev, (T, g.hidden), "int16", "x")
+        _check_dev(out_dev, (T, g.hidden), "int16", "out")
+        if ids_dev is not None:
+            _check_dev(ids_dev, (T, g.top_k), "int32", "ids")
+        if wts_dev is not None:
+            _check_dev(wts_dev, (T, g.top_k), "float32", "wts")
+        call("rmoe_moe_prefill_dev", self.ctx.handle, self.layer, ptr(x_dev), int(T), ptr(out_dev), int(bool(residual)),
+             act, gb, vb, ptr(ids_dev), ptr(wts_dev), _stream_ptr(stream))
+
+    def free(self):
+        call("rmoe_layer_free", self.ctx.handle, self.layer)

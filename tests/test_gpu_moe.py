@@ -1,0 +1,226 @@
+"""GPU: router, dispatch, decode MoE, grouped prefill and the residual stack vs the oracle.
+
+Bars: routing indices and dispatch permutations bit-exact; outputs
+within max-abs 1e-2 and rel-L2 1e-3 of the fp32 oracle.  Routing exactness is
+asserted for every token whose k/k+1 selection-score gap exceeds 1e-6 (tokens
+closer than that are reported; fp32 summation order can legitimately reorder a
+near-tie).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import raon_npu_amd.geometry as G
+from oracle import moe as om
+from oracle import planner as op
+from oracle.bf16 import bf16_to_f32, f32_to_bf16
+
+from moe_fixtures import compare_bf16, make_layer, random_tokens, routing_margin
+
+pytestmark = pytest.mark.gpu
+
+TOL_ABS, TOL_REL = 1e-2, 1e-3
+MARGIN = 1e-6
+
+
+def _check(out, ref, label, same_min=0.98):
+    err, rel, same = compare_bf16(out, ref)
+    print(f"{label}: max-abs {err:.3e} rel-L2 {rel:.3e} bit-identical {same:.4f}")
+    assert err <= TOL_ABS and rel <= TOL_REL and same >= same_min, (label, err, rel, same)
+
+
+@pytest.fixture(scope="module")
+def baseline(gpu_ctx):
+    """BASELINE geometry (H=2048, I=768, 128 routed + 1 shared, top-8), weights N(0, 0.02)
+    generated and quantized on the GPU, then read back as pack_gemv bytes for the oracle."""
+    import torch
+
+    geom = G.BASELINE
+    lyr = gpu_ctx.create_layer(0, geom)
+    gen = torch.Generator(device="cuda").manual_seed(1234)
+    for e in range(geom.n_experts):
+        gu = torch.randn(2 * geom.inter, geom.hidden, device="cuda", generator=gen) * 0.02
+        dn = torch.randn(geom.hidden, geom.inter, device="cuda", generator=gen) * 0.02
+        lyr.quantize_expert(e, gu, dn)
+    rw = (torch.randn(geom.n_routed, geom.hidden, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+    router = rw.view(torch.int16).cpu().numpy().view(np.uint16)
+    lyr.set_router(router, score="softmax")
+    parts = [lyr.download_expert(e) for e in range(geom.n_experts)]
+    bank = om.ExpertBank(b"".join(p[0] for p in parts), b"".join(p[1] for p in parts), geom.n_experts,
+                         geom.hidden, geom.inter, cache=geom.n_experts)
+    spec = om.RouterSpec(router, geom.top_k, score="softmax")
+    lyr.reserve(512)
+    yield geom, lyr, bank, spec
+    lyr.free()
+
+
+def test_router_matches_oracle(baseline):
+    geom, lyr, _, spec = baseline
+    xs = random_tokens(64, geom.hidden, 100)
+    ids, wts, logits = lyr.route(xs)
+    close = 0
+    for t in range(xs.shape[0]):
+        top, w, lg = om.route_token(xs[t], spec)
+        np.testing.assert_allclose(logits[t], lg, rtol=1e-4, atol=1e-5)
+        if routing_margin(xs[t], spec) <= MARGIN:
+            close += 1
+            continue
+        assert ids[t].tolist() == top.tolist(), t
+        np.testing.assert_allclose(wts[t], w, rtol=1e-5, atol=1e-7)
+    assert close <= 2
+
+
+@pytest.mark.parametrize("score,use_bias", [("sigmoid", True), ("softmax", True)])
+def test_router_variants(gpu_ctx, score, use_bias):
+    geom = G.MoeGeometry(hidden=2048, inter=128, n_routed=128, n_shared=0, top_k=6)
+    rng = np.random.default_rng(55)
+    router = f32_to_bf16(rng.normal(0, 0.02, (geom.n_routed, geom.hidden)).astype(np.float32))
+    bias = (rng.standard_normal(geom.n_routed) * 0.01).astype(np.float32) if use_bias else None
+    lyr = gpu_ctx.create_layer(901, geom)
+    lyr.set_router(router, bias=bias, score=score, scaling=2.5)
+    spec = om.RouterSpec(router, geom.top_k, score=score, bias=bias, scaling=2.5)
+    xs = random_tokens(48, geom.hidden, 56)
+    ids, wts, _ = lyr.route(xs)
+    for t in range(xs.shape[0]):
+        if routing_margin(xs[t], spec) <= MARGIN:
+            continue
+        top, w, _ = om.route_token(xs[t], spec)
+        assert ids[t].tolist() == top.tolist()
+        np.testing.assert_allclose(wts[t], w, rtol=1e-5, atol=1e-7)
+    lyr.free()
+
+
+@pytest.mark.parametrize("betas", [(None, None), (4.0, 25.0)], ids=["swiglu", "situ"])
+def test_moe_experts_matches_oracle(baseline, betas):
+    geom, lyr, bank, _ = baseline
+    xs = random_tokens(6, geom.hidden, 200)
+    rng = np.random.default_rng(201)
+    for t, x in enumerate(xs):
+        ids = rng.choice(geom.n_routed, geom.top_k, replace=False).astype(np.int32)
+        w = rng.random(geom.top_k, dtype=np.float32)
+        out = lyr.moe_experts(x, ids, w, *betas)
+        ref = om.moe_experts(bank, x, ids, w, *betas)
+        _check(out, ref, f"moe_experts[{t}]")
+
+
+def test_decode_layer_matches_oracle(baseline):
+    """router on the device + 8 routed + shared expert + fp32 combine."""
+    geom, lyr, bank, spec = baseline
+    xs = random_tokens(8, geom.hidden, 300)
+    for t, x in enumerate(xs):
+        out, ids, w = lyr.moe_decode(x, residual=False)
+        ref, top, rw, _ = om.moe_token(bank, spec, x, None, None, shared_id=geom.shared_id)
+        if routing_margin(x, spec) > MARGIN:
+            assert ids.tolist() == top.tolist()
+        _check(out, ref, f"decode[{t}]")
+        out_r, _, _ = lyr.moe_decode(x, residual=True)
+        ref_r = f32_to_bf16(bf16_to_f32(x) + bf16_to_f32(ref))
+        _check(out_r, ref_r, f"decode+residual[{t}]", same_min=0.97)
+
+
+def test_dispatch_matches_planner(gpu_ctx):
+    rng = np.random.default_rng(400)
+    for T, k, E in [(1, 8, 128), (445, 8, 128), (6700, 8, 128), (33, 6, 128), (5, 3, 7)]:
+        ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+        order, offsets = gpu_ctx.dispatch(ids, E)
+        ref_o, ref_off = op.dispatch_order(ids, n_routed=E)
+        np.testing.assert_array_equal(order, ref_o)
+        np.testing.assert_array_equal(offsets, ref_off)
+    # skewed routing: a hot expert with most tokens
+    ids = np.stack([np.concatenate([[0], rng.choice(np.arange(1, 128), 7, replace=False)]) for _ in range(3000)])
+    order, offsets = gpu_ctx.dispatch(ids.astype(np.int32), 128)
+    ref_o, ref_off = op.dispatch_order(ids, n_routed=128)
+    np.testing.assert_array_equal(order, ref_o)
+    np.testing.assert_array_equal(offsets, ref_off)
+    with pytest.raises(ValueError):
+        gpu_ctx.dispatch(np.array([[1, 1]], np.int32), 128)
+
+
+def test_grouped_matches_oracle(baseline):
+    geom, lyr, bank, _ = baseline
+    T = 24
+    xs = random_tokens(T, geom.hidden, 500)
+    rng = np.random.default_rng(501)
+    ids = np.stack([rng.choice(geom.n_routed, geom.top_k, replace=False) for _ in range(T)]).astype(np.int64)
+    w = rng.random((T, geom.top_k), dtype=np.float32)
+    sgu = np.stack([om.shared_gate_up(bank, geom.shared_id, x) for x in xs])
+    routed, sdown = lyr.moe_experts_grouped(xs, ids, w, sgu, None, None)
+    r_ref, s_ref = om.moe_experts_grouped(bank, xs, ids, w, sgu, geom.shared_id, None, None)
+    _check(routed, r_ref, "grouped routed")
+    _check(sdown, s_ref, "grouped shared_down")
+
+
+def test_prefill_layer_matches_oracle(baseline):
+    """BASELINE config 3 shape at T=96: router, dispatch, grouped experts, shared, combine."""
+    import torch
+
+    geom, lyr, bank, spec = baseline
+    T = 96
+    xs = random_tokens(T, geom.hidden, 600)
+    xd = torch.from_numpy(xs.view(np.int16)).cuda()
+    out = torch.empty_like(xd)
+    ids = torch.empty((T, geom.top_k), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, geom.top_k), dtype=torch.float32, device="cuda")
+    lyr.moe_prefill_dev(xd, T, out, ids_dev=ids, wts_dev=wts, stream=torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    ref, top, rw = om.prefill_layer(bank, spec, xs, geom.shared_id, None, None, batched=True)
+    got_ids = ids.cpu().numpy()
+    for t in range(T):
+        if routing_margin(xs[t], spec) > MARGIN:
+            assert got_ids[t].tolist() == top[t].tolist(), t
+    _check(out.cpu().numpy().view(np.uint16), ref, "prefill layer")
+
+
+def test_decode_graph_replays_match_eager(baseline):
+    import torch
+
+    geom, lyr, _, _ = baseline
+    x = torch.from_numpy(random_tokens(1, geom.hidden, 700)[0].view(np.int16)).cuda()
+    eager = torch.empty_like(x)
+    lyr.moe_decode_dev(x, eager, residual=True, stream=torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    out = torch.empty_like(x)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            lyr.moe_decode_dev(x, out, residual=True, stream=s)
+    torch.cuda.current_stream().wait_stream(s)
+    for _ in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        # eager work between replays
+        lyr.moe_decode_dev(x, eager, residual=True, stream=torch.cuda.current_stream())
+        torch.cuda.synchronize()
+
+
+def test_residual_stack_matches_oracle(gpu_ctx):
+    """BASELINE config 4 structure on a small geometry: 4 stacked layers with residual adds."""
+    import torch
+
+    geom = G.MoeGeometry(hidden=512, inter=256, n_routed=16, n_shared=1, top_k=4)
+    layers, oracle_layers = [], []
+    for li in range(4):
+        syn = make_layer(geom, seed=800 + li)
+        lyr = gpu_ctx.create_layer(910 + li, geom)
+        lyr.upload_experts(syn.gate_up, syn.down)
+        lyr.set_router(syn.router, score="softmax")
+        layers.append(lyr)
+        oracle_layers.append(syn.oracle_layer())
+    xs = random_tokens(6, geom.hidden, 810)
+    for x in xs:
+        h = torch.from_numpy(x.view(np.int16)).cuda()
+        for lyr in layers:
+            nxt = torch.empty_like(h)
+            lyr.moe_decode_dev(h, nxt, residual=True, stream=torch.cuda.current_stream())
+            h = nxt
+        torch.cuda.synchronize()
+        ref = om.residual_stack(oracle_layers, x)
+        _check(h.cpu().numpy().view(np.uint16), ref, "stack", same_min=0.9)
+    for lyr in layers:
+        lyr.free()
