@@ -25,7 +25,7 @@ TOL_ABS, TOL_REL = 1e-2, 1e-3
 MARGIN = 1e-6
 
 
-def _check(out, ref, label, same_min=0.98):
+def _check(out, ref, label, same_min=0.95):
     err, rel, same = compare_bf16(out, ref)
     print(f"{label}: max-abs {err:.3e} rel-L2 {rel:.3e} bit-identical {same:.4f}")
     assert err <= TOL_ABS and rel <= TOL_REL and same >= same_min, (label, err, rel, same)
