@@ -107,6 +107,11 @@ int rmoe_layer_upload_experts(rmoe_ctx* ctx, int layer, const void* gate_up, siz
  * the down input columns past I are zero-padded to Ipad).  Bit-exact quant/q4nx.py:127-200. */
 int rmoe_layer_quantize_expert_dev(rmoe_ctx* ctx, int layer, int expert, const float* gate_up_dev,
                                    const float* down_dev, void* stream);
+/* Fill every expert of the layer with seeded synthetic weights N(0, std) generated on
+ * the device (counter-based RNG, one stream per expert matrix) and quantized with the
+ * same bit-exact q4nx quantizer.  For benchmarks at full depth; synchronous.  No
+ * reference counterpart (the reference quantizes host arrays, quant/q4nx.py:127-200). */
+int rmoe_layer_synthesize_dev(rmoe_ctx* ctx, int layer, uint64_t seed, float std, void* stream);
 /* Read one expert back as pack_gemv bytes (round trips, oracle cross-checks). */
 int rmoe_layer_download_expert(rmoe_ctx* ctx, int layer, int expert, void* gate_up, size_t gu_nbytes,
                                void* down, size_t dn_nbytes);
@@ -139,6 +144,12 @@ int rmoe_moe_experts(rmoe_ctx* ctx, int layer, const uint16_t* x, const int32_t*
 int rmoe_moe_decode_dev(rmoe_ctx* ctx, int layer, const void* x_dev, void* out_dev, int residual,
                         int act, float gate_beta, float value_beta, void* top_ids_dev,
                         void* top_weights_dev, void* stream);
+/* One stage of rmoe_moe_decode_dev: 0 = router (ids/weights into context scratch),
+ * 1 = gate/up of all slots + activation, 2 = down of all slots + ordered combine into
+ * out_dev.  Stages read the previous stage's context scratch; the split mirrors the
+ * reference's moe_start("b1") / moe_start("b2") phases (npu/backend.py:5167-5284). */
+int rmoe_moe_decode_stage_dev(rmoe_ctx* ctx, int layer, int stage, const void* x_dev, void* out_dev, int residual,
+                              int act, float gate_beta, float value_beta, void* stream);
 int rmoe_moe_decode(rmoe_ctx* ctx, int layer, const uint16_t* x, uint16_t* out, int residual,
                     int act, float gate_beta, float value_beta, int32_t* top_ids, float* top_weights);
 

@@ -49,6 +49,7 @@ SIGNATURES: dict[str, list] = {
     "rmoe_reserve": [_p, _i, _i],
     "rmoe_layer_upload_experts": [_p, _i, _p, _sz, _p, _sz],
     "rmoe_layer_quantize_expert_dev": [_p, _i, _i, _p, _p, _p],
+    "rmoe_layer_synthesize_dev": [_p, _i, C.c_uint64, _f, _p],
     "rmoe_layer_download_expert": [_p, _i, _i, _p, _sz, _p, _sz],
     "rmoe_layer_set_router": [_p, _i, _p, _p, _i, _i, _f],
     "rmoe_layer_set_router_dev": [_p, _i, _p, _p, _i, _i, _f],
@@ -56,6 +57,7 @@ SIGNATURES: dict[str, list] = {
     "rmoe_route": [_p, _i, _p, _i, _p, _p, _p],
     "rmoe_moe_experts": [_p, _i, _p, _p, _p, _i, _i, _f, _f, _p],
     "rmoe_moe_decode_dev": [_p, _i, _p, _p, _i, _i, _f, _f, _p, _p, _p],
+    "rmoe_moe_decode_stage_dev": [_p, _i, _i, _p, _p, _i, _i, _f, _f, _p],
     "rmoe_moe_decode": [_p, _i, _p, _p, _i, _i, _f, _f, _p, _p],
     "rmoe_dispatch": [_p, _p, _i, _i, _i, _p, _p],
     "rmoe_moe_experts_grouped": [_p, _i, _p, _i, _p, _p, _p, _i, _f, _f, _p, _p],

@@ -67,13 +67,13 @@ __device__ void route_select(const RouteArgs& a, int t) {
   const float* lg = a.logits + (size_t)t * a.E;
   if (w0) {
     if (a.score == 0) {
-      for (int e = lane; e < a.E; e += 64) sc[e] = 1.0f / (1.0f + expf(-lg[e]));
+      for (int e = lane; e < a.E; e += 64) sc[e] = 1.0f / (1.0f + expf(-ld_dev(&lg[e])));
     } else {
       float m = -__builtin_inff();
-      for (int e = lane; e < a.E; e += 64) m = fmaxf(m, lg[e]);
+      for (int e = lane; e < a.E; e += 64) m = fmaxf(m, ld_dev(&lg[e]));
 #pragma unroll
       for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-      for (int e = lane; e < a.E; e += 64) zz[e] = expf(lg[e] - m);
+      for (int e = lane; e < a.E; e += 64) zz[e] = expf(ld_dev(&lg[e]) - m);
     }
   }
   __syncthreads();
@@ -138,16 +138,10 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
     float acc = 0.f;
     for (int c = lane; c < a.H / 2; c += 64) acc = dot2_bf16(wr[c], xr[c], acc);
     acc = wave_sum(acc);
-    if (lane == 0) a.logits[(size_t)t * a.E + e] = acc;
+    if (lane == 0) st_dev(&a.logits[(size_t)t * a.E + e], acc);
   }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) last_flag = (atomicAdd(&a.counters[t], 1u) == gridDim.x - 1) ? 1u : 0u;
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
+  if (!arrive_last(&a.counters[t], gridDim.x, &last_flag)) return;
   route_select(a, t);
-  if (threadIdx.x == 0) a.counters[t] = 0u;
 }
 
 // ------------------------------------------------------------- decode MoE --
@@ -163,7 +157,7 @@ struct DecodeArgs {
   float gb, vb;
   int residual;
   uint16_t* h;          // [slots, Ipad]
-  uint16_t* dout;       // [slots, H]
+  float* dout;          // [slots, H] fp32 values of the bf16-rounded expert outputs
   uint16_t* out;        // [H]
   uint16_t* out_routed; // [H] or null
   float* part_gu;       // [slots, I/64, ks1, 2, 64]
@@ -254,25 +248,19 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeArgs a) {
   if (a.ks1 > 1) {
     float* part = a.part_gu + (band * a.ks1 + ks) * 128;
     if (wave == 0) {
-      part[lane] = g;
-      part[64 + lane] = u;
+      st_dev(&part[lane], g);
+      st_dev(&part[64 + lane], u);
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) last_flag = (atomicAdd(&a.cnt_gu[band], 1u) == (unsigned)(a.ks1 - 1)) ? 1u : 0u;
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
+    if (!arrive_last(&a.cnt_gu[band], (unsigned)a.ks1, &last_flag)) return;
     if (wave == 0) {
       const float* pb = a.part_gu + band * a.ks1 * 128;
       g = 0.f;
       u = 0.f;
       for (int q = 0; q < a.ks1; ++q) {
-        g += pb[q * 128 + lane];
-        u += pb[q * 128 + 64 + lane];
+        g += ld_dev(&pb[q * 128 + lane]);
+        u += ld_dev(&pb[q * 128 + 64 + lane]);
       }
     }
-    if (tid == 0) a.cnt_gu[band] = 0u;
   }
   if (wave == 0) {
     const float gb = bf16_round(g), ub = bf16_round(u);
@@ -313,29 +301,20 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
   const size_t band = (size_t)s * nrt + rt;
   if (a.ks2 > 1) {
     float* part = a.part_dn + (band * a.ks2 + ks) * 64;
-    if (wave == 0) part[lane] = d;
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) last_flag = (atomicAdd(&a.cnt_dn[band], 1u) == (unsigned)(a.ks2 - 1)) ? 1u : 0u;
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
+    if (wave == 0) st_dev(&part[lane], d);
+    if (!arrive_last(&a.cnt_dn[band], (unsigned)a.ks2, &last_flag)) return;
     if (wave == 0) {
       const float* pb = a.part_dn + band * a.ks2 * 64;
       d = 0.f;
-      for (int q = 0; q < a.ks2; ++q) d += pb[q * 64 + lane];
+      for (int q = 0; q < a.ks2; ++q) d += ld_dev(&pb[q * 64 + lane]);
     }
-    if (tid == 0) a.cnt_dn[band] = 0u;
   }
   const int row = rt * 64 + lane;
-  if (wave == 0) a.dout[(size_t)s * a.H + row] = (uint16_t)f32_to_bf16(d);
+  // Expert outputs are handed to the combining workgroup as the fp32 value of the
+  // bf16-rounded result.
+  if (wave == 0) st_dev(&a.dout[(size_t)s * a.H + row], bf16_round(d));
   // Second level: the last slot to finish this 64-row band combines all slots.
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) last_flag = (atomicAdd(&a.cnt_rt[rt], 1u) == (unsigned)(a.slots - 1)) ? 1u : 0u;
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
+  if (!arrive_last(&a.cnt_rt[rt], (unsigned)a.slots, &last_flag)) return;
   if (wave == 0) {
     // Ascending expert id over the routed slots (ids are distinct per token).
     float acc2 = 0.f;
@@ -351,16 +330,15 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
       }
       if (bs < 0) break;
       prev = best;
-      const float dv = bf16_to_f32(a.dout[(size_t)bs * a.H + row]);
+      const float dv = ld_dev(&a.dout[(size_t)bs * a.H + row]);
       acc2 = __fadd_rn(acc2, __fmul_rn(dv, a.wts[bs]));
     }
     uint32_t o = f32_to_bf16(acc2);
     if (a.out_routed) a.out_routed[row] = (uint16_t)o;
-    if (a.slots > a.k) o = f32_to_bf16(__fadd_rn(bf16_to_f32(o), bf16_to_f32(a.dout[(size_t)a.k * a.H + row])));
+    if (a.slots > a.k) o = f32_to_bf16(__fadd_rn(bf16_to_f32(o), ld_dev(&a.dout[(size_t)a.k * a.H + row])));
     if (a.residual) o = f32_to_bf16(__fadd_rn(bf16_to_f32(a.x[row]), bf16_to_f32(o)));
     if (a.out) a.out[row] = (uint16_t)o;
   }
-  if (tid == 0) a.cnt_rt[rt] = 0u;
 }
 
 }  // namespace
@@ -400,7 +378,7 @@ size_t decode_scratch_counters(const RmoeLayer& L) {
 
 hipError_t launch_moe_decode(const RmoeLayer& L, const uint16_t* x, const int32_t* ids, const float* wts, int k,
                              bool with_shared, int act, float gb, float vb, bool residual, uint16_t* out,
-                             uint16_t* out_routed, RmoeScratch& s, hipStream_t st) {
+                             uint16_t* out_routed, RmoeScratch& s, hipStream_t st, int stages) {
   int ks1, ks2;
   decode_splits(L, ks1, ks2);
   const int slots = k + (with_shared ? 1 : 0);
@@ -442,11 +420,16 @@ hipError_t launch_moe_decode(const RmoeLayer& L, const uint16_t* x, const int32_
   const int nkt1 = L.H / kTileCols, nkt2 = L.Ipad / kTileCols;
   const int per1 = (nkt1 + ks1 - 1) / ks1, per2 = (nkt2 + ks2 - 1) / ks2;
   const int w1 = min(4, 2 * per1), w2 = min(4, per2);
-  hipLaunchKernelGGL(decode_gate_up_kernel, dim3(slots * (L.I / 64) * ks1), dim3(64 * w1), 0, st, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(decode_down_kernel, dim3(slots * (L.H / 64) * ks2), dim3(64 * w2), 0, st, a);
-  return hipGetLastError();
+  if (stages & 1) {
+    hipLaunchKernelGGL(decode_gate_up_kernel, dim3(slots * (L.I / 64) * ks1), dim3(64 * w1), 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (stages & 2) {
+    hipLaunchKernelGGL(decode_down_kernel, dim3(slots * (L.H / 64) * ks2), dim3(64 * w2), 0, st, a);
+    return hipGetLastError();
+  }
+  return hipSuccess;
 }
 
 }  // namespace rmoe

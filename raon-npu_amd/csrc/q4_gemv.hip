@@ -98,22 +98,16 @@ __global__ __launch_bounds__(256) void linear_kernel(LinearArgs a) {
     float v = 0.f;
     for (int w = 0; w < nwaves; ++w) v += red[w][t][lane];
     if (a.ksplit == 1) a.y[(size_t)(tok0 + t) * a.M + row] = (uint16_t)f32_to_bf16(v);
-    else part[t * 64 + lane] = v;
+    else st_dev(&part[t * 64 + lane], v);
   }
   if (a.ksplit == 1) return;
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) last_flag = (atomicAdd(&a.counters[band], 1u) == (unsigned)(a.ksplit - 1)) ? 1u : 0u;
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
+  if (!arrive_last(&a.counters[band], (unsigned)a.ksplit, &last_flag)) return;
   const float* pb = a.part + band * a.ksplit * (kNT * 64);
   for (int t = wave; t < nt; t += nwaves) {
     float s = 0.f;
-    for (int k2 = 0; k2 < a.ksplit; ++k2) s += pb[k2 * (kNT * 64) + t * 64 + lane];
+    for (int k2 = 0; k2 < a.ksplit; ++k2) s += ld_dev(&pb[k2 * (kNT * 64) + t * 64 + lane]);
     a.y[(size_t)(tok0 + t) * a.M + row] = (uint16_t)f32_to_bf16(s);
   }
-  if (tid == 0) a.counters[band] = 0u;
 }
 
 }  // namespace

@@ -129,27 +129,11 @@ __device__ __forceinline__ float bf16_next_up(float x) {
   return bits_f(nx << 16);
 }
 
-__global__ void quantize_kernel(const float* __restrict__ w, int M, int K, int ld, int k_valid,
-                                uint8_t* __restrict__ tiles, int* __restrict__ err) {
-  const int G = K / 32, nkt = K / 128;
-  const size_t n = (size_t)M * G;
-  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= n) return;
-  const int lane = idx & 63;
-  const size_t rest = idx >> 6;
-  const int j = rest & 3;
-  const size_t tile = rest >> 2;
-  const int rt = (int)(tile / nkt), kt = (int)(tile % nkt);
-  const int r = rt * 64 + lane, g = kt * 4 + j;
-  const float* row = w + (size_t)r * ld;
-  float v[32];
+// Quantize one (row, group) of 32 fp32 values and store it at (tile, j, lane).
+__device__ void quantize_group(const float (&v)[32], uint8_t* tile, int j, int lane, int* err) {
   bool finite = true;
 #pragma unroll
-  for (int c = 0; c < 32; ++c) {
-    const int col = g * 32 + c;
-    v[c] = col < k_valid ? row[col] : 0.f;
-    finite = finite && isfinite(v[c]);
-  }
+  for (int c = 0; c < 32; ++c) finite = finite && isfinite(v[c]);
   if (!finite) atomicOr(err, 1);
   float lo = v[0], hi = v[0];
 #pragma unroll
@@ -179,10 +163,70 @@ __global__ void quantize_kernel(const float* __restrict__ w, int M, int K, int l
     const int ni = tile_nibble_index(c);
     words[ni >> 3] |= code << (4 * (ni & 7));
   }
-  uint8_t* t = tiles + tile * kTileBytes;
-  *reinterpret_cast<uint4*>(t + j * 1024 + lane * 16) = make_uint4(words[0], words[1], words[2], words[3]);
+  *reinterpret_cast<uint4*>(tile + j * 1024 + lane * 16) = make_uint4(words[0], words[1], words[2], words[3]);
   const uint32_t sb = __float_as_uint(sc) >> 16, mb = __float_as_uint(minq) >> 16;
-  *reinterpret_cast<uint32_t*>(t + kCodeBytes + lane * 16 + j * 4) = sb | (mb << 16);
+  *reinterpret_cast<uint32_t*>(tile + kCodeBytes + lane * 16 + j * 4) = sb | (mb << 16);
+}
+
+// Thread = (tile, j, lane) -> (row, group), coalesced on the tile side.
+struct GroupIndex {
+  size_t tile;
+  int j, lane, r, g;
+};
+__device__ __forceinline__ GroupIndex group_index(size_t idx, int nkt) {
+  GroupIndex gi;
+  gi.lane = idx & 63;
+  const size_t rest = idx >> 6;
+  gi.j = rest & 3;
+  gi.tile = rest >> 2;
+  const int rt = (int)(gi.tile / nkt), kt = (int)(gi.tile % nkt);
+  gi.r = rt * 64 + gi.lane;
+  gi.g = kt * 4 + gi.j;
+  return gi;
+}
+
+__global__ void quantize_kernel(const float* __restrict__ w, int M, int K, int ld, int k_valid,
+                                uint8_t* __restrict__ tiles, int* __restrict__ err) {
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (size_t)M * (K / 32)) return;
+  const GroupIndex gi = group_index(idx, K / 128);
+  const float* row = w + (size_t)gi.r * ld;
+  float v[32];
+#pragma unroll
+  for (int c = 0; c < 32; ++c) {
+    const int col = gi.g * 32 + c;
+    v[c] = col < k_valid ? row[col] : 0.f;
+  }
+  quantize_group(v, tiles + gi.tile * kTileBytes, gi.j, gi.lane, err);
+}
+
+// Counter-based N(0, std) weights: splitmix64 of (seed, row*k_valid + col) -> Box-Muller.
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ float synth_normal(uint64_t seed, uint64_t i) {
+  const uint64_t h = splitmix64(seed * 0x100000001B3ull ^ splitmix64(i));
+  const float u1 = ((uint32_t)(h >> 40) + 1u) * (1.0f / 16777217.0f);  // (0, 1)
+  const float u2 = (uint32_t)(h & 0xFFFFFFu) * (1.0f / 16777216.0f);   // [0, 1)
+  return sqrtf(-2.0f * logf(u1)) * cospif(2.0f * u2);
+}
+
+__global__ void synth_quantize_kernel(uint64_t seed, float std, int M, int K, int k_valid,
+                                      uint8_t* __restrict__ tiles, int* __restrict__ err) {
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (size_t)M * (K / 32)) return;
+  const GroupIndex gi = group_index(idx, K / 128);
+  float v[32];
+#pragma unroll
+  for (int c = 0; c < 32; ++c) {
+    const int col = gi.g * 32 + c;
+    v[c] = col < k_valid ? std * synth_normal(seed, (uint64_t)gi.r * k_valid + col) : 0.f;
+  }
+  quantize_group(v, tiles + gi.tile * kTileBytes, gi.j, gi.lane, err);
 }
 
 }  // namespace
@@ -206,6 +250,14 @@ hipError_t launch_quantize(const float* w, int M, int K, int ld, int k_valid, ui
   const size_t n = (size_t)M * (K / 32);
   const unsigned blocks = (unsigned)((n + 255) / 256);
   hipLaunchKernelGGL(quantize_kernel, dim3(blocks), dim3(256), 0, st, w, M, K, ld, k_valid, tiles, err);
+  return hipGetLastError();
+}
+
+hipError_t launch_synth_quantize(uint64_t seed, float std, int M, int K, int k_valid, uint8_t* tiles, int* err,
+                                 hipStream_t st) {
+  const size_t n = (size_t)M * (K / 32);
+  const unsigned blocks = (unsigned)((n + 255) / 256);
+  hipLaunchKernelGGL(synth_quantize_kernel, dim3(blocks), dim3(256), 0, st, seed, std, M, K, k_valid, tiles, err);
   return hipGetLastError();
 }
 

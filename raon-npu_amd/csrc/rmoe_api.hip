@@ -449,6 +449,22 @@ int rmoe_layer_quantize_expert_dev(rmoe_ctx* ctx, int layer, int expert, const f
   return sync_and_check(ctx, st);
 }
 
+int rmoe_layer_synthesize_dev(rmoe_ctx* ctx, int layer, uint64_t seed, float std, void* stream) {
+  RmoeLayer* L;
+  TRY(check_layer(ctx, layer, &L));
+  if (!(std > 0.f) || !(std < 1e30f)) return fail(RMOE_EINVAL, "std must be positive and finite");
+  HIP_TRY(hipSetDevice(ctx->device));
+  hipStream_t st = pick_stream(ctx, stream);
+  const int ne = L->n_routed + L->n_shared;
+  for (int e = 0; e < ne; ++e) {
+    const uint64_t s_gu = seed * 1000003ull + (uint64_t)e * 2ull + 1ull;
+    const uint64_t s_dn = seed * 1000003ull + (uint64_t)e * 2ull + 2ull;
+    HIP_TRY(rmoe::launch_synth_quantize(s_gu, std, 2 * L->I, L->H, L->H, L->gu + (size_t)e * L->gu_bytes, ctx->s.err, st));
+    HIP_TRY(rmoe::launch_synth_quantize(s_dn, std, L->H, L->Ipad, L->I, L->dn + (size_t)e * L->dn_bytes, ctx->s.err, st));
+  }
+  return sync_and_check(ctx, st);
+}
+
 int rmoe_layer_download_expert(rmoe_ctx* ctx, int layer, int expert, void* gate_up, size_t gu_nbytes, void* down,
                                size_t dn_nbytes) {
   RmoeLayer* L;
@@ -567,6 +583,29 @@ int rmoe_moe_decode_dev(rmoe_ctx* ctx, int layer, const void* x_dev, void* out_d
   HIP_TRY(rmoe::launch_route(*L, (const uint16_t*)x_dev, 1, ids, wts, ctx->s.logits, ctx->s, st));
   hipError_t e = rmoe::launch_moe_decode(*L, (const uint16_t*)x_dev, ids, wts, L->top_k, true, act, gate_beta,
                                          value_beta, residual != 0, (uint16_t*)out_dev, nullptr, ctx->s, st);
+  if (e == hipErrorInvalidValue) return fail(RMOE_EINVAL, "scratch too small for layer %d: call rmoe_reserve", layer);
+  HIP_TRY(e);
+  return RMOE_OK;
+}
+
+int rmoe_moe_decode_stage_dev(rmoe_ctx* ctx, int layer, int stage, const void* x_dev, void* out_dev, int residual,
+                              int act, float gate_beta, float value_beta, void* stream) {
+  RmoeLayer* L;
+  TRY(check_layer(ctx, layer, &L));
+  if (stage < 0 || stage > 2) return fail(RMOE_EINVAL, "stage must be 0 (router), 1 (gate/up) or 2 (down)");
+  if (!L->has_router || L->n_shared < 1) return fail(RMOE_EINVAL, "layer %d needs a router and a shared expert", layer);
+  if (!x_dev || (stage == 2 && !out_dev)) return fail(RMOE_EINVAL, "null argument");
+  if (act != RMOE_ACT_SITU && act != RMOE_ACT_SWIGLU) return fail(RMOE_EINVAL, "unknown activation %d", act);
+  if ((size_t)L->top_k > ctx->s.route_elems || (size_t)L->n_routed > ctx->s.logit_elems)
+    return fail(RMOE_EINVAL, "scratch not reserved for layer %d", layer);
+  hipStream_t st = pick_stream(ctx, stream);
+  hipError_t e;
+  if (stage == 0) {
+    e = rmoe::launch_route(*L, (const uint16_t*)x_dev, 1, ctx->s.ids, ctx->s.wts, ctx->s.logits, ctx->s, st);
+  } else {
+    e = rmoe::launch_moe_decode(*L, (const uint16_t*)x_dev, ctx->s.ids, ctx->s.wts, L->top_k, true, act, gate_beta,
+                                value_beta, residual != 0, (uint16_t*)out_dev, nullptr, ctx->s, st, stage == 1 ? 1 : 2);
+  }
   if (e == hipErrorInvalidValue) return fail(RMOE_EINVAL, "scratch too small for layer %d: call rmoe_reserve", layer);
   HIP_TRY(e);
   return RMOE_OK;

@@ -117,6 +117,49 @@ __device__ __forceinline__ float act_apply(int act, float g, float u, float gb, 
   return act == 1 ? act_swiglu(g, u) : act_situ(g, u, gb, vb);
 }
 
+// ---- cross-workgroup hand-off inside one kernel ----------------------------------
+// An agent-scope fence (__threadfence) is a full L2 write-back + invalidate on this
+// multi-XCD part and costs microseconds per workgroup.  Data that one workgroup hands
+// to another inside a kernel is therefore written and read with device-scope relaxed
+// atomics (global_store/global_load with sc1: written through / read past the XCD's
+// L2), ordered by a workgroup-scope fence (s_waitcnt on the issuing wave) and a
+// device-scope atomic counter; no L2-wide maintenance is issued.
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_dev_u32(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Every thread of the block calls this after its st_dev() writes.  Returns true in
+// every thread of the block that is the n-th (last) to arrive at *counter, and then
+// resets the counter for the next launch.  Reads of the other blocks' data must use
+// ld_dev() after a true return.
+__device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned n, unsigned* flag_lds) {
+  // The workgroup-scope fence orders the compiler; it does not wait for global stores.
+  // Each wave waits for its own sc1 stores to be acknowledged (s_waitcnt vmcnt(0),
+  // encoded as 0 = every counter drained) before the block arrives at the counter.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned last = (prev == n - 1) ? 1u : 0u;
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag_lds = last;
+  }
+  __syncthreads();
+  const bool last = *flag_lds != 0u;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  return last;
+}
+
 // Wave-wide (64 lanes) sum.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -156,7 +199,7 @@ struct RmoeScratch {
   size_t n_counters = 0;
   uint16_t* h = nullptr;         // activations [slots, Ipad] / [A, Ipad]
   size_t h_elems = 0;
-  uint16_t* dout = nullptr;      // expert outputs [slots, H] / [A, H]
+  float* dout = nullptr;         // expert outputs [slots, H] (fp32 of the bf16-rounded value)
   size_t dout_elems = 0;
   int32_t* ids = nullptr;        // routing ids
   float* wts = nullptr;          // routing weights
@@ -191,6 +234,8 @@ hipError_t launch_relayout_in(const uint8_t* packed, uint8_t* tiles, int M, int 
 hipError_t launch_relayout_out(const uint8_t* tiles, uint8_t* packed, int M, int K, hipStream_t st);
 hipError_t launch_quantize(const float* w, int M, int K, int ld, int k_valid, uint8_t* tiles, int* err,
                            hipStream_t st);
+hipError_t launch_synth_quantize(uint64_t seed, float std, int M, int K, int k_valid, uint8_t* tiles, int* err,
+                                 hipStream_t st);
 
 hipError_t launch_linear(const uint8_t* tiles, int M, int K, const uint16_t* x, int T, uint16_t* y, RmoeScratch& s,
                          hipStream_t st);
@@ -203,7 +248,7 @@ hipError_t launch_route(const RmoeLayer& L, const uint16_t* x, int T, int32_t* i
 // (routed + shared, + x when residual).
 hipError_t launch_moe_decode(const RmoeLayer& L, const uint16_t* x, const int32_t* ids, const float* wts, int k,
                              bool with_shared, int act, float gb, float vb, bool residual, uint16_t* out,
-                             uint16_t* out_routed, RmoeScratch& s, hipStream_t st);
+                             uint16_t* out_routed, RmoeScratch& s, hipStream_t st, int stages = 3);
 
 hipError_t launch_dispatch(const int32_t* ids, int T, int k, int n_experts, int32_t* order, int32_t* inv,
                            int32_t* offsets, RmoeScratch& s, hipStream_t st);

@@ -165,6 +165,11 @@ class MoeLayer:
         call("rmoe_layer_quantize_expert_dev", self.ctx.handle, self.layer, int(expert), ptr(gate_up_dev),
              ptr(down_dev), _stream_ptr(stream))
 
+    def synthesize(self, seed: int, std: float = 0.02, stream=None):
+        """Seeded N(0, std) weights for every expert, generated and quantized on the device."""
+        call("rmoe_layer_synthesize_dev", self.ctx.handle, self.layer, int(seed) & (2**64 - 1), float(std),
+             _stream_ptr(stream))
+
     def download_expert(self, expert: int) -> tuple[bytes, bytes]:
         gu = np.empty(self.geom.gu_bytes, np.uint8)
         dn = np.empty(self.geom.dn_bytes, np.uint8)
@@ -236,6 +241,17 @@ class MoeLayer:
             _check_dev(wts_dev, (g.top_k,), "float32", "wts")
         call("rmoe_moe_decode_dev", self.ctx.handle, self.layer, ptr(x_dev), ptr(out_dev), int(bool(residual)), act,
              gb, vb, ptr(ids_dev), ptr(wts_dev), _stream_ptr(stream))
+
+    def moe_decode_stage_dev(self, stage: int, x_dev, out_dev=None, residual: bool = False, gate_beta=None,
+                             value_beta=None, stream=None):
+        """Launch one decode stage (0 router, 1 gate/up + activation, 2 down + combine)."""
+        act, gb, vb = act_code(gate_beta, value_beta)
+        g = self.geom
+        _check_dev(x_dev, (g.hidden,), "int16", "x")
+        if out_dev is not None:
+            _check_dev(out_dev, (g.hidden,), "int16", "out")
+        call("rmoe_moe_decode_stage_dev", self.ctx.handle, self.layer, int(stage), ptr(x_dev), ptr(out_dev),
+             int(bool(residual)), act, gb, vb, _stream_ptr(stream))
 
     def moe_experts_grouped(self, x, top_ids, top_weights, shared_gu, gate_beta=4.0, value_beta=25.0):
         xa = _u16(x, "x")
