@@ -1,0 +1,669 @@
+// Prefill (many-token) MoE on bf16 MFMA: router GEMM + top-k, tile table over the
+// dispatch, grouped q4nx GEMMs (gate/up with the activation fused, down), ordered
+// combine.  Restates NpuBackend.moe_experts_grouped (npu/backend.py:4845-4979) and the
+// planner's scatter/combine (kernels/moe_grouped/planner.py:184-322) on the device.
+//
+// q4nx on MFMA without rounding the weights:  w = min + scale*n  (n = 4-bit code).
+// For one 32-column group g and a tile of tokens m and weight rows r:
+//   sum_k x[m,k] w[r,k] = 16*scale[r]*C'[m,r] + (min[r] - 16*scale[r]) * S[m]
+// where C' = sum_k x[m,k]*(1 + n[r,k]/16) is one v_mfma_f32_16x16x32_bf16 with the
+// codes as exact bf16 values (1 + n/16) and S[m] = sum_k x[m,k].  The first term is
+// added per group with one fp32 FMA per output (scales differ per row and group); the
+// second is a small GEMM over the groups, done on MFMA with S and the coefficient
+// split into bf16 hi + lo parts (relative error ~2^-16).
+#include "rmoe_internal.h"
+
+namespace rmoe {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_t mfma16(const uint4 a, const uint4 b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                 0, 0, 0);
+}
+
+// Exact 3-way bf16 split of an fp32 value: v = hi + mid + lo (8 + 8 + 8 significant
+// bits cover the 24 of fp32), each part the RNE bf16 of the remainder.
+__device__ __forceinline__ void split3_bf16(float v, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
+  hi = f32_to_bf16(v);
+  const float r = v - bf16_to_f32(hi);
+  mid = f32_to_bf16(r);
+  lo = f32_to_bf16(r - bf16_to_f32(mid));
+}
+// Group sums are stored as two dwords per (row, group): (hi | mid << 16), lo.
+__device__ __forceinline__ void store_split3(uint32_t* dst, float v) {
+  uint32_t hi, mid, lo;
+  split3_bf16(v, hi, mid, lo);
+  dst[0] = hi | (mid << 16);
+  dst[1] = lo;
+}
+
+// ---------------------------------------------------------------- router GEMM --
+// logits[T, E] = x[T, H] . Wr[E, H]^T on MFMA (exact bf16 products, fp32 sums).
+// Block: 4 waves, 64 tokens; wave w: tokens 16w..16w+15 x all experts (E/16 n-frags).
+constexpr int kMaxEFrags = 16;  // E <= 256
+
+__global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __restrict__ x, int T, int H,
+                                                          const uint16_t* __restrict__ w, int E,
+                                                          float* __restrict__ logits) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t0 = blockIdx.x * 64 + wave * 16;
+  const int nfr = E / 16;
+  f32x4_t acc[kMaxEFrags];
+#pragma unroll
+  for (int f = 0; f < kMaxEFrags; ++f) acc[f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int tok = min(t0 + (lane & 15), T - 1);
+  const uint16_t* xr = x + (size_t)tok * H + 8 * (lane >> 4);
+  for (int k0 = 0; k0 < H; k0 += 32) {
+    const uint4 a = *reinterpret_cast<const uint4*>(xr + k0);
+#pragma unroll
+    for (int f = 0; f < kMaxEFrags; ++f) {
+      if (f < nfr) {
+        const uint4 b = *reinterpret_cast<const uint4*>(w + (size_t)(16 * f + (lane & 15)) * H + k0 + 8 * (lane >> 4));
+        acc[f] = mfma16(a, b, acc[f]);
+      }
+    }
+  }
+#pragma unroll
+  for (int f = 0; f < kMaxEFrags; ++f) {
+    if (f < nfr) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + 4 * (lane >> 4) + i;
+        if (t < T) logits[(size_t)t * E + 16 * f + (lane & 15)] = acc[f][i];
+      }
+    }
+  }
+}
+
+// numpy float32 sum order (pairwise_sum, n <= 128 per block of 8 partial sums).
+__device__ float np_sum_f32_lds(const float* v, int n) {
+  if (n < 8) {
+    float r = 0.f;
+    for (int i = 0; i < n; ++i) r = __fadd_rn(r, v[i]);
+    return r;
+  }
+  float r[8];
+  for (int j = 0; j < 8; ++j) r[j] = v[j];
+  int i = 8;
+  for (; i + 8 <= n; i += 8)
+    for (int j = 0; j < 8; ++j) r[j] = __fadd_rn(r[j], v[i + j]);
+  float res = __fadd_rn(__fadd_rn(__fadd_rn(r[0], r[1]), __fadd_rn(r[2], r[3])),
+                        __fadd_rn(__fadd_rn(r[4], r[5]), __fadd_rn(r[6], r[7])));
+  for (; i < n; ++i) res = __fadd_rn(res, v[i]);
+  return res;
+}
+
+// One wave per token: scores, selection (score + bias, ties to the lower id), renorm.
+__global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int T, int E, int k, int score,
+                                                   const float* __restrict__ bias, int renorm, float scaling,
+                                                   int32_t* __restrict__ ids, float* __restrict__ wts) {
+  __shared__ float sc[4][256];
+  __shared__ float ch[4][16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  const float* lg = logits + (size_t)t * E;
+  float* s = sc[wave];
+  if (score == 0) {
+    for (int e = lane; e < E; e += 64) s[e] = 1.0f / (1.0f + expf(-lg[e]));
+  } else {
+    float m = -__builtin_inff();
+    for (int e = lane; e < E; e += 64) m = fmaxf(m, lg[e]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    for (int e = lane; e < E; e += 64) s[e] = expf(lg[e] - m);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    float total = 0.f;
+    if (lane == 0) total = np_sum_f32_lds(s, E);
+    total = __shfl(total, 0, 64);
+    __builtin_amdgcn_wave_barrier();
+    for (int e = lane; e < E; e += 64) s[e] = s[e] / total;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  // Candidates of this lane: e = lane + 64*i; taken flags in a lane mask.
+  uint32_t taken = 0u;
+  int chosen_id = 0;
+  for (int r = 0; r < k; ++r) {
+    float best = 0.f;
+    int bid = 0x7fffffff;
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E && !((taken >> i) & 1u)) {
+        const float c = bias ? __fadd_rn(s[e], bias[e]) : s[e];
+        if (bid == 0x7fffffff || c > best) {
+          best = c;
+          bid = e;
+        }
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ob = __shfl_xor(best, off, 64);
+      const int oi = __shfl_xor(bid, off, 64);
+      if (oi != 0x7fffffff && (bid == 0x7fffffff || ob > best || (ob == best && oi < bid))) {
+        best = ob;
+        bid = oi;
+      }
+    }
+    if ((bid & 63) == lane) taken |= 1u << (bid >> 6);
+    if (lane == r) chosen_id = bid;
+    if (lane == 0) ch[wave][r] = s[bid];
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  float denom = 1.f;
+  if (lane == 0 && renorm) denom = __fadd_rn(np_sum_f32_lds(ch[wave], k), 1e-20f);
+  denom = __shfl(denom, 0, 64);
+  if (lane < k) {
+    float v = renorm ? ch[wave][lane] / denom : ch[wave][lane];
+    ids[(size_t)t * k + lane] = chosen_id;
+    wts[(size_t)t * k + lane] = __fmul_rn(v, scaling);
+  }
+}
+
+// ------------------------------------------------------------ row group sums --
+// S[row, g] = sum of the 32 bf16 values of group g of row `row`, stored as an exact
+// 3-way bf16 split in dwords dst32[(row*G + g)*2 + {0,1}].  Thread per (row, group).
+__global__ void group_sums_kernel(const uint16_t* __restrict__ src, int rows, int K, uint32_t* __restrict__ dst) {
+  const int G = K / 32;
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (size_t)rows * G) return;
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(src + idx * 32);
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    const uint32_t v = p[c];
+    s += bf16_to_f32(v & 0xffffu);
+    s += bf16_to_f32(v >> 16);
+  }
+  store_split3(dst + idx * 2, s);
+}
+
+// ----------------------------------------------------------------- tile table --
+// tiles[i] = expert | (row_start << 9) for the m-tiles of every group; group e covers
+// sorted rows [offsets[e], offsets[e+1]); the extra group n_routed (shared expert)
+// covers rows [offsets[n_routed], offsets[n_routed] + shared_rows).  tiles[-1]... the
+// count is written to *ntiles.
+constexpr int kBM = 128;
+
+__global__ void tile_table_kernel(const int32_t* __restrict__ offsets, int n_routed, int shared_rows,
+                                  uint32_t* __restrict__ tiles, int* __restrict__ ntiles, int cap) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  int n = 0;
+  const int ng = n_routed + (shared_rows > 0 ? 1 : 0);
+  for (int e = 0; e < ng; ++e) {
+    const int b = offsets[min(e, n_routed)];
+    const int end = e < n_routed ? offsets[e + 1] : b + shared_rows;
+    for (int r = b; r < end && n < cap; r += kBM) tiles[n++] = (uint32_t)e | ((uint32_t)r << 9);
+  }
+  *ntiles = n;
+}
+
+// ------------------------------------------------------------- grouped GEMM --
+struct GemmArgs {
+  // weights: expert e at wbase + e*wstride, q4nx tiles of an [N_total, K] matrix
+  const uint8_t* wbase;
+  size_t wstride;
+  int K;             // input width (multiple of 128)
+  int N_total;       // weight rows (gate/up: 2I; down: H)
+  int inter;         // gate/up: I (the up rows start at I)
+  int mode;          // 0: gate/up + activation -> h; 1: down -> D
+  int n_tiles;       // WG N-tiles (gate/up: I/64; down: N_total/128)
+  // activation rows
+  const uint16_t* src;      // mode 0: x [T, K] gathered by token; mode 1: h [rows, K] in sorted order
+  const int32_t* order;     // mode 0: sorted position -> assignment (token*k + route)
+  int k_routes;
+  int n_routed;             // group id n_routed = shared expert (rows identity tokens / sorted)
+  int shared_base;          // sorted row index of the first shared row
+  const uint32_t* ssum;     // row group sums, 2 dwords each: mode 0 [T, K/32] by token; mode 1 [rows, K/32] by row
+  const uint32_t* tiles;
+  const int* ntiles;
+  const int32_t* offsets;   // group row ends: offsets[e+1] (routed); shared end = shared_base + shared_rows
+  int shared_rows;
+  // outputs
+  uint16_t* out;            // mode 0: h [rows, out_ld]; mode 1: D [rows, out_ld]
+  int out_ld;
+  uint32_t* out_ssum;       // mode 0: group sums of h rows [rows, out_ld/32], 2 dwords each
+  int act;
+  float gb, vb;
+};
+
+constexpr int kXStride = 128 + 8;  // bf16 elements per LDS row (pad: 16 B)
+
+__device__ __forceinline__ int group_end(const GemmArgs& a, int e) {
+  return e < a.n_routed ? a.offsets[e + 1] : a.shared_base + a.shared_rows;
+}
+
+// Source row of sorted row p.
+__device__ __forceinline__ const uint16_t* src_row(const GemmArgs& a, int e, int p) {
+  if (a.mode == 1) return a.src + (size_t)p * a.K;
+  const int tok = e < a.n_routed ? a.order[p] / a.k_routes : p - a.shared_base;
+  return a.src + (size_t)tok * a.K;
+}
+__device__ __forceinline__ const uint32_t* ssum_row(const GemmArgs& a, int e, int p) {
+  const int G = a.K / 32;
+  if (a.mode == 1) return a.ssum + (size_t)p * G * 2;
+  const int tok = e < a.n_routed ? a.order[p] / a.k_routes : p - a.shared_base;
+  return a.ssum + (size_t)tok * G * 2;
+}
+
+// Grid: n_tiles * tile_cap workgroups (rounded to a multiple of 8), 256 threads.
+__global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a, int tile_cap) {
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][kBM * kXStride];
+  __shared__ float hsum[4][kBM][2];
+  // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs; make each XCD
+  // take a contiguous range of (n-tile, m-tile) so m-tiles sharing a weight tile meet
+  // in the same L2.
+  const int nb = gridDim.x, per = nb / 8;
+  const int lid = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  const int nt = lid / tile_cap, mt = lid % tile_cap;
+  if (nt >= a.n_tiles || mt >= *a.ntiles) return;
+  const uint32_t te = a.tiles[mt];
+  const int e = (int)(te & 511u), row0 = (int)(te >> 9);
+  const int rend = group_end(a, e);
+  const int nrows = min(kBM, rend - row0);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, lq = lane >> 4;
+  const int nkt = a.K / kTileCols;
+  const uint8_t* W = a.wbase + (size_t)e * a.wstride;
+  // The wave's two n-fragments: rows within the weight matrix.
+  int wrow[2];
+  if (a.mode == 0) {
+    wrow[0] = 64 * nt + 16 * wave;            // gate
+    wrow[1] = a.inter + 64 * nt + 16 * wave;  // up
+  } else {
+    wrow[0] = 128 * nt + 16 * wave;
+    wrow[1] = 128 * nt + 64 + 16 * wave;
+  }
+
+  // Per-thread source rows for the X staging: thread loads 16 B pieces.
+  // A tile step is 128 rows x 128 k = 128 rows x 16 pieces; 256 threads -> 8 pieces each.
+  auto stage = [&](int buf, int kt) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int piece = tid + 256 * q;
+      const int r = piece >> 4, c = piece & 15;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (r < nrows) v = *reinterpret_cast<const uint4*>(src_row(a, e, row0 + r) + kt * 128 + 8 * c);
+      *reinterpret_cast<uint4*>(&xs[buf][r * kXStride + 8 * c]) = v;
+    }
+  };
+
+  f32x4_t acc[8][2];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    acc[m][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    acc[m][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+
+  stage(0, 0);
+  __syncthreads();
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nkt) stage(cur ^ 1, kt + 1);
+    // Weight fragments of this K tile for the wave's two n-fragments.
+    uint32_t code[2][4];
+    uint4 smv[2];
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const int rt = wrow[f] / 64, r_in = wrow[f] % 64 + l16;
+      const uint8_t* tile = W + ((size_t)rt * nkt + kt) * kTileBytes;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) code[f][j] = *reinterpret_cast<const uint32_t*>(tile + j * 1024 + r_in * 16 + 4 * lq);
+      smv[f] = *reinterpret_cast<const uint4*>(tile + kCodeBytes + r_in * 16);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint4 b[2];
+      float s16[2];
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        uint32_t p0, p1, p2, p3;
+        unpack_codes(code[f][j], p0, p1, p2, p3);
+        b[f] = make_uint4(p0, p1, p2, p3);
+        const uint32_t smw = j == 0 ? smv[f].x : (j == 1 ? smv[f].y : (j == 2 ? smv[f].z : smv[f].w));
+        s16[f] = 16.f * bf16_to_f32(smw & 0xffffu);
+      }
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const uint4 av = *reinterpret_cast<const uint4*>(&xs[cur][(16 * m + l16) * kXStride + 32 * j + 8 * lq]);
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+          const f32x4_t c = mfma16(av, b[f], zero);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[m][f][i] = fmaf(s16[f], c[i], acc[m][f][i]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // Correction: y += sum_g (min - 16*scale)[r, g] * S[m, g] over blocks of 32 groups,
+  // both factors split exactly into 3 bf16 parts; the 6 leading products are kept.
+  const int G = a.K / 32;
+  auto pack8 = [](const uint32_t* v) {
+    return make_uint4(v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16), v[6] | (v[7] << 16));
+  };
+  for (int g0 = 0; g0 < G; g0 += 32) {
+    uint4 bc[2][3];
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      uint32_t hv[8], mv[8], lv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int g = g0 + 8 * lq + i;
+        float coef = 0.f;
+        if (g < G) {
+          const int rt = wrow[f] / 64, r_in = wrow[f] % 64 + l16;
+          const uint8_t* tile = W + ((size_t)rt * nkt + g / 4) * kTileBytes;
+          const uint32_t smw = *reinterpret_cast<const uint32_t*>(tile + kCodeBytes + r_in * 16 + 4 * (g % 4));
+          const float sc = bf16_to_f32(smw & 0xffffu), mn = bf16_to_f32(smw >> 16);
+          coef = mn - 16.f * sc;
+        }
+        split3_bf16(coef, hv[i], mv[i], lv[i]);
+      }
+      bc[f][0] = pack8(hv);
+      bc[f][1] = pack8(mv);
+      bc[f][2] = pack8(lv);
+    }
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int r = 16 * m + l16;
+      uint32_t sh[8], sm2[8], sl[8];
+      const uint32_t* sp = r < nrows ? ssum_row(a, e, row0 + r) : nullptr;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int g = g0 + 8 * lq + i;
+        uint32_t v0 = 0u, v1 = 0u;
+        if (sp && g < G) {
+          v0 = sp[2 * g];
+          v1 = sp[2 * g + 1];
+        }
+        sh[i] = v0 & 0xffffu;
+        sm2[i] = v0 >> 16;
+        sl[i] = v1 & 0xffffu;
+      }
+      const uint4 ah = pack8(sh), am = pack8(sm2), al = pack8(sl);
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        f32x4_t c = acc[m][f];
+        c = mfma16(al, bc[f][0], c);
+        c = mfma16(am, bc[f][1], c);
+        c = mfma16(ah, bc[f][2], c);
+        c = mfma16(am, bc[f][0], c);
+        c = mfma16(ah, bc[f][1], c);
+        c = mfma16(ah, bc[f][0], c);
+        acc[m][f] = c;
+      }
+    }
+  }
+
+  // Epilogue.  C layout: lane holds rows 16m + 4*lq + i, column l16 of the fragment.
+  if (a.mode == 0) {
+    const int col = 64 * nt + 16 * wave + l16;  // intermediate unit
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * m + 4 * lq + i;
+        const float g = bf16_round(acc[m][0][i]), u = bf16_round(acc[m][1][i]);
+        const uint32_t h = f32_to_bf16(act_apply(a.act, g, u, a.gb, a.vb));
+        if (r < nrows) a.out[(size_t)(row0 + r) * a.out_ld + col] = (uint16_t)h;
+        // Group sums of h: reduce the 16 columns of this wave, then 2 waves per group.
+        float hv = r < nrows ? bf16_to_f32(h) : 0.f;
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) hv += __shfl_xor(hv, off, 16);
+        if (l16 == 0) hsum[wave][r][0] = hv;
+      }
+    }
+    __syncthreads();
+    // Group (32 columns) = waves {0,1} and {2,3}; 64*nt + 32*q is group 2*nt + q.
+    for (int idx = tid; idx < kBM * 2; idx += 256) {
+      const int r = idx >> 1, q = idx & 1;
+      if (r < nrows) {
+        const float s = hsum[2 * q][r][0] + hsum[2 * q + 1][r][0];
+        store_split3(a.out_ssum + ((size_t)(row0 + r) * (a.out_ld / 32) + 2 * nt + q) * 2, s);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 16 * m + 4 * lq + i;
+          if (r < nrows) a.out[(size_t)(row0 + r) * a.out_ld + wrow[f] + l16] = (uint16_t)f32_to_bf16(acc[m][f][i]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- combine --
+// out[t] = RTNE(RTNE(sum_{routes by ascending expert} f32(D[inv[t,r]]) * w[t,r]) + D_shared[t])
+// (+ x[t] with residual); optionally also the routed and shared rows separately.
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ D, int H, const int32_t* __restrict__ ids,
+                                                      const float* __restrict__ wts, const int32_t* __restrict__ inv,
+                                                      int k, int shared_base, const uint16_t* __restrict__ x,
+                                                      uint16_t* __restrict__ out, uint16_t* __restrict__ routed,
+                                                      uint16_t* __restrict__ shared_out, int has_shared) {
+  const int t = blockIdx.x;
+  __shared__ int ord[16];
+  if (threadIdx.x == 0) {
+    int prev = -1;
+    for (int r = 0; r < k; ++r) {
+      int best = 0x7fffffff, bs = 0;
+      for (int q = 0; q < k; ++q) {
+        const int eq = ids[(size_t)t * k + q];
+        if (eq > prev && eq < best) {
+          best = eq;
+          bs = q;
+        }
+      }
+      prev = best;
+      ord[r] = bs;
+    }
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < H; c += blockDim.x) {
+    float acc = 0.f;
+    for (int r = 0; r < k; ++r) {
+      const int q = ord[r];
+      const int pos = inv[(size_t)t * k + q];
+      acc = __fadd_rn(acc, __fmul_rn(bf16_to_f32(D[(size_t)pos * H + c]), wts[(size_t)t * k + q]));
+    }
+    uint32_t o = f32_to_bf16(acc);
+    if (routed) routed[(size_t)t * H + c] = (uint16_t)o;
+    if (has_shared) {
+      const uint16_t sd = D[(size_t)(shared_base + t) * H + c];
+      if (shared_out) shared_out[(size_t)t * H + c] = sd;
+      o = f32_to_bf16(__fadd_rn(bf16_to_f32(o), bf16_to_f32(sd)));
+    }
+    if (x) o = f32_to_bf16(__fadd_rn(bf16_to_f32(x[(size_t)t * H + c]), bf16_to_f32(o)));
+    if (out) out[(size_t)t * H + c] = (uint16_t)o;
+  }
+}
+
+// Zero h[:, I:Ipad] and the group sums of those columns (thread per row).
+__global__ void zero_pad_cols_kernel(uint16_t* __restrict__ h, uint32_t* __restrict__ hsum, int rows, int I, int Ipad) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  for (int c = I; c < Ipad; ++c) h[(size_t)r * Ipad + c] = 0;
+  // Groups entirely past I; a group straddling I gets its sum from the GEMM epilogue
+  // only when I is a multiple of 32 (guaranteed: I % 64 == 0).
+  for (int g = I / 32; g < Ipad / 32; ++g) {
+    hsum[((size_t)r * (Ipad / 32) + g) * 2] = 0u;
+    hsum[((size_t)r * (Ipad / 32) + g) * 2 + 1] = 0u;
+  }
+}
+
+// h[shared_base + t] = RTNE(act(shared_gu[t])) (padded to Ipad) and its group sums.
+__global__ void shared_act_kernel(const uint16_t* __restrict__ gu, int T, int I, int Ipad, int act, float gb, float vb,
+                                  uint16_t* __restrict__ h, uint32_t* __restrict__ hsum) {
+  const int G = Ipad / 32;
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (size_t)T * G) return;
+  const int t = (int)(idx / G), g = (int)(idx % G);
+  float s = 0.f;
+  for (int c = 0; c < 32; ++c) {
+    const int col = 32 * g + c;
+    uint16_t v = 0;
+    if (col < I) {
+      const float gg = bf16_to_f32(gu[(size_t)t * 2 * I + col]);
+      const float uu = bf16_to_f32(gu[(size_t)t * 2 * I + I + col]);
+      v = (uint16_t)f32_to_bf16(act_apply(act, gg, uu, gb, vb));
+    }
+    h[(size_t)t * Ipad + col] = v;
+    s += bf16_to_f32(v);
+  }
+  store_split3(hsum + ((size_t)t * G + g) * 2, s);
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ launchers --
+hipError_t launch_router_gemm(const uint16_t* x, int T, int H, const uint16_t* w, int E, float* logits, hipStream_t st) {
+  if (E % 16 || E > 16 * kMaxEFrags || H % 32) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(router_gemm_kernel, dim3((T + 63) / 64), dim3(256), 0, st, x, T, H, w, E, logits);
+  return hipGetLastError();
+}
+
+hipError_t launch_topk(const float* logits, int T, int E, int k, int score, const float* bias, int renorm,
+                       float scaling, int32_t* ids, float* wts, hipStream_t st) {
+  if (E > 256 || k > 16 || k > 64) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(topk_kernel, dim3((T + 3) / 4), dim3(256), 0, st, logits, T, E, k, score, bias, renorm, scaling,
+                     ids, wts);
+  return hipGetLastError();
+}
+
+size_t prefill_scratch_bytes(const RmoeLayer& L, int T) {
+  const size_t A = (size_t)T * L.top_k, R = A + T;
+  const size_t tiles = A / kBM + L.n_routed + T / kBM + 4;
+  return R * L.Ipad * 2                  // h
+         + R * (L.Ipad / 32) * 8         // h group sums
+         + R * L.H * 2                   // D
+         + (size_t)T * (L.H / 32) * 8    // x group sums
+         + (size_t)T * L.n_routed * 4    // logits
+         + tiles * 4 + 256 * 3;          // tile table, counts
+}
+
+hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, const int32_t* ids_in, const float* wts_in,
+                              int32_t* ids_out, float* wts_out, const uint16_t* shared_gu, int act, float gb, float vb,
+                              bool residual, uint16_t* out, uint16_t* routed, uint16_t* shared_down, uint8_t* scratch,
+                              size_t scratch_bytes, RmoeScratch& s, hipStream_t st) {
+  const int k = L.top_k, E = L.n_routed;
+  const size_t A = (size_t)T * k, R = A + T;
+  if (L.n_shared < 1 || prefill_scratch_bytes(L, T) > scratch_bytes) return hipErrorInvalidValue;
+  if (A > s.order_elems || (size_t)((A + 1023) / 1024) * E > s.chunk_elems) return hipErrorInvalidValue;
+  uint8_t* p = scratch;
+  auto carve = [&](size_t bytes) {
+    uint8_t* q = p;
+    p += (bytes + 255) / 256 * 256;
+    return q;
+  };
+  uint16_t* h = (uint16_t*)carve(R * L.Ipad * 2);
+  uint32_t* hsum = (uint32_t*)carve(R * (L.Ipad / 32) * 8);
+  uint16_t* D = (uint16_t*)carve(R * L.H * 2);
+  uint32_t* xsum = (uint32_t*)carve((size_t)T * (L.H / 32) * 8);
+  float* logits = (float*)carve((size_t)T * E * 4);
+  const int tile_cap = (int)(A / kBM + E + T / kBM + 4);
+  uint32_t* tiles = (uint32_t*)carve((size_t)tile_cap * 4);
+  int* ntiles = (int*)carve(256);
+  hipError_t err;
+  const int32_t* ids = ids_in;
+  const float* wts = wts_in;
+  if (!ids_in) {
+    err = launch_router_gemm(x, T, L.H, L.router_w, E, logits, st);
+    if (err != hipSuccess) return err;
+    err = launch_topk(logits, T, E, k, L.score, L.router_bias, L.renorm, L.scaling, ids_out, wts_out, st);
+    if (err != hipSuccess) return err;
+    ids = ids_out;
+    wts = wts_out;
+  }
+  err = launch_dispatch(ids, T, k, E, s.order, s.inv, s.offsets, s, st);
+  if (err != hipSuccess) return err;
+  {
+    const size_t n = (size_t)T * (L.H / 32);
+    hipLaunchKernelGGL(group_sums_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, T, L.H, xsum);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+  }
+  if (L.Ipad > L.I) {
+    // h columns past I (and their group sums) feed the zero-padded down columns.
+    hipLaunchKernelGGL(zero_pad_cols_kernel, dim3((unsigned)((R + 255) / 256)), dim3(256), 0, st, h, hsum, (int)R, L.I,
+                       L.Ipad);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+  }
+  // Gate/up (+ activation): routed groups, and the shared expert unless its gate/up is given.
+  GemmArgs g{};
+  g.wbase = L.gu;
+  g.wstride = L.gu_bytes;
+  g.K = L.H;
+  g.N_total = 2 * L.I;
+  g.inter = L.I;
+  g.mode = 0;
+  g.n_tiles = L.I / 64;
+  g.src = x;
+  g.order = s.order;
+  g.k_routes = k;
+  g.n_routed = E;
+  g.shared_base = (int)A;
+  g.ssum = xsum;
+  g.tiles = tiles;
+  g.ntiles = ntiles;
+  g.offsets = s.offsets;
+  g.shared_rows = shared_gu ? 0 : T;
+  g.out = h;
+  g.out_ld = L.Ipad;
+  g.out_ssum = hsum;
+  g.act = act;
+  g.gb = gb;
+  g.vb = vb;
+  hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(64), 0, st, s.offsets, E, g.shared_rows, tiles, ntiles, tile_cap);
+  if ((err = hipGetLastError()) != hipSuccess) return err;
+  if (shared_gu) {
+    const size_t n = (size_t)T * (L.Ipad / 32);
+    hipLaunchKernelGGL(shared_act_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, shared_gu, T, L.I,
+                       L.Ipad, act, gb, vb, h + A * L.Ipad, hsum + A * (L.Ipad / 32) * 2);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+  }
+  {
+    const int blocks = (g.n_tiles * tile_cap + 7) / 8 * 8;  // the XCD mapping needs a multiple of 8
+    hipLaunchKernelGGL(grouped_gemm_kernel, dim3(blocks), dim3(256), 0, st, g, tile_cap);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+  }
+  // Down: every sorted row (routed + shared), rows of h contiguous.
+  if (shared_gu) {
+    hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(64), 0, st, s.offsets, E, T, tiles, ntiles, tile_cap);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+  }
+  GemmArgs d = g;
+  d.wbase = L.dn;
+  d.wstride = L.dn_bytes;
+  d.K = L.Ipad;
+  d.N_total = L.H;
+  d.mode = 1;
+  d.n_tiles = L.H / 128;
+  d.src = h;
+  d.ssum = hsum;
+  d.shared_rows = T;
+  d.out = D;
+  d.out_ld = L.H;
+  d.out_ssum = nullptr;
+  {
+    const int blocks = (d.n_tiles * tile_cap + 7) / 8 * 8;
+    hipLaunchKernelGGL(grouped_gemm_kernel, dim3(blocks), dim3(256), 0, st, d, tile_cap);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+  }
+  hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, st, D, L.H, ids, wts, s.inv, k, (int)A,
+                     residual ? x : nullptr, out, routed, shared_down, 1);
+  return hipGetLastError();
+}
+
+}  // namespace rmoe

@@ -108,8 +108,7 @@ int reserve_layer(rmoe_ctx* ctx, const RmoeLayer& L, int T, int k) {
   const size_t counters = std::max({rmoe::decode_scratch_counters(Lk), c1, c2, (size_t)T});
   TRY(grow(s.part, s.part_floats, floats, ctx));
   TRY(grow(s.counters, s.n_counters, counters, ctx));
-  const size_t h = (size_t)(kk + 1) * L.Ipad + (size_t)T * (2 * L.I + L.Ipad + 2 * L.H);
-  TRY(grow(s.h, s.h_elems, h, ctx));
+  TRY(grow(s.h, s.h_elems, (size_t)(kk + 1) * L.Ipad, ctx));
   TRY(grow(s.dout, s.dout_elems, (size_t)(kk + 1) * L.H, ctx));
   size_t re = s.route_elems;
   TRY(grow(s.ids, re, (size_t)T * kk, ctx));
@@ -125,6 +124,7 @@ int reserve_layer(rmoe_ctx* ctx, const RmoeLayer& L, int T, int k) {
   TRY(grow(s.inv, oe, (size_t)T * kk, ctx));
   s.order_elems = oe;
   TRY(grow(s.offsets, s.offset_elems, 257, ctx));
+  if (L.n_shared > 0) TRY(grow(s.pf, s.pf_bytes, rmoe::prefill_scratch_bytes(Lk, T), ctx));
   s.max_tokens = std::max(s.max_tokens, T);
   return RMOE_OK;
 }
@@ -200,7 +200,7 @@ int rmoe_destroy(rmoe_ctx* ctx) {
   }
   RmoeScratch& s = ctx->s;
   void* bufs[] = {s.part, s.counters, s.h, s.dout, s.ids, s.wts, s.logits, s.order, s.inv, s.offsets,
-                  s.chunk_counts, s.err, s.staging};
+                  s.chunk_counts, s.err, s.staging, s.pf};
   for (void* b : bufs)
     if (b) hipFree(b);
   auto it = g_io.find(ctx);
@@ -679,8 +679,8 @@ int rmoe_moe_experts_grouped(rmoe_ctx* ctx, int layer, const uint16_t* x, int T,
   HIP_TRY(hipMemcpyAsync(idd, top_ids, (size_t)T * k * 4, hipMemcpyHostToDevice, ctx->stream));
   HIP_TRY(hipMemcpyAsync(wd, top_weights, (size_t)T * k * 4, hipMemcpyHostToDevice, ctx->stream));
   HIP_TRY(hipMemcpyAsync(gd, shared_gu, (size_t)T * 2 * L->I * 2, hipMemcpyHostToDevice, ctx->stream));
-  HIP_TRY(rmoe::launch_moe_grouped(*L, xd, T, idd, wd, gd, false, act, gate_beta, value_beta, false, rd, sd, nullptr,
-                                   ctx->s, ctx->stream));
+  HIP_TRY(rmoe::launch_moe_prefill(*L, xd, T, idd, wd, nullptr, nullptr, gd, act, gate_beta, value_beta, false, nullptr,
+                                   rd, sd, ctx->s.pf, ctx->s.pf_bytes, ctx->s, ctx->stream));
   HIP_TRY(hipMemcpyAsync(routed, rd, (size_t)T * L->H * 2, hipMemcpyDeviceToHost, ctx->stream));
   HIP_TRY(hipMemcpyAsync(shared_down, sd, (size_t)T * L->H * 2, hipMemcpyDeviceToHost, ctx->stream));
   return sync_and_check(ctx, ctx->stream);
@@ -698,9 +698,9 @@ int rmoe_moe_prefill_dev(rmoe_ctx* ctx, int layer, const void* x_dev, int T, voi
   hipStream_t st = pick_stream(ctx, stream);
   int32_t* ids = top_ids_dev ? (int32_t*)top_ids_dev : ctx->s.ids;
   float* wts = top_weights_dev ? (float*)top_weights_dev : ctx->s.wts;
-  HIP_TRY(rmoe::launch_route(*L, (const uint16_t*)x_dev, T, ids, wts, ctx->s.logits, ctx->s, st));
-  hipError_t e = rmoe::launch_moe_grouped(*L, (const uint16_t*)x_dev, T, ids, wts, nullptr, true, act, gate_beta,
-                                          value_beta, residual != 0, nullptr, nullptr, (uint16_t*)out_dev, ctx->s, st);
+  hipError_t e = rmoe::launch_moe_prefill(*L, (const uint16_t*)x_dev, T, nullptr, nullptr, ids, wts, nullptr, act,
+                                          gate_beta, value_beta, residual != 0, (uint16_t*)out_dev, nullptr, nullptr,
+                                          ctx->s.pf, ctx->s.pf_bytes, ctx->s, st);
   if (e == hipErrorInvalidValue) return fail(RMOE_EINVAL, "scratch too small for T=%d: call rmoe_reserve", T);
   HIP_TRY(e);
   return RMOE_OK;

@@ -212,6 +212,8 @@ struct RmoeScratch {
   int32_t* chunk_counts = nullptr;
   size_t order_elems = 0, offset_elems = 0, chunk_elems = 0;
   int* err = nullptr;            // device error flag
+  uint8_t* pf = nullptr;         // prefill working set (h, D, group sums, tiles)
+  size_t pf_bytes = 0;
   uint8_t* staging = nullptr;    // upload staging
   size_t staging_bytes = 0;
   int max_tokens = 0;
@@ -253,10 +255,18 @@ hipError_t launch_moe_decode(const RmoeLayer& L, const uint16_t* x, const int32_
 hipError_t launch_dispatch(const int32_t* ids, int T, int k, int n_experts, int32_t* order, int32_t* inv,
                            int32_t* offsets, RmoeScratch& s, hipStream_t st);
 
-hipError_t launch_moe_grouped(const RmoeLayer& L, const uint16_t* x, int T, const int32_t* ids, const float* wts,
-                              const uint16_t* shared_gu, bool shared_from_x, int act, float gb, float vb,
-                              bool residual, uint16_t* routed, uint16_t* shared_down, uint16_t* out,
-                              RmoeScratch& s, hipStream_t st);
+// Prefill MoE (moe_prefill.hip).  With ids_in == nullptr the router runs on the device
+// and writes ids_out/wts_out; otherwise ids_in/wts_in are used.  With shared_gu the
+// shared expert's gate/up is taken from it, otherwise computed from x.  Any of out /
+// routed / shared_down may be null.  scratch: prefill_scratch_bytes(L, T) bytes.
+size_t prefill_scratch_bytes(const RmoeLayer& L, int T);
+hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, const int32_t* ids_in, const float* wts_in,
+                              int32_t* ids_out, float* wts_out, const uint16_t* shared_gu, int act, float gb, float vb,
+                              bool residual, uint16_t* out, uint16_t* routed, uint16_t* shared_down, uint8_t* scratch,
+                              size_t scratch_bytes, RmoeScratch& s, hipStream_t st);
+hipError_t launch_router_gemm(const uint16_t* x, int T, int H, const uint16_t* w, int E, float* logits, hipStream_t st);
+hipError_t launch_topk(const float* logits, int T, int E, int k, int score, const float* bias, int renorm,
+                       float scaling, int32_t* ids, float* wts, hipStream_t st);
 
 // Scratch requirements (bytes) for the launch wrappers above.
 size_t decode_scratch_floats(const RmoeLayer& L);

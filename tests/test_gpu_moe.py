@@ -31,6 +31,18 @@ def _check(out, ref, label, same_min=0.95):
     assert err <= TOL_ABS and rel <= TOL_REL and same >= same_min, (label, err, rel, same)
 
 
+def _check_ulp(out, ref, label):
+    """Residual-stream values reach |x| >= 2, where one bf16 ulp (0.0156) exceeds the 1e-2
+    max-abs bar; there the bound is two ulps of the reference value, with rel-L2 <= 1e-3."""
+    a = bf16_to_f32(out).astype(np.float64)
+    b = bf16_to_f32(ref).astype(np.float64)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(b), 1e-30))) - 7)
+    bound = np.maximum(TOL_ABS, 2 * ulp)
+    rel = np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30)
+    print(f"{label}: max |d|/bound {np.max(np.abs(a - b) / bound):.3f} rel-L2 {rel:.3e} bit-identical {np.mean(out == ref):.4f}")
+    assert np.all(np.abs(a - b) <= bound) and rel <= TOL_REL
+
+
 @pytest.fixture(scope="module")
 def baseline(gpu_ctx):
     """BASELINE geometry (H=2048, I=768, 128 routed + 1 shared, top-8), weights N(0, 0.02)
@@ -115,9 +127,9 @@ def test_decode_layer_matches_oracle(baseline):
         if routing_margin(x, spec) > MARGIN:
             assert ids.tolist() == top.tolist()
         _check(out, ref, f"decode[{t}]")
+        # The residual add is elementwise: bit-exact against the GPU's own MoE output.
         out_r, _, _ = lyr.moe_decode(x, residual=True)
-        ref_r = f32_to_bf16(bf16_to_f32(x) + bf16_to_f32(ref))
-        _check(out_r, ref_r, f"decode+residual[{t}]", same_min=0.97)
+        np.testing.assert_array_equal(out_r, f32_to_bf16(bf16_to_f32(x) + bf16_to_f32(out)))
 
 
 def test_dispatch_matches_planner(gpu_ctx):
@@ -173,6 +185,55 @@ def test_prefill_layer_matches_oracle(baseline):
     _check(out.cpu().numpy().view(np.uint16), ref, "prefill layer")
 
 
+def test_prefill_config3_matches_oracle(baseline):
+    """one prefill layer of 445 tokens (~28 tokens per expert)."""
+    import torch
+
+    geom, lyr, bank, spec = baseline
+    T = 445
+    xs = random_tokens(T, geom.hidden, 610)
+    xd = torch.from_numpy(xs.view(np.int16)).cuda()
+    out = torch.empty_like(xd)
+    ids = torch.empty((T, geom.top_k), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, geom.top_k), dtype=torch.float32, device="cuda")
+    out_r = torch.empty_like(xd)
+    stream = torch.cuda.current_stream()
+    lyr.moe_prefill_dev(xd, T, out, residual=False, ids_dev=ids, wts_dev=wts, stream=stream)
+    lyr.moe_prefill_dev(xd, T, out_r, residual=True, stream=stream)
+    torch.cuda.synchronize()
+    ref, top, rw = om.prefill_layer(bank, spec, xs, geom.shared_id, None, None, batched=True)
+    got = ids.cpu().numpy()
+    flips = [t for t in range(T) if got[t].tolist() != top[t].tolist()]
+    assert all(routing_margin(xs[t], spec) <= MARGIN for t in flips), flips
+    ok = np.array([t not in flips for t in range(T)])
+    o = out.cpu().numpy().view(np.uint16)
+    _check(o[ok], ref[ok], "prefill 445")
+    # residual add: elementwise, bit-exact against the GPU's own MoE output
+    np.testing.assert_array_equal(out_r.cpu().numpy().view(np.uint16), f32_to_bf16(bf16_to_f32(xs) + bf16_to_f32(o)))
+
+
+def test_grouped_skewed_routing(baseline):
+    """Load-imbalanced groups (hot expert with every token, cold experts with 1-2) and
+    ragged tails: grouped routed sums and shared rows vs the token-serial oracle."""
+    geom, lyr, bank, _ = baseline
+    T = 300
+    xs = random_tokens(T, geom.hidden, 620)
+    rng = np.random.default_rng(621)
+    ids = np.zeros((T, geom.top_k), np.int64)
+    warm = np.array([1, 2, 3, 4, 6, 7, 8, 9, 10, 11])
+    for t in range(T):
+        pool = warm if t % 3 else np.arange(12, 127)
+        rest = rng.choice(pool, geom.top_k - 2, replace=False)
+        ids[t] = np.concatenate([[0, 127 if t == T - 1 else 5], rest])  # expert 127: one token
+        assert len(set(ids[t].tolist())) == geom.top_k
+    w = rng.random((T, geom.top_k), dtype=np.float32)
+    sgu = np.stack([om.shared_gate_up(bank, geom.shared_id, x) for x in xs])
+    routed, sdown = lyr.moe_experts_grouped(xs, ids, w, sgu, None, None)
+    r_ref, s_ref = om.moe_experts_grouped_batched(bank, xs, ids, w, sgu, geom.shared_id, None, None)
+    _check(routed, r_ref, "skewed routed")
+    _check(sdown, s_ref, "skewed shared_down")
+
+
 def test_decode_graph_replays_match_eager(baseline):
     import torch
 
@@ -221,6 +282,6 @@ def test_residual_stack_matches_oracle(gpu_ctx):
             h = nxt
         torch.cuda.synchronize()
         ref = om.residual_stack(oracle_layers, x)
-        _check(h.cpu().numpy().view(np.uint16), ref, "stack", same_min=0.9)
+        _check_ulp(h.cpu().numpy().view(np.uint16), ref, "stack")
     for lyr in layers:
         lyr.free()
