@@ -42,6 +42,10 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the oracle CPU sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--prefill-tokens", type=int, default=6700)
+    ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--zipf-tau", type=float, default=0.02)
+    ap.add_argument("--no-prefill", action="store_true")
     return ap.parse_args()
 
 
@@ -113,6 +117,48 @@ def gate_up_roofline(layers, geom, x, stream, reps: int = 20):
     per_launch = secs / (reps * len(layers))
     nbytes = (geom.top_k + 1) * geom.gu_bytes + geom.hidden * 2
     return per_launch, nbytes
+
+
+def zipf_bias(n: int, tau: float, seed: int):
+    """Selection bias b_e = tau * log p_e with p_e proportional to rank_e^-1.1 (seeded ranks)."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    ranks = rng.permutation(n) + 1
+    p = ranks.astype(np.float64) ** -1.1
+    p /= p.sum()
+    return (tau * np.log(p)).astype(np.float32)
+
+
+def prefill_bench(ctx, geom, T: int, seed: int, reps: int, tau: float, stream):
+    """one MoE layer prefill of T tokens with Zipf(1.1) expert popularity.
+    Returns (seconds per layer, FLOPs per layer, expert histogram)."""
+    import numpy as np
+    import torch
+
+    lyr = ctx.create_layer(1000, geom)
+    lyr.synthesize(seed * 1000 + 999, 0.02)
+    gen = torch.Generator(device="cuda").manual_seed(seed * 1000 + 999)
+    rw = (torch.randn(geom.n_routed, geom.hidden, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+    lyr.set_router(rw.contiguous(), bias=zipf_bias(geom.n_routed, tau, seed), score="softmax")
+    lyr.reserve(T)
+    x = torch.randn(T, geom.hidden, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
+    out = torch.empty_like(x)
+    ids = torch.empty((T, geom.top_k), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, geom.top_k), dtype=torch.float32, device="cuda")
+    with torch.cuda.stream(stream):
+        lyr.moe_prefill_dev(x, T, out, ids_dev=ids, wts_dev=wts, stream=stream)
+    torch.cuda.synchronize()
+    hist = np.bincount(ids.cpu().numpy().reshape(-1), minlength=geom.n_routed)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g, stream=stream):
+            lyr.moe_prefill_dev(x, T, out, ids_dev=ids, wts_dev=wts, stream=stream)
+        g.replay()
+    secs = time_graph(g, reps, stream) / reps
+    flops = T * (geom.top_k + 1) * geom.flops_per_assignment + 2 * T * geom.hidden * geom.n_routed
+    lyr.free()
+    return secs, flops, hist
 
 
 def cpu_baseline(lyr, geom, budget_s: float, seed: int):
@@ -194,6 +240,25 @@ def main() -> int:
     achieved = nbytes / per_launch / 1e9
     log(f"gate/up kernel: {per_launch * 1e6:.2f} us/launch, {achieved:.1f} GB/s")
 
+    prefill = None
+    if not args.no_prefill:
+        psec, pflops, hist = prefill_bench(ctx, geom, args.prefill_tokens, args.seed, args.prefill_reps, args.zipf_tau,
+                                           stream)
+        tflops = pflops / psec / 1e12
+        prefill = {
+            "workload": f"BASELINE config 5: {args.prefill_tokens} tokens, Zipf(1.1) routing (selection bias tau={args.zipf_tau})",
+            "ms_per_layer": round(psec * 1e3, 4),
+            "flops_per_layer": pflops,
+            "tflops": round(tflops, 2),
+            "frac_bf16_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "expert_tokens_max": int(hist.max()),
+            "expert_tokens_min": int(hist.min()),
+            "experts_over_1000": int((hist > 1000).sum()),
+            "experts_under_10": int((hist < 10).sum()),
+        }
+        log(f"prefill {args.prefill_tokens} tokens: {psec * 1e3:.3f} ms/layer, {tflops:.1f} TFLOP/s "
+            f"(hist max {hist.max()} min {hist.min()})")
+
     cpu = None
     if not args.no_cpu:
         per_layer, n, threads = cpu_baseline(layers[0], geom, args.cpu_seconds, args.seed)
@@ -209,7 +274,7 @@ def main() -> int:
         log(f"cpu baseline: {cpu['value']} tok/s ({per_layer * 1e3:.1f} ms/token-layer, {threads} BLAS threads)")
 
     line = {
-        "metric": "MoE decode tokens/s (48-layer q4nx stack, batch 1)",
+        "metric": "MoE decode tokens/s (48-layer q4nx stack, batch 1); prefill grouped-GEMM TFLOP/s in 'prefill'",
         "value": round(tok_s, 2),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -245,6 +310,7 @@ def main() -> int:
             "us_per_launch": round(per_launch * 1e6, 3),
         },
         "cpu_baseline": cpu,
+        "prefill": prefill,
     }
     print(json.dumps(line), flush=True)
     ctx.close()

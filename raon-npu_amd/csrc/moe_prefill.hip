@@ -42,40 +42,59 @@ __device__ __forceinline__ void store_split3(uint32_t* dst, float v) {
 
 // ---------------------------------------------------------------- router GEMM --
 // logits[T, E] = x[T, H] . Wr[E, H]^T on MFMA (exact bf16 products, fp32 sums).
-// Block: 4 waves, 64 tokens; wave w: tokens 16w..16w+15 x all experts (E/16 n-frags).
+// Block: 4 waves x 64 tokens; a 64-column chunk of Wr for all experts is staged in LDS
+// and shared by the 4 waves; A fragments come straight from the token rows.
 constexpr int kMaxEFrags = 16;  // E <= 256
+constexpr int kRouterChunk = 64;
+constexpr int kRouterStride = kRouterChunk + 8;  // bf16 per LDS row (16-byte pad)
 
+template <int NFR>
 __global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __restrict__ x, int T, int H,
                                                           const uint16_t* __restrict__ w, int E,
                                                           float* __restrict__ logits) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int t0 = blockIdx.x * 64 + wave * 16;
-  const int nfr = E / 16;
-  f32x4_t acc[kMaxEFrags];
+  __shared__ __attribute__((aligned(16))) uint16_t ws[256 * kRouterStride];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, lq = lane >> 4;
+  const int t0 = blockIdx.x * 256 + wave * 64;
+  f32x4_t acc[4][NFR];
 #pragma unroll
-  for (int f = 0; f < kMaxEFrags; ++f) acc[f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const int tok = min(t0 + (lane & 15), T - 1);
-  const uint16_t* xr = x + (size_t)tok * H + 8 * (lane >> 4);
-  for (int k0 = 0; k0 < H; k0 += 32) {
-    const uint4 a = *reinterpret_cast<const uint4*>(xr + k0);
+  for (int m = 0; m < 4; ++m)
 #pragma unroll
-    for (int f = 0; f < kMaxEFrags; ++f) {
-      if (f < nfr) {
-        const uint4 b = *reinterpret_cast<const uint4*>(w + (size_t)(16 * f + (lane & 15)) * H + k0 + 8 * (lane >> 4));
-        acc[f] = mfma16(a, b, acc[f]);
+    for (int f = 0; f < NFR; ++f) acc[m][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const uint16_t* xr[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) xr[m] = x + (size_t)min(t0 + 16 * m + l16, T - 1) * H + 8 * lq;
+  for (int k0 = 0; k0 < H; k0 += kRouterChunk) {
+    __syncthreads();
+    for (int i = tid; i < E * (kRouterChunk / 8); i += 256) {
+      const int e = i / (kRouterChunk / 8), c = i % (kRouterChunk / 8);
+      *reinterpret_cast<uint4*>(&ws[e * kRouterStride + 8 * c]) =
+          *reinterpret_cast<const uint4*>(w + (size_t)e * H + k0 + 8 * c);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < kRouterChunk; kk += 32) {
+      uint4 a[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) a[m] = *reinterpret_cast<const uint4*>(xr[m] + k0 + kk);
+#pragma unroll
+      for (int f = 0; f < NFR; ++f) {
+        const uint4 b = *reinterpret_cast<const uint4*>(&ws[(16 * f + l16) * kRouterStride + kk + 8 * lq]);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) acc[m][f] = mfma16(a[m], b, acc[m][f]);
       }
     }
   }
 #pragma unroll
-  for (int f = 0; f < kMaxEFrags; ++f) {
-    if (f < nfr) {
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int f = 0; f < NFR; ++f) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int t = t0 + 4 * (lane >> 4) + i;
-        if (t < T) logits[(size_t)t * E + 16 * f + (lane & 15)] = acc[f][i];
+        const int t = t0 + 16 * m + 4 * lq + i;
+        if (t < T) logits[(size_t)t * E + 16 * f + l16] = acc[m][f][i];
       }
     }
-  }
 }
 
 // numpy float32 sum order (pairwise_sum, n <= 128 per block of 8 partial sums).
@@ -191,17 +210,30 @@ __global__ void group_sums_kernel(const uint16_t* __restrict__ src, int rows, in
 // count is written to *ntiles.
 constexpr int kBM = 128;
 
-__global__ void tile_table_kernel(const int32_t* __restrict__ offsets, int n_routed, int shared_rows,
-                                  uint32_t* __restrict__ tiles, int* __restrict__ ntiles, int cap) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  int n = 0;
+// One workgroup of 512 threads; thread e owns group e (routed 0..n_routed-1, shared n_routed).
+__global__ __launch_bounds__(512) void tile_table_kernel(const int32_t* __restrict__ offsets, int n_routed,
+                                                         int shared_rows, uint32_t* __restrict__ tiles,
+                                                         int* __restrict__ ntiles, int cap) {
+  __shared__ int base[513];
+  const int e = threadIdx.x;
   const int ng = n_routed + (shared_rows > 0 ? 1 : 0);
-  for (int e = 0; e < ng; ++e) {
-    const int b = offsets[min(e, n_routed)];
-    const int end = e < n_routed ? offsets[e + 1] : b + shared_rows;
-    for (int r = b; r < end && n < cap; r += kBM) tiles[n++] = (uint32_t)e | ((uint32_t)r << 9);
+  int b = 0, end = 0, nt = 0;
+  if (e < ng) {
+    b = offsets[min(e, n_routed)];
+    end = e < n_routed ? offsets[e + 1] : b + shared_rows;
+    nt = (end - b + kBM - 1) / kBM;
   }
-  *ntiles = n;
+  base[e + 1] = nt;
+  if (e == 0) base[0] = 0;
+  __syncthreads();
+  if (e == 0)
+    for (int q = 1; q <= ng; ++q) base[q] += base[q - 1];
+  __syncthreads();
+  for (int i = 0; i < nt; ++i) {
+    const int slot = base[e] + i;
+    if (slot < cap) tiles[slot] = (uint32_t)e | ((uint32_t)(b + i * kBM) << 9);
+  }
+  if (e == 0) *ntiles = min(base[ng], cap);
 }
 
 // ------------------------------------------------------------- grouped GEMM --
@@ -213,7 +245,7 @@ struct GemmArgs {
   int N_total;       // weight rows (gate/up: 2I; down: H)
   int inter;         // gate/up: I (the up rows start at I)
   int mode;          // 0: gate/up + activation -> h; 1: down -> D
-  int n_tiles;       // WG N-tiles (gate/up: I/64; down: N_total/128)
+  int n_tiles;       // WG N-tiles (gate/up: ceil(I/128) units of 128; down: N_total/256 rows of 256)
   // activation rows
   const uint16_t* src;      // mode 0: x [T, K] gathered by token; mode 1: h [rows, K] in sorted order
   const int32_t* order;     // mode 0: sorted position -> assignment (token*k + route)
@@ -252,16 +284,21 @@ __device__ __forceinline__ const uint32_t* ssum_row(const GemmArgs& a, int e, in
   return a.ssum + (size_t)tok * G * 2;
 }
 
-// Grid: n_tiles * tile_cap workgroups (rounded to a multiple of 8), 256 threads.
-__global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a, int tile_cap) {
+// Grid: n_tiles * tile_cap workgroups (rounded to a multiple of 8), 512 threads (8 waves).
+// A workgroup multiplies 128 sorted rows by 256 weight rows: gate/up mode takes 128
+// intermediate units (gate rows + the matching up rows), wave w units 128*nt + 16w..+15;
+// down mode takes 256 output rows, wave w rows 256*nt + 16w and 256*nt + 128 + 16w.
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void grouped_gemm_kernel(GemmArgs a, int tile_cap) {
   __shared__ __attribute__((aligned(16))) uint16_t xs[2][kBM * kXStride];
-  __shared__ float hsum[4][kBM][2];
+  __shared__ float hsum[8][kBM];
   // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs; make each XCD
   // take a contiguous range of (n-tile, m-tile) so m-tiles sharing a weight tile meet
   // in the same L2.
   const int nb = gridDim.x, per = nb / 8;
   const int lid = (blockIdx.x % 8) * per + blockIdx.x / 8;
-  const int nt = lid / tile_cap, mt = lid % tile_cap;
+  // m-tile major: the n-tiles of one m-tile (sharing the gathered rows) and consecutive
+  // m-tiles of one expert (sharing its weights) run back to back on one XCD.
+  const int mt = lid / a.n_tiles, nt = lid % a.n_tiles;
   if (nt >= a.n_tiles || mt >= *a.ntiles) return;
   const uint32_t te = a.tiles[mt];
   const int e = (int)(te & 511u), row0 = (int)(te >> 9);
@@ -274,23 +311,56 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a, int tile_
   // The wave's two n-fragments: rows within the weight matrix.
   int wrow[2];
   if (a.mode == 0) {
-    wrow[0] = 64 * nt + 16 * wave;            // gate
-    wrow[1] = a.inter + 64 * nt + 16 * wave;  // up
+    wrow[0] = 128 * nt + 16 * wave;            // gate
+    wrow[1] = a.inter + 128 * nt + 16 * wave;  // up
   } else {
-    wrow[0] = 128 * nt + 16 * wave;
-    wrow[1] = 128 * nt + 64 + 16 * wave;
+    wrow[0] = 256 * nt + 16 * wave;
+    wrow[1] = 256 * nt + 128 + 16 * wave;
+  }
+  // Gate/up: when I is not a multiple of 128 the last n-tile has waves past I; they
+  // read valid rows (unit 0) and store nothing.
+  const bool active = a.mode == 1 || 128 * nt + 16 * wave < a.inter;
+  if (!active) {
+    wrow[0] = 0;
+    wrow[1] = a.inter;
   }
 
-  // Per-thread source rows for the X staging: thread loads 16 B pieces.
-  // A tile step is 128 rows x 128 k = 128 rows x 16 pieces; 256 threads -> 8 pieces each.
-  auto stage = [&](int buf, int kt) {
+  // X staging: a K step is 128 rows x 128 columns = 2,048 16-byte pieces, 8 per thread.
+  // Global loads for step kt+1 go to registers at the top of step kt and are written
+  // to the other LDS buffer after the MFMA work, so their latency hides behind it.
+  int xoff[4];  // element offset of the thread's piece in a.src, or -1 past the group
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int piece = tid + 256 * q;
-      const int r = piece >> 4, c = piece & 15;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (r < nrows) v = *reinterpret_cast<const uint4*>(src_row(a, e, row0 + r) + kt * 128 + 8 * c);
-      *reinterpret_cast<uint4*>(&xs[buf][r * kXStride + 8 * c]) = v;
+  for (int q = 0; q < 4; ++q) {
+    const int r = (tid + 512 * q) >> 4;
+    xoff[q] = r < nrows ? (int)(src_row(a, e, row0 + r) - a.src) + 8 * ((tid + 512 * q) & 15) : -1;
+  }
+  auto load_x = [&](uint4 (&v)[4], int kt) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      v[q] = xoff[q] >= 0 ? *reinterpret_cast<const uint4*>(a.src + xoff[q] + kt * 128) : make_uint4(0u, 0u, 0u, 0u);
+  };
+  auto store_x = [&](const uint4 (&v)[4], int buf) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int piece = tid + 512 * q;
+      *reinterpret_cast<uint4*>(&xs[buf][(piece >> 4) * kXStride + 8 * (piece & 15)]) = v[q];
+    }
+  };
+  // Weight fragments of one K tile for the wave's two n-fragments (codes + scale/min).
+  const uint8_t* wtile[2];
+  int r_in[2];
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    wtile[f] = W + (size_t)(wrow[f] / 64) * nkt * kTileBytes;
+    r_in[f] = wrow[f] % 64 + l16;
+  }
+  auto load_w = [&](uint32_t (&code)[2][4], uint4 (&smv)[2], int kt) {
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const uint8_t* tile = wtile[f] + (size_t)kt * kTileBytes;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) code[f][j] = *reinterpret_cast<const uint32_t*>(tile + j * 1024 + r_in[f] * 16 + 4 * lq);
+      smv[f] = *reinterpret_cast<const uint4*>(tile + kCodeBytes + r_in[f] * 16);
     }
   };
 
@@ -302,23 +372,21 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a, int tile_
   }
   const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
 
-  stage(0, 0);
+  uint4 xv[4];
+  uint32_t code[2][4], code_n[2][4];
+  uint4 smv[2], smv_n[2];
+  load_x(xv, 0);
+  load_w(code, smv, 0);
+  store_x(xv, 0);
   __syncthreads();
   for (int kt = 0; kt < nkt; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < nkt) stage(cur ^ 1, kt + 1);
-    // Weight fragments of this K tile for the wave's two n-fragments.
-    uint32_t code[2][4];
-    uint4 smv[2];
-#pragma unroll
-    for (int f = 0; f < 2; ++f) {
-      const int rt = wrow[f] / 64, r_in = wrow[f] % 64 + l16;
-      const uint8_t* tile = W + ((size_t)rt * nkt + kt) * kTileBytes;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) code[f][j] = *reinterpret_cast<const uint32_t*>(tile + j * 1024 + r_in * 16 + 4 * lq);
-      smv[f] = *reinterpret_cast<const uint4*>(tile + kCodeBytes + r_in * 16);
+    const bool more = kt + 1 < nkt;
+    if (more) {
+      load_x(xv, kt + 1);
+      load_w(code_n, smv_n, kt + 1);
     }
-#pragma unroll
+#pragma unroll 1  // one group at a time keeps 16 MFMA results live, not 64
     for (int j = 0; j < 4; ++j) {
       uint4 b[2];
       float s16[2];
@@ -341,6 +409,15 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a, int tile_
         }
       }
     }
+    if (more) {
+      store_x(xv, cur ^ 1);
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        smv[f] = smv_n[f];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) code[f][j] = code_n[f][j];
+      }
+    }
     __syncthreads();
   }
 
@@ -360,9 +437,8 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a, int tile_
         const int g = g0 + 8 * lq + i;
         float coef = 0.f;
         if (g < G) {
-          const int rt = wrow[f] / 64, r_in = wrow[f] % 64 + l16;
-          const uint8_t* tile = W + ((size_t)rt * nkt + g / 4) * kTileBytes;
-          const uint32_t smw = *reinterpret_cast<const uint32_t*>(tile + kCodeBytes + r_in * 16 + 4 * (g % 4));
+          const uint8_t* tile = wtile[f] + (size_t)(g / 4) * kTileBytes;
+          const uint32_t smw = *reinterpret_cast<const uint32_t*>(tile + kCodeBytes + r_in[f] * 16 + 4 * (g % 4));
           const float sc = bf16_to_f32(smw & 0xffffu), mn = bf16_to_f32(smw >> 16);
           coef = mn - 16.f * sc;
         }
@@ -374,6 +450,9 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a, int tile_
     }
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
+      // Keep each iteration's loads next to its MFMAs: hoisting all of them exhausts
+      // the register file.
+      __builtin_amdgcn_sched_barrier(0);
       const int r = 16 * m + l16;
       uint32_t sh[8], sm2[8], sl[8];
       const uint32_t* sp = r < nrows ? ssum_row(a, e, row0 + r) : nullptr;
@@ -406,7 +485,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a, int tile_
 
   // Epilogue.  C layout: lane holds rows 16m + 4*lq + i, column l16 of the fragment.
   if (a.mode == 0) {
-    const int col = 64 * nt + 16 * wave + l16;  // intermediate unit
+    const int col = 128 * nt + 16 * wave + l16;  // intermediate unit
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
 #pragma unroll
@@ -414,21 +493,21 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a, int tile_
         const int r = 16 * m + 4 * lq + i;
         const float g = bf16_round(acc[m][0][i]), u = bf16_round(acc[m][1][i]);
         const uint32_t h = f32_to_bf16(act_apply(a.act, g, u, a.gb, a.vb));
-        if (r < nrows) a.out[(size_t)(row0 + r) * a.out_ld + col] = (uint16_t)h;
+        if (active && r < nrows) a.out[(size_t)(row0 + r) * a.out_ld + col] = (uint16_t)h;
         // Group sums of h: reduce the 16 columns of this wave, then 2 waves per group.
         float hv = r < nrows ? bf16_to_f32(h) : 0.f;
 #pragma unroll
         for (int off = 8; off > 0; off >>= 1) hv += __shfl_xor(hv, off, 16);
-        if (l16 == 0) hsum[wave][r][0] = hv;
+        if (l16 == 0) hsum[wave][r] = hv;
       }
     }
     __syncthreads();
     // Group (32 columns) = waves {0,1} and {2,3}; 64*nt + 32*q is group 2*nt + q.
-    for (int idx = tid; idx < kBM * 2; idx += 256) {
-      const int r = idx >> 1, q = idx & 1;
-      if (r < nrows) {
-        const float s = hsum[2 * q][r][0] + hsum[2 * q + 1][r][0];
-        store_split3(a.out_ssum + ((size_t)(row0 + r) * (a.out_ld / 32) + 2 * nt + q) * 2, s);
+    for (int idx = tid; idx < kBM * 4; idx += 512) {
+      const int r = idx >> 2, q = idx & 3;  // group 4*nt + q = waves 2q, 2q+1
+      if (r < nrows && 128 * nt + 32 * q < a.inter) {
+        const float s = hsum[2 * q][r] + hsum[2 * q + 1][r];
+        store_split3(a.out_ssum + ((size_t)(row0 + r) * (a.out_ld / 32) + 4 * nt + q) * 2, s);
       }
     }
   } else {
@@ -531,7 +610,21 @@ __global__ void shared_act_kernel(const uint16_t* __restrict__ gu, int T, int I,
 // ------------------------------------------------------------------ launchers --
 hipError_t launch_router_gemm(const uint16_t* x, int T, int H, const uint16_t* w, int E, float* logits, hipStream_t st) {
   if (E % 16 || E > 16 * kMaxEFrags || H % 32) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(router_gemm_kernel, dim3((T + 63) / 64), dim3(256), 0, st, x, T, H, w, E, logits);
+  if (H % kRouterChunk) return hipErrorInvalidValue;
+  const dim3 grid((T + 255) / 256), block(256);
+  switch (E / 16) {
+#define RMOE_ROUTER_CASE(n) \
+  case n:                   \
+    hipLaunchKernelGGL(router_gemm_kernel<n>, grid, block, 0, st, x, T, H, w, E, logits); \
+    break;
+    RMOE_ROUTER_CASE(1) RMOE_ROUTER_CASE(2) RMOE_ROUTER_CASE(3) RMOE_ROUTER_CASE(4) RMOE_ROUTER_CASE(5)
+    RMOE_ROUTER_CASE(6) RMOE_ROUTER_CASE(7) RMOE_ROUTER_CASE(8) RMOE_ROUTER_CASE(9) RMOE_ROUTER_CASE(10)
+    RMOE_ROUTER_CASE(11) RMOE_ROUTER_CASE(12) RMOE_ROUTER_CASE(13) RMOE_ROUTER_CASE(14) RMOE_ROUTER_CASE(15)
+    RMOE_ROUTER_CASE(16)
+#undef RMOE_ROUTER_CASE
+    default:
+      return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
@@ -608,7 +701,7 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   g.N_total = 2 * L.I;
   g.inter = L.I;
   g.mode = 0;
-  g.n_tiles = L.I / 64;
+  g.n_tiles = (L.I + 127) / 128;
   g.src = x;
   g.order = s.order;
   g.k_routes = k;
@@ -625,7 +718,7 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   g.act = act;
   g.gb = gb;
   g.vb = vb;
-  hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(64), 0, st, s.offsets, E, g.shared_rows, tiles, ntiles, tile_cap);
+  hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(512), 0, st, s.offsets, E, g.shared_rows, tiles, ntiles, tile_cap);
   if ((err = hipGetLastError()) != hipSuccess) return err;
   if (shared_gu) {
     const size_t n = (size_t)T * (L.Ipad / 32);
@@ -635,12 +728,12 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   }
   {
     const int blocks = (g.n_tiles * tile_cap + 7) / 8 * 8;  // the XCD mapping needs a multiple of 8
-    hipLaunchKernelGGL(grouped_gemm_kernel, dim3(blocks), dim3(256), 0, st, g, tile_cap);
+    hipLaunchKernelGGL(grouped_gemm_kernel, dim3(blocks), dim3(512), 0, st, g, tile_cap);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
   // Down: every sorted row (routed + shared), rows of h contiguous.
   if (shared_gu) {
-    hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(64), 0, st, s.offsets, E, T, tiles, ntiles, tile_cap);
+    hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(512), 0, st, s.offsets, E, T, tiles, ntiles, tile_cap);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
   GemmArgs d = g;
@@ -649,7 +742,7 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   d.K = L.Ipad;
   d.N_total = L.H;
   d.mode = 1;
-  d.n_tiles = L.H / 128;
+  d.n_tiles = L.H / 256;
   d.src = h;
   d.ssum = hsum;
   d.shared_rows = T;
@@ -658,7 +751,7 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   d.out_ssum = nullptr;
   {
     const int blocks = (d.n_tiles * tile_cap + 7) / 8 * 8;
-    hipLaunchKernelGGL(grouped_gemm_kernel, dim3(blocks), dim3(256), 0, st, d, tile_cap);
+    hipLaunchKernelGGL(grouped_gemm_kernel, dim3(blocks), dim3(512), 0, st, d, tile_cap);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
   hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, st, D, L.H, ids, wts, s.inv, k, (int)A,

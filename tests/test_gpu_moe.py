@@ -234,6 +234,46 @@ def test_grouped_skewed_routing(baseline):
     _check(sdown, s_ref, "skewed shared_down")
 
 
+def test_reference_model_shape(gpu_ctx):
+    """The reference model's shape (host/raon.py:127-142; kernels/moe/pack.py:46-69):
+    H=2560, I=1088 (down input padded to 1280), top-6, sigmoid router with selection bias
+    and scaling, SiTU-GLU -- here with 16 routed experts + the shared expert."""
+    import torch
+
+    geom = G.MoeGeometry(hidden=2560, inter=1088, n_routed=16, n_shared=1, top_k=6)
+    syn = make_layer(geom, seed=930, score="sigmoid",
+                     bias=(np.random.default_rng(931).standard_normal(16) * 0.01).astype(np.float32))
+    lyr = gpu_ctx.create_layer(930, geom)
+    lyr.upload_experts(syn.gate_up, syn.down)
+    lyr.set_router(syn.router, bias=syn.bias, score="sigmoid", scaling=2.5)
+    spec = om.RouterSpec(syn.router, geom.top_k, score="sigmoid", bias=syn.bias, scaling=2.5)
+    bank = syn.bank()
+    lyr.reserve(64)
+    xs = random_tokens(40, geom.hidden, 932)
+    # decode (one token at a time), router on the device
+    for t in range(3):
+        out, ids, w = lyr.moe_decode(xs[t], gate_beta=4.0, value_beta=25.0)
+        ref, top, rw, _ = om.moe_token(bank, spec, xs[t], 4.0, 25.0, shared_id=geom.shared_id)
+        if routing_margin(xs[t], spec) > MARGIN:
+            assert ids.tolist() == top.tolist()
+        _check(out, ref, f"raon-shape decode[{t}]")
+    # prefill of 40 tokens
+    xd = torch.from_numpy(xs.view(np.int16)).cuda()
+    out = torch.empty_like(xd)
+    ids = torch.empty((40, geom.top_k), dtype=torch.int32, device="cuda")
+    wts = torch.empty((40, geom.top_k), dtype=torch.float32, device="cuda")
+    lyr.moe_prefill_dev(xd, 40, out, gate_beta=4.0, value_beta=25.0, ids_dev=ids, wts_dev=wts,
+                        stream=torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    ref, top, _ = om.prefill_layer(bank, spec, xs, geom.shared_id, 4.0, 25.0, batched=True)
+    got = ids.cpu().numpy()
+    ok = np.array([got[t].tolist() == top[t].tolist() or routing_margin(xs[t], spec) <= MARGIN for t in range(40)])
+    assert ok.all()
+    same = np.array([got[t].tolist() == top[t].tolist() for t in range(40)])
+    _check(out.cpu().numpy().view(np.uint16)[same], ref[same], "raon-shape prefill")
+    lyr.free()
+
+
 def test_decode_graph_replays_match_eager(baseline):
     import torch
 
