@@ -4,13 +4,15 @@
 Default workload: 48 stacked MoE layers of the BASELINE
 shape (H=2048, I=768, 128 routed experts + 1 shared, softmax top-8, SwiGLU, q4nx
 weights N(0, 0.02)), residual add between layers, batch 1.  One step = one token
-through all 48 layers (router on the device, 8 routed + shared experts, ordered
-fp32 combine).  Weights are synthesized and quantized on the GPU (seeded per
-layer); inputs are random N(0, 1) hidden states, one per step, resident in HBM.
+through all 48 layers in ONE persistent launch (router on the device, 8 routed +
+shared experts, ordered fp32 combine, residual).  Weights are synthesized and
+quantized on the GPU (seeded per layer); inputs are random N(0, 1) hidden states,
+one per step, resident in HBM.
 
 Printed: one JSON line with tokens/s, the roofline of the dominant kernel (the
-decode gate/up expert GEMV), and the NumPy oracle (the reference CPU path) timed
-on a bounded sample on this host.
+persistent decode kernel: 48 x 27,066,368 algorithmic bytes per launch), the
+prefill grouped GEMM (config 5) and the NumPy oracle (the reference CPU path)
+timed on a bounded sample on this host.
 """
 
 from __future__ import annotations
@@ -64,59 +66,35 @@ def build_stack(ctx, geom, n_layers: int, seed: int):
     return layers
 
 
-def decode_graph(layers, geom, x_pool, cursor, bufs, stream):
-    """One decode step: fetch the next input from the pool, 48 layers with residual."""
+def decode_graph(ctx, layers, x_pool, out_pool, stream, n_launch: int):
+    """A HIP graph of n_launch decode steps: step i carries token x_pool[i] through every
+    layer in ONE persistent launch and writes out_pool[i]."""
     import torch
-
-    def step():
-        torch.index_select(x_pool, 0, cursor, out=bufs[0].view(1, -1))
-        cursor.add_(1).remainder_(x_pool.shape[0])
-        for li, lyr in enumerate(layers):
-            lyr.moe_decode_dev(bufs[li % 2], bufs[(li + 1) % 2], residual=True, stream=stream)
 
     g = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
-        step()  # warm the allocator / kernels outside capture
+        ctx.decode_stack_dev(layers, x_pool[0], out_pool[0], residual=True, stream=stream)  # warm
         torch.cuda.synchronize()
         with torch.cuda.graph(g, stream=stream):
-            step()
+            for i in range(n_launch):
+                ctx.decode_stack_dev(layers, x_pool[i], out_pool[i], residual=True, stream=stream)
     return g
 
 
 def time_graph(g, n: int, stream) -> float:
+    """Seconds for n replays, timed with events recorded on the replay stream."""
     import torch
 
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    with torch.cuda.stream(stream):  # replays and events on the same stream
+    with torch.cuda.stream(stream):
         start.record(stream)
         for _ in range(n):
             g.replay()
         end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end) / 1e3
-
-
-def gate_up_roofline(layers, geom, x, stream, reps: int = 20):
-    """Average duration of the dominant kernel (decode gate/up of 8 routed + shared
-    experts), one launch per layer so every launch streams distinct weights."""
-    import torch
-
-    for lyr in layers:  # routing state for stage 1 (the same ids for all layers)
-        lyr.moe_decode_stage_dev(0, x, stream=stream)
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(stream):
-        torch.cuda.synchronize()
-        with torch.cuda.graph(g, stream=stream):
-            for lyr in layers:
-                lyr.moe_decode_stage_dev(1, x, stream=stream)
-    with torch.cuda.stream(stream):
-        g.replay()
-    secs = time_graph(g, reps, stream)
-    per_launch = secs / (reps * len(layers))
-    nbytes = (geom.top_k + 1) * geom.gu_bytes + geom.hidden * 2
-    return per_launch, nbytes
 
 
 def zipf_bias(n: int, tau: float, seed: int):
@@ -219,26 +197,30 @@ def main() -> int:
 
     stream = torch.cuda.Stream()
     gen = torch.Generator(device="cuda").manual_seed(args.seed + 7)
-    n_inputs = args.steps + args.warmup + 1
-    x_pool = torch.randn(n_inputs, geom.hidden, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
-    cursor = torch.zeros(1, dtype=torch.long, device="cuda")
-    bufs = [torch.empty(geom.hidden, dtype=torch.int16, device="cuda") for _ in range(2)]
-    g = decode_graph(layers, geom, x_pool, cursor, bufs, stream)
-    log("decode step captured")
+    n_launch = 32
+    x_pool = torch.randn(n_launch, geom.hidden, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
+    out_pool = torch.empty_like(x_pool)
+    ctx.reserve_decode_stack(layers)
+    g = decode_graph(ctx, layers, x_pool, out_pool, stream, n_launch)
+    log(f"decode graph of {n_launch} steps captured (one persistent launch per step)")
 
+    reps_w = max(1, (args.warmup + n_launch - 1) // n_launch)
+    reps = max(1, (args.steps + n_launch - 1) // n_launch)
     with torch.cuda.stream(stream):
-        for _ in range(args.warmup):
+        for _ in range(reps_w):
             g.replay()
     torch.cuda.synchronize()
-    secs = time_graph(g, args.steps, stream)
-    tok_s = args.steps / secs
-    ms_per_step = secs * 1e3 / args.steps
+    secs = time_graph(g, reps, stream)
+    steps = reps * n_launch
+    tok_s = steps / secs
+    ms_per_step = secs * 1e3 / steps
     bytes_per_token = args.layers * geom.decode_bytes()
-    log(f"decode: {tok_s:.1f} tok/s, {ms_per_step:.3f} ms/token, {bytes_per_token * tok_s / 1e9:.1f} GB/s")
-
-    per_launch, nbytes = gate_up_roofline(layers, geom, bufs[0], stream)
+    log(f"decode: {tok_s:.1f} tok/s, {ms_per_step:.4f} ms/token, {bytes_per_token * tok_s / 1e9:.1f} GB/s")
+    # The dominant kernel is the persistent decode kernel itself (one launch per step):
+    # its average duration is the step time measured above.
+    per_launch = secs / steps
+    nbytes = bytes_per_token
     achieved = nbytes / per_launch / 1e9
-    log(f"gate/up kernel: {per_launch * 1e6:.2f} us/launch, {achieved:.1f} GB/s")
 
     prefill = None
     if not args.no_prefill:
@@ -278,8 +260,8 @@ def main() -> int:
         "value": round(tok_s, 2),
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": reps_w * n_launch,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -300,7 +282,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_gate_up_kernel",
+            "kernel": "decode_stack_kernel (48 layers per launch)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -153,6 +153,23 @@ int rmoe_moe_decode_stage_dev(rmoe_ctx* ctx, int layer, int stage, const void* x
 int rmoe_moe_decode(rmoe_ctx* ctx, int layer, const uint16_t* x, uint16_t* out, int residual,
                     int act, float gate_beta, float value_beta, int32_t* top_ids, float* top_weights);
 
+/* One decode token through n_layers (1..64) MoE layers of one geometry in ONE persistent
+ * launch: the per-layer loop of RaonModel.advance (host/raon.py:862-909) restricted to its
+ * MoE sublayers, each layer as rmoe_moe_decode_dev with x_{l+1} = out_l (residual != 0:
+ * x_{l+1} = RTNE(f32(x_l) + f32(out_l))).  layers is a host array of layer ids read during
+ * the call.  top_ids/top_weights (device, may be NULL) receive [n_layers, k].  The kernel
+ * keeps one workgroup per CU resident; its waits are bounded (a timeout is reported as
+ * RMOE_EDEVICE by the next synchronous call).  Every layer must have a router and a
+ * shared expert.  rmoe_reserve_decode_stack sizes the hand-off buffers (host call,
+ * allocates); the _dev call never allocates. */
+int rmoe_reserve_decode_stack(rmoe_ctx* ctx, const int* layers, int n_layers);
+int rmoe_moe_decode_stack_dev(rmoe_ctx* ctx, const int* layers, int n_layers, const void* x_dev, void* out_dev,
+                              int residual, int act, float gate_beta, float value_beta, void* top_ids_dev,
+                              void* top_weights_dev, void* stream);
+int rmoe_moe_decode_stack(rmoe_ctx* ctx, const int* layers, int n_layers, const uint16_t* x, uint16_t* out,
+                          int residual, int act, float gate_beta, float value_beta, int32_t* top_ids,
+                          float* top_weights);
+
 /* Dispatch permutation (kernels/moe_grouped/planner.py:76-108 flattened): top_ids int32
  * [T, k] -> order int32 [T*k] (assignment index t*k + r at each expert-sorted position;
  * ascending expert, then token, then route) and offsets int32 [n_experts + 1]. */

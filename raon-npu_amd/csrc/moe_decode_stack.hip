@@ -1,0 +1,945 @@
+// Persistent decode of a stack of MoE layers for one token in one launch.
+//
+// Per layer l (RaonModel._moe_token, host/raon.py:1288-1330, with the router of
+// RaonModel._route_token, host/raon.py:1224-1247, on the device, and the expert loop of
+// NumpyBackend.moe_experts, host/backend.py:466-510):
+//   logits = x_l . Wr^T; scores (sigmoid or softmax); top-k by score (+ bias), ties to
+//   the lower expert id; weights renormalised by (sum + 1e-20) and scaled
+//   per slot s (k routed experts, then the shared expert):
+//     g = RTNE(x_l . Wg^T), u = RTNE(x_l . Wu^T), h = RTNE(act(g, u)), d = RTNE(h . Wd^T)
+//   routed = RTNE(sum over the routed slots in ascending expert id of f32(d) * w)
+//   out = RTNE(f32(routed) + f32(d_shared));  x_{l+1} = residual ? RTNE(x_l + out) : out
+//
+// One workgroup per CU stays resident for the whole stack.  The work of a layer is cut
+// into units that are the same for every layer:
+//   GU unit (slot s, band pair j, K part q): gate rows 64j..64j+63 and the matching up
+//     rows over K tiles [kb(q), ke(q)); wave w streams the two tiles at K tile kb + w and
+//     the workgroup writes the fp32 partial sums of the 128 rows.
+//   DN unit (slot s, output band b of 64 rows): all K tiles of the band; waves 1..7
+//     stream them.  A DN wave reads the GU partials of its 128 columns of h, sums the
+//     parts in q order and applies the activation itself.
+// Workgroups hand results to each other through device-scope counters (per layer):
+//   slot[s]   every GU part of slot s is written                   -> DN units of s
+//   band[b]   every slot has written d of band b; the last one to arrive combines the
+//             band, writes x_{l+1}[band] and the band's share of the router logits of
+//             layer l+1                                              -> ready[l+1]
+//   ready     all bands of x_l and of its partial router logits are written
+// Every workgroup computes the top-k of a layer itself from the partial logits (the
+// same reads in the same order give the same routing everywhere), and loads the weight
+// tiles of all its units into registers as soon as the routing is known, before it
+// waits for anything else in that layer: the HBM stream of a layer is issued at once.
+// Results do not depend on the arrival order: every sum over parts, bands or slots is
+// taken in a fixed order.
+#include "rmoe_internal.h"
+
+namespace rmoe {
+namespace {
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxH = 4096;
+constexpr int kMaxE = 256;
+constexpr int kMaxSlots = 17;
+constexpr int kMaxDnPos = 4;      // DN tiles per DN wave (waves 1..7, both units): Ipad <= 1792
+constexpr int kMaxDnUnits = 2;    // DN units per workgroup and layer (prefetched)
+constexpr int kMaxQ = 4;          // GU K parts: H <= 4096
+constexpr int kLRow = 4096;       // floats of partial logits staged in LDS at a time
+constexpr unsigned kSpinLimit = 1u << 21;
+
+struct StackArgs {
+  int L, H, I, Ipad, E, k, S, score, renorm, act, residual;
+  float scaling, gb, vb;
+  size_t gu_bytes, dn_bytes;
+  int nb1, nb2, nkt1, nkt2, nq1, n_gu, n_dn;
+  int Ep;  // n_routed rounded up to 32: row stride of the partial router logits
+  const uint16_t* x0;
+  uint16_t* out;
+  int32_t* ids_out;  // [L, k] or null
+  float* wts_out;    // [L, k] or null
+  uint8_t* scratch;  // per layer: layer_bytes
+  size_t layer_bytes, off_lpart, off_gpart, off_dout;
+  unsigned* cnt;     // per layer cnt_stride counters, then exit, abort
+  int cnt_stride;
+  int* err;
+  const uint8_t* gu[kMaxStack];
+  const uint8_t* dn[kMaxStack];
+  const uint16_t* rw[kMaxStack];
+  const float* rb[kMaxStack];
+};
+
+struct TileRegs {
+  uint4 c[4];
+  uint4 sm;
+};
+
+__device__ __forceinline__ void load_tile(TileRegs& r, const uint8_t* tile, int lane) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r.c[j] = load_stream16(tile + j * 1024 + lane * 16);
+  r.sm = load_stream16(tile + kCodeBytes + lane * 16);
+}
+
+// load_tile of `tile` when valid, otherwise five loads of the same 16 bytes at `dummy`
+// (no offsets: dummy only has to hold 16 bytes), so the load count does not depend on
+// validity.
+__device__ __forceinline__ void load_tile_or(TileRegs& r, bool valid, const uint8_t* tile, const uint8_t* dummy,
+                                             int lane) {
+  const uint8_t* base = valid ? tile + lane * 16 : dummy;
+  const int step = valid ? 1024 : 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r.c[j] = load_stream16(base + j * step);
+  r.sm = load_stream16(base + 4 * step);
+}
+
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+typedef __attribute__((address_space(1))) void* global_void_ptr;
+
+// Direct global -> LDS copy of one tile by one wave (five 1 KB pieces; lane L moves
+// bytes [16L, 16L+16) of each piece).  Invalid tiles copy 16 bytes of `dummy` into the
+// 1 KB `sink` instead, so the number of loads does not depend on validity.  The data is
+// in LDS once the wave's vmcnt has drained.
+__device__ __forceinline__ void dma_tile(bool valid, const uint8_t* tile, const uint8_t* dummy, uint8_t* lds_tile,
+                                         uint8_t* sink, int lane) {
+#pragma unroll
+  for (int j = 0; j < 5; ++j) {
+    const uint8_t* src = valid ? tile + j * 1024 + lane * 16 : dummy;
+    uint8_t* dst = valid ? lds_tile + j * 1024 : sink;
+    __builtin_amdgcn_global_load_lds((global_void_ptr)src, (lds_void_ptr)dst, 16, 0, 0);
+  }
+}
+
+// tile_dot of a tile held in LDS (same byte layout as in HBM).
+__device__ __forceinline__ float tile_dot_lds(const uint8_t* t, int lane, const uint32_t* xw, const float* ss,
+                                              float acc) {
+  TileRegs r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r.c[j] = *reinterpret_cast<const uint4*>(t + j * 1024 + lane * 16);
+  r.sm = *reinterpret_cast<const uint4*>(t + kCodeBytes + lane * 16);
+  const uint32_t sm[4] = {r.sm.x, r.sm.y, r.sm.z, r.sm.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc = group_apply(sm[j], group_dot(r.c[j], xw + j * 16), ss[j], acc);
+  return acc;
+}
+
+__device__ __forceinline__ float tile_dot(const TileRegs& r, const uint32_t* xw, const float* ss, float acc) {
+  const uint32_t sm[4] = {r.sm.x, r.sm.y, r.sm.z, r.sm.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc = group_apply(sm[j], group_dot(r.c[j], xw + j * 16), ss[j], acc);
+  return acc;
+}
+
+// Counters of layer l: [0] ready, [1, 1+S) slot, [1+S, 1+S+nb2) band, then pair[S*nb1].
+__device__ __forceinline__ unsigned* layer_cnt(const StackArgs& a, int l) { return a.cnt + (size_t)l * a.cnt_stride; }
+__device__ __forceinline__ unsigned* exit_cnt(const StackArgs& a) { return a.cnt + (size_t)a.L * a.cnt_stride; }
+__device__ __forceinline__ unsigned* abort_flag(const StackArgs& a) { return exit_cnt(a) + 1; }
+
+// Hand-off protocol.  Data handed to other workgroups is stored with device-scope
+// stores (st_dev); the storing wave waits until its stores are acknowledged
+// (s_waitcnt 0 drains every counter of that wave) before the arrival is counted, and
+// readers load it (ld_hand_u64) after they have seen the count with a device-scope poll.  A wave's wait also
+// covers its own earlier loads, so the waves that publish (wave 0, and every wave for
+// the router logits) never hold long-latency weight prefetches.
+
+// Reads of hand-off data.  Every hand-off buffer is written exactly once per launch (a
+// separate region per layer), by device-scope stores that go through to memory, and is
+// read only after the counter that covers it is complete; no L2 holds a copy of it from
+// before the write (kernel launches start with invalidated L2s, and nothing reads a
+// region of this launch before its counter is complete).  So ordinary cached loads see
+// the stored values, and each XCD's L2 fetches a line once for all 32 workgroups on it
+// instead of every workgroup going to the memory side.  The compiler may not hoist
+// them above the wait: wait_geq ends with a barrier and an acquire fence.
+// Every hand-off cache line has exactly one writer, so even an L2 that allocated a line
+// on its own workgroup's store holds exactly what was stored.
+__device__ __forceinline__ uint64_t ld_hand_u64(const void* p) { return *reinterpret_cast<const uint64_t*>(p); }
+__device__ __forceinline__ float ld_hand_f32(const float* p) { return *p; }
+
+// One wave, after its device-scope stores: count one arrival.  With `ret` the previous
+// count is returned (in every lane) -- one more round trip; without it the add is
+// posted and the wave moves on.
+__device__ __forceinline__ unsigned wave_arrive(unsigned* counter, bool ret) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(0);
+  unsigned prev = 0u;
+  if ((threadIdx.x & 63) == 0) {
+    if (ret)
+      prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+      __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  prev = __builtin_amdgcn_readfirstlane(prev);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  return prev;
+}
+
+// Block-wide: every wave waits for its own stores, then thread 0 counts one arrival.
+// Returns true in every thread for the n-th arrival.
+__device__ __forceinline__ bool block_arrive(unsigned* counter, unsigned n, unsigned* flag_lds) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag_lds = (prev + 1u == n) ? 1u : 0u;
+  }
+  __syncthreads();
+  const bool last = *flag_lds != 0u;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  return last;
+}
+
+// Block-wide publication without a result: every wave waits for its own stores, then
+// thread 0 posts one arrival.
+__device__ __forceinline__ void block_publish(unsigned* counter) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Block-wide wait until *p >= target (thread 0 polls).  Bounded: after kSpinLimit polls
+// (seconds) or when another workgroup gave up, the stack is abandoned (error bit 8,
+// abort flag) and false is returned in every thread, so every wave of the grid still
+// reaches its end.
+__device__ __forceinline__ bool wait_geq(const StackArgs& a, const unsigned* p, unsigned target, unsigned* flag_lds) {
+  if (threadIdx.x == 0) {
+    unsigned ok = 1u;
+    unsigned it = 0;
+    while (ld_dev_u32(p) < target) {
+      ++it;
+      if ((it & 63u) == 0u && ld_dev_u32(abort_flag(a)) != 0u) {
+        ok = 0u;
+        break;
+      }
+      if (it > kSpinLimit) {
+        st_dev_u32(abort_flag(a), 1u);
+        __hip_atomic_fetch_or(a.err, 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ok = 0u;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    *flag_lds = ok;
+  }
+  __syncthreads();
+  const bool ok = *flag_lds != 0u;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  return ok;
+}
+
+struct SelectLds {
+  float lg[kMaxE];                               // logits, then scores
+  __attribute__((aligned(16))) uint32_t key[kMaxE];  // ordered selection keys
+  int rank[kMaxE];
+  int id[kMaxSlots];  // slot -> expert (routed slots by rank, then shared)
+  float w[kMaxSlots];
+  int ord[kMaxSlots]; // routed slots in ascending expert id
+};
+
+struct SelectParams {
+  int E, k, S, score, renorm;
+  float scaling;
+};
+
+// Float -> uint32 whose unsigned order is the float order (finite values).
+__device__ __forceinline__ uint32_t order_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Scores, top-k and weights of one token from sl.lg (every thread of the block):
+//   sl.id[r], sl.w[r]  the expert and weight of rank r (descending selection key, ties
+//                      to the lower id), then the shared expert in slot k (weight 1)
+//   sl.ord[i]          the rank of the i-th selected expert in ascending id order
+// Scores and weights follow host/raon.py:1224-1247 (softmax / sigmoid, selection bias,
+// renormalisation by (sum + 1e-20), scaling).  The softmax denominator and the
+// renormalisation sum are wave tree sums (a fixed order; numpy's pairwise order differs
+// in the last bit at most, and the selection does not depend on either sum).
+// rank(i) = #{j : key_j > key_i, or key_j == key_i and j < i} is counted by the whole
+// block, each thread over a contiguous quarter (or half) of the keys read 16 bytes at a
+// time; the selected ranks are then ordered by expert id from ballots.
+__device__ __forceinline__ void select_topk(const SelectParams a, const float* __restrict__ bias, SelectLds& sl) {
+  constexpr int NC = kMaxE / 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int E = a.E;
+  if (wave == 0) {
+    float sc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) sc[c] = lane + 64 * c < E ? sl.lg[lane + 64 * c] : -__builtin_inff();
+    if (a.score == 0) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) sc[c] = 1.0f / (1.0f + expf(-sc[c]));
+    } else {
+      float m = sc[0];
+#pragma unroll
+      for (int c = 1; c < NC; ++c) m = fmaxf(m, sc[c]);
+      m = wave_max(m);
+      float z = 0.f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        sc[c] = lane + 64 * c < E ? expf(sc[c] - m) : 0.f;
+        z += sc[c];
+      }
+      z = wave_sum(z);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) sc[c] = sc[c] / z;
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int e = lane + 64 * c;
+      // Padded entries (e >= E) sort below every real key and are never counted.
+      sl.key[e] = e < E ? order_key(bias ? __fadd_rn(sc[c], bias[e]) : sc[c]) : 0u;
+      sl.lg[e] = sc[c];
+      sl.rank[e] = 0;
+    }
+  }
+  __syncthreads();
+  {
+    const int Ep = E <= 128 ? 128 : 256;
+    const int P = kThreads / Ep;  // parts of the key range
+    const int i = tid % Ep, p = tid / Ep;
+    const int len = Ep / P;       // 32 or 128 keys per part
+    const uint32_t ki = sl.key[i];
+    const uint4* kp = reinterpret_cast<const uint4*>(sl.key + p * len);
+    int cnt = 0;
+    for (int j0 = 0; j0 < len; j0 += 32) {
+      uint4 kv[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) kv[q] = kp[j0 / 4 + q];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const uint32_t kk[4] = {kv[q].x, kv[q].y, kv[q].z, kv[q].w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = p * len + j0 + 4 * q + r;
+          cnt += (kk[r] > ki || (kk[r] == ki && j < i)) ? 1 : 0;
+        }
+      }
+    }
+    if (i < E) atomicAdd(&sl.rank[i], cnt);
+  }
+  __syncthreads();
+  if (wave == 0) {
+    unsigned long long sel[NC];
+    int below = 0;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int e = lane + 64 * c;
+      const int r = e < E ? sl.rank[e] : a.k;
+      sel[c] = __ballot(r < a.k);
+      if (r < a.k) {
+        sl.id[r] = e;
+        sl.w[r] = sl.lg[e];
+        sl.ord[below + __popcll(sel[c] & ((1ull << lane) - 1ull))] = r;
+      }
+      below += __popcll(sel[c]);
+    }
+    if (below != a.k && lane == 0) {
+      // Only unordered keys (NaN) can leave ranks unfilled: name valid experts, weight 0.
+      for (int r = 0; r < a.k; ++r) {
+        sl.id[r] = r;
+        sl.w[r] = 0.f;
+        sl.ord[r] = r;
+      }
+    }
+    const float wr = lane < a.k ? sl.w[lane] : 0.f;
+    const float denom = a.renorm ? __fadd_rn(wave_sum(wr), 1e-20f) : 1.f;
+    if (lane < a.k) sl.w[lane] = __fmul_rn(a.renorm ? wr / denom : wr, a.scaling);
+    if (lane == 0 && a.S > a.k) {
+      sl.id[a.k] = a.E;  // shared expert
+      sl.w[a.k] = 1.f;
+    }
+  }
+  __syncthreads();
+}
+
+// Partial router logits of 64 rows (band b) of x for every expert:
+//   part[b * Ep + e] = sum_{c in band} x[c] * Wr[e, c]
+// (one row of Ep = E rounded up to 32 floats per band: whole cache lines, one writer).
+// xp: the band as 32 bf16 pairs in LDS.  wv: this thread's router weights for items
+// tid + kThreads*it (item = expert*4 + quarter of 16 columns).  Every thread stores.
+template <int NIT>
+__device__ __forceinline__ void band_logits(const StackArgs& a, const uint32_t* xp, const uint4 (&wv)[NIT][2],
+                                            float* part, int b) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int idx = tid + kThreads * it;
+    float v = 0.f;
+    if (idx < a.E * 4) {
+      const uint32_t* xq = xp + 8 * (idx & 3);
+      const uint32_t w8[8] = {wv[it][0].x, wv[it][0].y, wv[it][0].z, wv[it][0].w,
+                              wv[it][1].x, wv[it][1].y, wv[it][1].z, wv[it][1].w};
+#pragma unroll
+      for (int c = 0; c < 8; ++c) v = dot2_bf16(w8[c], xq[c], v);
+    }
+    v += __shfl_xor(v, 1, 64);
+    v += __shfl_xor(v, 2, 64);
+    if (idx < a.E * 4 && (idx & 3) == 0) st_dev(&part[(size_t)b * a.Ep + (idx >> 2)], v);
+  }
+}
+
+// Router weights of band b for this thread's items (invalid items read `dummy`, so the
+// number of loads is the same on every path and the compiler's waits stay exact).
+template <int NIT>
+__device__ __forceinline__ void load_router_slice(const StackArgs& a, const uint16_t* rw, int b, bool valid,
+                                                  const uint8_t* dummy, uint4 (&wv)[NIT][2]) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int idx = tid + kThreads * it;
+    const uint8_t* p = dummy;
+    if (valid && idx < a.E * 4)
+      p = reinterpret_cast<const uint8_t*>(rw + (size_t)(idx >> 2) * a.H + 64 * b + 16 * (idx & 3));
+    wv[it][0] = *reinterpret_cast<const uint4*>(p);
+    wv[it][1] = *reinterpret_cast<const uint4*>(p + 16);
+  }
+}
+
+// DNPOS: DN tiles per DN wave (waves 1..7 stream the tiles of both DN units:
+// 2 * Ipad/128 <= 7 * DNPOS); NIT: router items per thread (n_routed <= 128 * NIT);
+// QM: GU K parts (nq1 <= QM).  They size register and LDS arrays, so they are template
+// parameters.
+//
+// Wave roles: every wave streams GU tiles; waves 1..7 stream the DN tiles; wave 0 does
+// the cross-workgroup hand-offs (partial sums, h, d, the combine) and holds no DN
+// prefetch, so its waits for its own stores are short.  Loads that have no valid
+// target read `dummy` instead of being skipped: every wave issues the same number of
+// loads on every path, which keeps the compiler's s_waitcnt counts exact (a GU tile is
+// consumed without waiting for the DN tiles issued after it).
+template <int DNPOS, int NIT, int QM>
+__global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
+  __shared__ __attribute__((aligned(16))) uint32_t xs[kMaxH / 2];  // x_l as bf16 pairs
+  __shared__ float xsum[kMaxH / 32];                              // group sums of x_l
+  __shared__ SelectLds sl;
+  __shared__ float red[kWaves][2][64];
+  __shared__ __attribute__((aligned(16))) uint32_t hs[kWaves][DNPOS][64];
+  __shared__ float hsum[kWaves][DNPOS][4];
+  __shared__ float cmb[kMaxSlots][64];                         // d of every slot of a band
+  __shared__ __attribute__((aligned(16))) uint32_t xband[32];  // x_{l+1} of a band, bf16 pairs
+  __shared__ __attribute__((aligned(16))) float lrow[kLRow];   // partial logits being summed
+  __shared__ unsigned flag, band_last_d[kMaxDnUnits];
+  // DN tiles of this workgroup's units: [kMaxDnUnits][nkt2] tiles, then a 1 KB sink.
+  extern __shared__ __attribute__((aligned(16))) uint8_t dn_lds[];
+  uint8_t* dn_sink = dn_lds + (size_t)kMaxDnUnits * a.nkt2 * kTileBytes;
+
+  // This workgroup's first GU unit (slot, band pair, K tiles [kb, ke), part q) and its DN
+  // units (slot, band; -1 when absent).  The same in every layer; kept in LDS so that
+  // the index arithmetic does not hold registers across the layer loop.
+  __shared__ int gu_d[5], dn_d[kMaxDnUnits][2];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = blockIdx.x, G = gridDim.x;
+  const int Hp = a.H / 2;
+  if (tid == 0) {
+    const int u = g;
+    if (u < a.n_gu) {
+      const int s = u / (a.nb1 * a.nq1), rem = u % (a.nb1 * a.nq1);
+      const int q = rem % a.nq1;
+      gu_d[0] = s;
+      gu_d[1] = rem / a.nq1;
+      gu_d[2] = q * a.nkt1 / a.nq1;
+      gu_d[3] = (q + 1) * a.nkt1 / a.nq1;
+      gu_d[4] = q;
+    } else {
+      gu_d[0] = -1;
+    }
+    const int v0 = ((g - a.n_gu) % G + G) % G;  // first DN unit of this workgroup
+    for (int d = 0; d < kMaxDnUnits; ++d) {
+      const int v = v0 + d * G;
+      dn_d[d][0] = v < a.n_dn ? v / a.nb2 : -1;
+      dn_d[d][1] = v < a.n_dn ? v % a.nb2 : 0;
+    }
+  }
+  __syncthreads();
+  const uint8_t* dummy = reinterpret_cast<const uint8_t*>(a.x0);
+  const unsigned gu_parts = (unsigned)(a.nb1 * a.nq1);
+
+  // Layer 0: the band share of the router logits of x0 (workgroups b < nb2).
+  if (g < a.nb2) {
+    if (tid < 32) xband[tid] = reinterpret_cast<const uint32_t*>(a.x0)[32 * g + tid];
+    uint4 wv[NIT][2];
+    load_router_slice<NIT>(a, a.rw[0], g, true, dummy, wv);
+    __syncthreads();
+    band_logits<NIT>(a, xband, wv, reinterpret_cast<float*>(a.scratch + a.off_lpart), g);
+    block_publish(&layer_cnt(a, 0)[0]);
+  }
+
+  for (int l = 0; l < a.L; ++l) {
+    unsigned* cl = layer_cnt(a, l);
+    unsigned* c_slot = cl + 1;
+    unsigned* c_band = cl + 1 + a.S;
+    uint8_t* lay = a.scratch + (size_t)l * a.layer_bytes;
+    const uint32_t* xin = reinterpret_cast<const uint32_t*>(lay);
+    const float* lpart = reinterpret_cast<const float*>(lay + a.off_lpart);
+    float* gpart = reinterpret_cast<float*>(lay + a.off_gpart);
+    float* dout = reinterpret_cast<float*>(lay + a.off_dout);
+
+    if (!wait_geq(a, &cl[0], (unsigned)a.nb2, &flag)) return;
+
+    // ---- x_l and the routing of this layer.  Every device-scope load of a thread is
+    // issued before the first use, so the latencies overlap.
+    {
+      // x_l: 64-bit loads (tid covers dwords 2*idx, 2*idx+1).  The partial logits
+      // [nb2][Ep] are contiguous: chunks of up to kLRow floats are copied into LDS with
+      // 16-byte loads (the first chunk's loads issued together with x's), then thread e
+      // sums its expert's bands in band order.
+      uint64_t xv[kMaxH / 4 / kThreads];
+#pragma unroll
+      for (int i = 0; i < kMaxH / 4 / kThreads; ++i) {
+        const int idx = tid + kThreads * i;
+        if (2 * idx < Hp)
+          xv[i] = l == 0 ? reinterpret_cast<const uint64_t*>(a.x0)[idx] : ld_hand_u64(xin + 2 * idx);
+      }
+      const int nbc = kLRow / a.Ep;  // bands per chunk
+      float lacc = 0.f;
+      for (int b0 = 0; b0 < a.nb2; b0 += nbc) {
+        const int nf4 = (min(nbc, a.nb2 - b0) * a.Ep) / 4;
+        const uint4* src = reinterpret_cast<const uint4*>(lpart + (size_t)b0 * a.Ep);
+        uint4 lv[kLRow / 4 / kThreads];
+#pragma unroll
+        for (int i = 0; i < kLRow / 4 / kThreads; ++i)
+          if (tid + kThreads * i < nf4) lv[i] = src[tid + kThreads * i];
+        if (b0 == 0) {
+#pragma unroll
+          for (int i = 0; i < kMaxH / 4 / kThreads; ++i) {
+            const int idx = tid + kThreads * i;
+            if (2 * idx < Hp) {
+              xs[2 * idx] = (uint32_t)xv[i];
+              xs[2 * idx + 1] = (uint32_t)(xv[i] >> 32);
+            }
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < kLRow / 4 / kThreads; ++i)
+          if (tid + kThreads * i < nf4) reinterpret_cast<uint4*>(lrow)[tid + kThreads * i] = lv[i];
+        __syncthreads();
+        if (tid < a.E) {
+          // In band order; eight LDS reads in flight at a time.
+          const int nb = min(nbc, a.nb2 - b0);
+          int b = 0;
+          for (; b + 8 <= nb; b += 8) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = lrow[(b + i) * a.Ep + tid];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) lacc += v[i];
+          }
+          for (; b < nb; ++b) lacc += lrow[b * a.Ep + tid];
+        }
+        __syncthreads();
+      }
+      if (tid < a.E) sl.lg[tid] = lacc;
+    }
+    for (int gi = tid; gi < a.H / 32; gi += kThreads) {
+      float sum = 0.f;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        const uint32_t v = xs[gi * 16 + c];
+        sum += bf16_to_f32(v & 0xffffu);
+        sum += bf16_to_f32(v >> 16);
+      }
+      xsum[gi] = sum;
+    }
+    __syncthreads();
+    select_topk(SelectParams{a.E, a.k, a.S, a.score, a.renorm, a.scaling}, a.rb[l], sl);
+    if (g == 0 && tid < a.k) {
+      if (a.ids_out) a.ids_out[(size_t)l * a.k + tid] = sl.id[tid];
+      if (a.wts_out) a.wts_out[(size_t)l * a.k + tid] = sl.w[tid];
+    }
+
+    // ---- issue every weight load of this workgroup's units for this layer.
+    const uint8_t* gu_l = a.gu[l];
+    const uint8_t* dn_l = a.dn[l];
+    TileRegs gt, ut;
+    {
+      const uint8_t* pg = dummy;
+      const uint8_t* pu = dummy;
+      bool ok = false;
+      const int s = gu_d[0];
+      if (s >= 0) {
+        const int j = gu_d[1], kb = gu_d[2], ke = gu_d[3];
+        const int kt = kb + wave;
+        if (kt < ke) {
+          const uint8_t* W = gu_l + (size_t)sl.id[s] * a.gu_bytes;
+          pg = W + ((size_t)j * a.nkt1 + kt) * kTileBytes;
+          pu = W + ((size_t)(a.nb1 + j) * a.nkt1 + kt) * kTileBytes;
+          ok = true;
+        }
+      }
+      load_tile_or(gt, ok, pg, dummy, lane);
+      load_tile_or(ut, ok, pu, dummy, lane);
+    }
+    // DN tiles of both units, flattened as t = d * nkt2 + kt: wave 1 + t % 7 copies tile t
+    // into LDS slot t at its position t / 7.
+    const int n_dn_t = (dn_d[0][0] >= 0 ? a.nkt2 : 0) + (dn_d[1][0] >= 0 ? a.nkt2 : 0);
+#pragma unroll
+    for (int p = 0; p < DNPOS; ++p) {
+      const int t = wave - 1 + (kWaves - 1) * p;
+      const bool ok = wave > 0 && t < n_dn_t;
+      const int d = ok ? t / a.nkt2 : 0, kt = ok ? t % a.nkt2 : 0;
+      const uint8_t* W = dn_l + (size_t)sl.id[ok ? dn_d[d][0] : 0] * a.dn_bytes;
+      dma_tile(ok, W + ((size_t)dn_d[d][1] * a.nkt2 + kt) * kTileBytes, dummy, dn_lds + (size_t)t * kTileBytes,
+               dn_sink, lane);
+    }
+    uint4 rwv[kMaxDnUnits][NIT][2];
+#pragma unroll
+    for (int d = 0; d < kMaxDnUnits; ++d)
+      load_router_slice<NIT>(a, a.rw[l + 1 < a.L ? l + 1 : l], dn_d[d][1], dn_d[d][0] >= 0 && l + 1 < a.L, dummy,
+                             rwv[d]);
+
+    // ---- GU units: the first one from the registers loaded above (kept out of the loop so
+    // the compiler's wait for its tiles does not also cover the DN loads), then any
+    // further ones (more units than workgroups) loaded on the spot.
+    auto gu_unit = [&](int s, int j, int kb, int ke, int q) {
+      const int kt = kb + wave;
+      float ag = 0.f, au = 0.f;
+      if (kt < ke) {
+        ag = tile_dot(gt, xs + kt * 64, xsum + kt * 4, 0.f);
+        au = tile_dot(ut, xs + kt * 64, xsum + kt * 4, 0.f);
+      }
+      red[wave][0][lane] = ag;
+      red[wave][1][lane] = au;
+      __syncthreads();
+      if (wave == 0) {
+        float* gp = gpart + ((size_t)(s * a.nb1 + j) * a.nq1 + q) * 128;
+        float sg = 0.f, su = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          sg += red[w][0][lane];
+          su += red[w][1][lane];
+        }
+        st_dev(&gp[lane], sg);
+        st_dev(&gp[64 + lane], su);
+        wave_arrive(&c_slot[s], false);
+      }
+    };
+    if (gu_d[0] >= 0) gu_unit(gu_d[0], gu_d[1], gu_d[2], gu_d[3], gu_d[4]);
+    for (int u = g + G; u < a.n_gu; u += G) {
+      const int s = u / (a.nb1 * a.nq1), rem = u % (a.nb1 * a.nq1);
+      const int j = rem / a.nq1, q = rem % a.nq1;
+      const int kb = q * a.nkt1 / a.nq1, ke = (q + 1) * a.nkt1 / a.nq1;
+      const int kt = kb + wave;
+      __syncthreads();  // red[] of the previous unit has been read
+      if (kt < ke) {
+        const uint8_t* W = gu_l + (size_t)sl.id[s] * a.gu_bytes;
+        load_tile(gt, W + ((size_t)j * a.nkt1 + kt) * kTileBytes, lane);
+        load_tile(ut, W + ((size_t)(a.nb1 + j) * a.nkt1 + kt) * kTileBytes, lane);
+      }
+      gu_unit(s, j, kb, ke, q);
+    }
+
+    // ---- DN units, both of a workgroup at once, and the combine of a band by the last
+    // slot to finish it.
+    if (n_dn_t > 0) {
+      if (!wait_geq(a, &c_slot[dn_d[0][0]], gu_parts, &flag)) return;
+      if (dn_d[1][0] >= 0 && !wait_geq(a, &c_slot[dn_d[1][0]], gu_parts, &flag)) return;
+      if (wave > 0) {
+        // h for columns 128kt + 2*lane (+1) of each of this wave's tiles: the GU partials
+        // of both columns for every K part (64-bit loads, all issued before the sums),
+        // summed in part order.
+        uint64_t gq[DNPOS][QM], uq[DNPOS][QM];
+#pragma unroll
+        for (int p = 0; p < DNPOS; ++p) {
+          const int t = wave - 1 + (kWaves - 1) * p;
+          const int d = t < n_dn_t ? t / a.nkt2 : 0, kt = t < n_dn_t ? t % a.nkt2 : 0;
+          const int c0 = 128 * kt + 2 * lane;
+          const bool ok = t < n_dn_t && c0 < a.I;
+          const float* gp = gpart + ((size_t)(dn_d[d][0] * a.nb1 + (ok ? c0 >> 6 : 0)) * a.nq1) * 128 + (c0 & 63);
+#pragma unroll
+          for (int q = 0; q < QM; ++q)
+            if (ok && q < a.nq1) {
+              gq[p][q] = ld_hand_u64(gp + q * 128);
+              uq[p][q] = ld_hand_u64(gp + q * 128 + 64);
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < DNPOS; ++p) {
+          const int t = wave - 1 + (kWaves - 1) * p;
+          if (t < n_dn_t) {
+            const int c0 = 128 * (t % a.nkt2) + 2 * lane;
+            float h0 = 0.f, h1 = 0.f;
+            if (c0 < a.I) {
+              float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
+#pragma unroll
+              for (int q = 0; q < QM; ++q)
+                if (q < a.nq1) {
+                  g0 += __uint_as_float((uint32_t)gq[p][q]);
+                  g1 += __uint_as_float((uint32_t)(gq[p][q] >> 32));
+                  u0 += __uint_as_float((uint32_t)uq[p][q]);
+                  u1 += __uint_as_float((uint32_t)(uq[p][q] >> 32));
+                }
+              h0 = bf16_round(act_apply(a.act, bf16_round(g0), bf16_round(u0), a.gb, a.vb));
+              h1 = bf16_round(act_apply(a.act, bf16_round(g1), bf16_round(u1), a.gb, a.vb));
+            }
+            hs[wave][p][lane] = f32_to_bf16(h0) | (f32_to_bf16(h1) << 16);
+            float gs = h0 + h1;
+#pragma unroll
+            for (int off = 8; off > 0; off >>= 1) gs += __shfl_xor(gs, off, 16);
+            if ((lane & 15) == 0) hsum[wave][p][lane >> 4] = gs;
+          }
+        }
+      }
+      // This wave's DN tiles were copied into LDS by its own loads: drain them.
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      float acc[kMaxDnUnits] = {0.f, 0.f};
+      if (wave > 0) {
+#pragma unroll
+        for (int p = 0; p < DNPOS; ++p) {
+          const int t = wave - 1 + (kWaves - 1) * p;
+          if (t < n_dn_t) {
+            const float v = tile_dot_lds(dn_lds + (size_t)t * kTileBytes, lane, hs[wave][p], hsum[wave][p], 0.f);
+            if (t < a.nkt2) acc[0] += v;
+            else acc[1] += v;
+          }
+        }
+      }
+      red[wave][0][lane] = acc[0];
+      red[wave][1][lane] = acc[1];
+      __syncthreads();
+      if (wave == 0) {
+        // Expert outputs of both units, then both arrivals (issued together).
+        unsigned* cnt_d[kMaxDnUnits];
+        int nd = 0;
+#pragma unroll
+        for (int d = 0; d < kMaxDnUnits; ++d) {
+          if (dn_d[d][0] < 0) continue;
+          float dd = 0.f;
+#pragma unroll
+          for (int w = 1; w < kWaves; ++w) dd += red[w][d][lane];
+          st_dev(&dout[(size_t)dn_d[d][0] * a.H + 64 * dn_d[d][1] + lane], bf16_round(dd));
+          cnt_d[nd++] = &c_band[dn_d[d][1]];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_s_waitcnt(0);
+        unsigned prev[kMaxDnUnits] = {0u, 0u};
+        if (lane == 0)
+          for (int d = 0; d < nd; ++d)
+            prev[d] = __hip_atomic_fetch_add(cnt_d[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int d = 0; d < kMaxDnUnits; ++d) {
+          const unsigned pv = __builtin_amdgcn_readfirstlane(prev[d]);
+          if (lane == 0) band_last_d[d] = (d < nd && pv + 1u == (unsigned)a.S) ? 1u : 0u;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      }
+      __syncthreads();
+      for (int d = 0; d < kMaxDnUnits; ++d) {
+        if (band_last_d[d] == 0u) continue;
+        const int b = dn_d[d][1];
+        if (wave == 0) {
+          const int row = 64 * b + lane;
+          float dv[kMaxSlots];
+#pragma unroll
+          for (int q = 0; q < kMaxSlots; ++q)
+            if (q < a.S) dv[q] = ld_hand_f32(&dout[(size_t)q * a.H + row]);
+#pragma unroll
+          for (int q = 0; q < kMaxSlots; ++q)
+            if (q < a.S) cmb[q][lane] = dv[q];
+          // Ascending expert id: the slot order, then each slot's value and weight, read
+          // from LDS in batches, then summed in order.
+          float acc2 = 0.f;
+          for (int r0 = 0; r0 < a.k; r0 += 8) {
+            int o8[8];
+            float c8[8], w8[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o8[i] = r0 + i < a.k ? sl.ord[r0 + i] : 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              c8[i] = cmb[o8[i]][lane];
+              w8[i] = sl.w[o8[i]];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              if (r0 + i < a.k) acc2 = __fadd_rn(acc2, __fmul_rn(c8[i], w8[i]));
+          }
+          uint32_t o = f32_to_bf16(acc2);
+          if (a.S > a.k) o = f32_to_bf16(__fadd_rn(bf16_to_f32(o), cmb[a.k][lane]));
+          if (a.residual) {
+            const uint32_t xv = (xs[row >> 1] >> (16 * (row & 1))) & 0xffffu;
+            o = f32_to_bf16(__fadd_rn(bf16_to_f32(xv), bf16_to_f32(o)));
+          }
+          const uint32_t hi = __shfl_down(o, 1, 64);
+          if ((lane & 1) == 0) xband[lane >> 1] = o | (hi << 16);
+          if (l + 1 == a.L) {
+            a.out[row] = (uint16_t)o;
+          } else if ((lane & 1) == 0) {
+            uint32_t* xnext = reinterpret_cast<uint32_t*>(lay + a.layer_bytes);
+            st_dev_u32(&xnext[row >> 1], o | (hi << 16));
+          }
+        }
+        if (l + 1 < a.L) {
+          __syncthreads();
+          float* lnext = reinterpret_cast<float*>(lay + a.layer_bytes + a.off_lpart);
+          band_logits<NIT>(a, xband, rwv[d], lnext, b);
+          block_publish(&layer_cnt(a, l + 1)[0]);
+        }
+        __syncthreads();  // xband / cmb are reused by the next band
+      }
+    }
+  }
+
+  // Every wave's stores and counter updates are complete before the workgroup counts
+  // itself out; the last workgroup out clears every counter for the next launch.
+  if (block_arrive(exit_cnt(a), (unsigned)G, &flag)) {
+    const int n = a.L * a.cnt_stride;
+    for (int i = tid; i < n; i += kThreads) st_dev_u32(&a.cnt[i], 0u);
+    if (tid == 0) {
+      st_dev_u32(abort_flag(a), 0u);
+      st_dev_u32(exit_cnt(a), 0u);
+    }
+  }
+}
+
+struct StackShape {
+  int S, nb1, nb2, nkt1, nkt2, nq1, n_gu, n_dn;
+  size_t off_lpart, off_gpart, off_dout, layer_bytes;
+  int cnt_stride;
+};
+
+size_t al256(size_t v) { return (v + 255) / 256 * 256; }
+
+// Dynamic LDS of the kernel: the DN tiles of kMaxDnUnits units plus the 1 KB sink.
+size_t dn_lds_bytes(int nkt2) { return (size_t)kMaxDnUnits * nkt2 * kTileBytes + 1024; }
+constexpr size_t kLdsLimit = 160 * 1024;   // per CU on gfx950
+constexpr size_t kStaticLds = 48 * 1024;   // bound on the kernel's static LDS
+
+StackShape stack_shape(const RmoeLayer& L) {
+  StackShape sh{};
+  sh.S = L.top_k + L.n_shared;
+  sh.nb1 = L.I / 64;
+  sh.nb2 = L.H / 64;
+  sh.nkt1 = L.H / kTileCols;
+  sh.nkt2 = L.Ipad / kTileCols;
+  sh.nq1 = (sh.nkt1 + kWaves - 1) / kWaves;
+  sh.n_gu = sh.S * sh.nb1 * sh.nq1;
+  sh.n_dn = sh.S * sh.nb2;
+  size_t off = al256((size_t)L.H * 2);  // x_l (bf16)
+  sh.off_lpart = off;
+  off += al256((size_t)sh.nb2 * ((L.n_routed + 31) / 32 * 32) * 4);
+  sh.off_gpart = off;
+  off += al256((size_t)sh.S * sh.nb1 * sh.nq1 * 128 * 4);
+  sh.off_dout = off;
+  off += al256((size_t)sh.S * L.H * 4);
+  sh.layer_bytes = off;
+  sh.cnt_stride = 1 + sh.S + sh.nb2;
+  return sh;
+}
+
+}  // namespace
+
+size_t stack_scratch_bytes(const RmoeLayer& L, int n_layers) {
+  const StackShape sh = stack_shape(L);
+  // One extra layer slot: the last layer's combine addresses layer L's x and logits.
+  return sh.layer_bytes * (size_t)(n_layers + 1);
+}
+
+size_t stack_counter_count(const RmoeLayer& L, int n_layers) {
+  return (size_t)stack_shape(L).cnt_stride * n_layers + 2;
+}
+
+hipError_t stack_check(const RmoeLayer& L, int n_cu) {
+  const StackShape sh = stack_shape(L);
+  if (L.H > kMaxH || L.n_routed > kMaxE || sh.S > kMaxSlots || kMaxDnUnits * sh.nkt2 > (kWaves - 1) * kMaxDnPos ||
+      sh.nq1 > kMaxQ || dn_lds_bytes(sh.nkt2) + kStaticLds > kLdsLimit)
+    return hipErrorInvalidValue;
+
+  if (sh.n_dn > kMaxDnUnits * n_cu || n_cu < sh.nb2) return hipErrorInvalidValue;
+  return hipSuccess;
+}
+
+hipError_t launch_decode_stack(const RmoeLayer* const* layers, int n_layers, const uint16_t* x, uint16_t* out,
+                               bool residual, int act, float gb, float vb, int32_t* ids_out, float* wts_out,
+                               RmoeScratch& s, int n_cu, hipStream_t st) {
+  if (n_layers < 1 || n_layers > kMaxStack) return hipErrorInvalidValue;
+  const RmoeLayer& L0 = *layers[0];
+  if (stack_check(L0, n_cu) != hipSuccess) return hipErrorInvalidValue;
+  if (stack_scratch_bytes(L0, n_layers) > s.stack_bytes || stack_counter_count(L0, n_layers) > s.stack_cnt_n)
+    return hipErrorInvalidValue;
+  const StackShape sh = stack_shape(L0);
+  StackArgs a{};
+  a.L = n_layers;
+  a.H = L0.H;
+  a.I = L0.I;
+  a.Ipad = L0.Ipad;
+  a.E = L0.n_routed;
+  a.k = L0.top_k;
+  a.S = sh.S;
+  a.score = L0.score;
+  a.renorm = L0.renorm;
+  a.scaling = L0.scaling;
+  a.act = act;
+  a.residual = residual ? 1 : 0;
+  a.gb = gb;
+  a.vb = vb;
+  a.gu_bytes = L0.gu_bytes;
+  a.dn_bytes = L0.dn_bytes;
+  a.nb1 = sh.nb1;
+  a.nb2 = sh.nb2;
+  a.nkt1 = sh.nkt1;
+  a.nkt2 = sh.nkt2;
+  a.nq1 = sh.nq1;
+  a.n_gu = sh.n_gu;
+  a.n_dn = sh.n_dn;
+  a.Ep = (L0.n_routed + 31) / 32 * 32;
+  a.x0 = x;
+  a.out = out;
+  a.ids_out = ids_out;
+  a.wts_out = wts_out;
+  a.scratch = s.stack;
+  a.layer_bytes = sh.layer_bytes;
+  a.off_lpart = sh.off_lpart;
+  a.off_gpart = sh.off_gpart;
+  a.off_dout = sh.off_dout;
+  a.cnt = s.stack_cnt;
+  a.cnt_stride = sh.cnt_stride;
+  a.err = s.err;
+  for (int l = 0; l < n_layers; ++l) {
+    const RmoeLayer& Ll = *layers[l];
+    if (Ll.H != L0.H || Ll.I != L0.I || Ll.n_routed != L0.n_routed || Ll.n_shared != L0.n_shared ||
+        Ll.top_k != L0.top_k || Ll.score != L0.score || Ll.renorm != L0.renorm || Ll.scaling != L0.scaling ||
+        !Ll.has_router)
+      return hipErrorInvalidValue;
+    a.gu[l] = Ll.gu;
+    a.dn[l] = Ll.dn;
+    a.rw[l] = Ll.router_w;
+    a.rb[l] = Ll.router_bias;
+  }
+  const size_t lds = dn_lds_bytes(sh.nkt2);
+  const dim3 grid(n_cu), block(kThreads);
+  const int pos_need = (kMaxDnUnits * sh.nkt2 + kWaves - 2) / (kWaves - 1);
+  if (pos_need <= 2 && a.E <= 128 && sh.nq1 <= 2)
+    hipLaunchKernelGGL((decode_stack_kernel<2, 1, 2>), grid, block, lds, st, a);
+  else if (pos_need <= 2 && a.E <= 128)
+    hipLaunchKernelGGL((decode_stack_kernel<2, 1, 4>), grid, block, lds, st, a);
+  else if (a.E <= 128)
+    hipLaunchKernelGGL((decode_stack_kernel<4, 1, 4>), grid, block, lds, st, a);
+  else
+    hipLaunchKernelGGL((decode_stack_kernel<4, 2, 4>), grid, block, lds, st, a);
+  return hipGetLastError();
+}
+
+// Allow the largest dynamic LDS any instance takes, then report the resident workgroups
+// per CU of the most demanding instance at that size.
+hipError_t decode_stack_occupancy(int* blocks_per_cu) {
+  const int dyn = (int)(kLdsLimit - kStaticLds);
+  const void* fns[4] = {(const void*)decode_stack_kernel<2, 1, 2>, (const void*)decode_stack_kernel<2, 1, 4>,
+                        (const void*)decode_stack_kernel<4, 1, 4>, (const void*)decode_stack_kernel<4, 2, 4>};
+  int best = 1 << 30;
+  for (const void* f : fns) {
+    hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, dyn);
+    if (e != hipSuccess) return e;
+    int v = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, f, kThreads, dyn);
+    if (e != hipSuccess) return e;
+    best = v < best ? v : best;
+  }
+  *blocks_per_cu = best;
+  return hipSuccess;
+}
+
+}  // namespace rmoe

@@ -94,6 +94,8 @@ void linear_needs(int M, int K, int T, size_t& floats, size_t& counters) {
   counters = ych * n_rt;
 }
 
+int reserve_stack(rmoe_ctx* ctx, const RmoeLayer& L, int n_layers);
+
 // Size every scratch buffer for `layer` with up to T tokens and k routes.
 int reserve_layer(rmoe_ctx* ctx, const RmoeLayer& L, int T, int k) {
   RmoeScratch& s = ctx->s;
@@ -125,7 +127,17 @@ int reserve_layer(rmoe_ctx* ctx, const RmoeLayer& L, int T, int k) {
   s.order_elems = oe;
   TRY(grow(s.offsets, s.offset_elems, 257, ctx));
   if (L.n_shared > 0) TRY(grow(s.pf, s.pf_bytes, rmoe::prefill_scratch_bytes(Lk, T), ctx));
+  if (L.n_shared > 0) TRY(reserve_stack(ctx, L, 1));
   s.max_tokens = std::max(s.max_tokens, T);
+  return RMOE_OK;
+}
+
+// Hand-off buffers and counters of the persistent decode kernel for n_layers layers of
+// L's geometry.  Counters are zero when (re)allocated and after every complete launch.
+int reserve_stack(rmoe_ctx* ctx, const RmoeLayer& L, int n_layers) {
+  RmoeScratch& s = ctx->s;
+  TRY(grow(s.stack, s.stack_bytes, rmoe::stack_scratch_bytes(L, n_layers), ctx));
+  TRY(grow(s.stack_cnt, s.stack_cnt_n, rmoe::stack_counter_count(L, n_layers), ctx));
   return RMOE_OK;
 }
 
@@ -139,6 +151,15 @@ int sync_and_check(rmoe_ctx* ctx, hipStream_t st) {
     if (err & 1) return fail(RMOE_EINVAL, "Input weight matrix contains non-finite values (NaN or Inf)");
     if (err & 2) return fail(RMOE_EINVAL, "Quantization parameters (scale_q or min_q) overflowed to non-finite values");
     if (err & 4) return fail(RMOE_EINVAL, "expert id out of range in dispatch");
+    if (err & 8) {
+      // A wait of the persistent decode kernel timed out: its counters are left
+      // mid-way; clear them for the next launch.
+      if (ctx->s.stack_cnt) {
+        HIP_TRY(hipMemsetAsync(ctx->s.stack_cnt, 0, ctx->s.stack_cnt_n * sizeof(unsigned), ctx->stream));
+        HIP_TRY(hipStreamSynchronize(ctx->stream));
+      }
+      return fail(RMOE_EDEVICE, "persistent decode kernel timed out waiting for other workgroups");
+    }
     return fail(RMOE_EDEVICE, "device error flag 0x%x", err);
   }
   return RMOE_OK;
@@ -183,6 +204,12 @@ int rmoe_create(int device, rmoe_ctx** out) {
   }
   hipMemsetAsync(ctx->s.err, 0, sizeof(int), ctx->stream);
   hipStreamSynchronize(ctx->stream);
+  // The persistent decode kernel runs one workgroup per CU and needs all of them
+  // resident at once.
+  int n_cu = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess &&
+      rmoe::decode_stack_occupancy(&per_cu) == hipSuccess && per_cu >= 1)
+    ctx->n_cu = n_cu;
   *out = ctx;
   return RMOE_OK;
 }
@@ -200,7 +227,7 @@ int rmoe_destroy(rmoe_ctx* ctx) {
   }
   RmoeScratch& s = ctx->s;
   void* bufs[] = {s.part, s.counters, s.h, s.dout, s.ids, s.wts, s.logits, s.order, s.inv, s.offsets,
-                  s.chunk_counts, s.err, s.staging, s.pf};
+                  s.chunk_counts, s.err, s.staging, s.pf, s.stack, s.stack_cnt};
   for (void* b : bufs)
     if (b) hipFree(b);
   auto it = g_io.find(ctx);
@@ -567,25 +594,83 @@ int rmoe_moe_experts(rmoe_ctx* ctx, int layer, const uint16_t* x, const int32_t*
   return RMOE_OK;
 }
 
-int rmoe_moe_decode_dev(rmoe_ctx* ctx, int layer, const void* x_dev, void* out_dev, int residual, int act,
-                        float gate_beta, float value_beta, void* top_ids_dev, void* top_weights_dev, void* stream) {
-  RmoeLayer* L;
-  TRY(check_layer(ctx, layer, &L));
-  if (!L->has_router) return fail(RMOE_EINVAL, "layer %d has no router", layer);
-  if (L->n_shared < 1) return fail(RMOE_EINVAL, "layer %d has no shared expert", layer);
+// Validate a list of decode layers for the persistent kernel; fills ptrs.
+static int stack_layers(rmoe_ctx* ctx, const int* layers, int n_layers, std::vector<const RmoeLayer*>& ptrs) {
+  if (!ctx) return fail(RMOE_EINVAL, "null context");
+  if (!layers || n_layers < 1 || n_layers > rmoe::kMaxStack)
+    return fail(RMOE_EINVAL, "n_layers (%d) must be in 1..%d", n_layers, rmoe::kMaxStack);
+  if (ctx->n_cu < 1) return fail(RMOE_EDEVICE, "the persistent decode kernel cannot be resident on this device");
+  ptrs.clear();
+  for (int i = 0; i < n_layers; ++i) {
+    RmoeLayer* L;
+    TRY(check_layer(ctx, layers[i], &L));
+    if (!L->has_router) return fail(RMOE_EINVAL, "layer %d has no router", layers[i]);
+    if (L->n_shared < 1) return fail(RMOE_EINVAL, "layer %d has no shared expert", layers[i]);
+    if (!ptrs.empty()) {
+      const RmoeLayer& F = *ptrs[0];
+      if (L->H != F.H || L->I != F.I || L->n_routed != F.n_routed || L->top_k != F.top_k || L->score != F.score ||
+          L->renorm != F.renorm || L->scaling != F.scaling)
+        return fail(RMOE_EINVAL, "layer %d differs in shape or router settings from layer %d", layers[i], layers[0]);
+    }
+    ptrs.push_back(L);
+  }
+  if (rmoe::stack_check(*ptrs[0], ctx->n_cu) != hipSuccess)
+    return fail(RMOE_EINVAL, "layer shape (H=%d, I=%d, experts=%d, k=%d) exceeds the persistent decode kernel's limits",
+                ptrs[0]->H, ptrs[0]->I, ptrs[0]->n_routed, ptrs[0]->top_k);
+  return RMOE_OK;
+}
+
+int rmoe_reserve_decode_stack(rmoe_ctx* ctx, const int* layers, int n_layers) {
+  std::vector<const RmoeLayer*> ptrs;
+  TRY(stack_layers(ctx, layers, n_layers, ptrs));
+  HIP_TRY(hipSetDevice(ctx->device));
+  return reserve_stack(ctx, *ptrs[0], n_layers);
+}
+
+int rmoe_moe_decode_stack_dev(rmoe_ctx* ctx, const int* layers, int n_layers, const void* x_dev, void* out_dev,
+                              int residual, int act, float gate_beta, float value_beta, void* top_ids_dev,
+                              void* top_weights_dev, void* stream) {
+  std::vector<const RmoeLayer*> ptrs;
+  TRY(stack_layers(ctx, layers, n_layers, ptrs));
   if (!x_dev || !out_dev) return fail(RMOE_EINVAL, "null argument");
   if (act != RMOE_ACT_SITU && act != RMOE_ACT_SWIGLU) return fail(RMOE_EINVAL, "unknown activation %d", act);
   hipStream_t st = pick_stream(ctx, stream);
-  int32_t* ids = top_ids_dev ? (int32_t*)top_ids_dev : ctx->s.ids;
-  float* wts = top_weights_dev ? (float*)top_weights_dev : ctx->s.wts;
-  if ((size_t)L->top_k > ctx->s.route_elems || (size_t)L->n_routed > ctx->s.logit_elems)
-    return fail(RMOE_EINVAL, "scratch not reserved for layer %d", layer);
-  HIP_TRY(rmoe::launch_route(*L, (const uint16_t*)x_dev, 1, ids, wts, ctx->s.logits, ctx->s, st));
-  hipError_t e = rmoe::launch_moe_decode(*L, (const uint16_t*)x_dev, ids, wts, L->top_k, true, act, gate_beta,
-                                         value_beta, residual != 0, (uint16_t*)out_dev, nullptr, ctx->s, st);
-  if (e == hipErrorInvalidValue) return fail(RMOE_EINVAL, "scratch too small for layer %d: call rmoe_reserve", layer);
+  hipError_t e = rmoe::launch_decode_stack(ptrs.data(), n_layers, (const uint16_t*)x_dev, (uint16_t*)out_dev,
+                                           residual != 0, act, gate_beta, value_beta, (int32_t*)top_ids_dev,
+                                           (float*)top_weights_dev, ctx->s, ctx->n_cu, st);
+  if (e == hipErrorInvalidValue)
+    return fail(RMOE_EINVAL, "decode stack scratch too small for %d layers: call rmoe_reserve_decode_stack", n_layers);
   HIP_TRY(e);
   return RMOE_OK;
+}
+
+int rmoe_moe_decode_stack(rmoe_ctx* ctx, const int* layers, int n_layers, const uint16_t* x, uint16_t* out,
+                          int residual, int act, float gate_beta, float value_beta, int32_t* top_ids,
+                          float* top_weights) {
+  std::vector<const RmoeLayer*> ptrs;
+  TRY(stack_layers(ctx, layers, n_layers, ptrs));
+  if (!x || !out) return fail(RMOE_EINVAL, "null argument");
+  HIP_TRY(hipSetDevice(ctx->device));
+  TRY(reserve_stack(ctx, *ptrs[0], n_layers));
+  const RmoeLayer& L = *ptrs[0];
+  const size_t xb = align_up((size_t)L.H * 2, 256), rb = align_up((size_t)n_layers * L.top_k * 4, 256);
+  uint8_t* io;
+  TRY(io_area(ctx, 2 * xb + 2 * rb, &io));
+  HIP_TRY(hipMemcpyAsync(io, x, (size_t)L.H * 2, hipMemcpyHostToDevice, ctx->stream));
+  TRY(rmoe_moe_decode_stack_dev(ctx, layers, n_layers, io, io + xb, residual, act, gate_beta, value_beta,
+                                io + 2 * xb, io + 2 * xb + rb, nullptr));
+  TRY(sync_and_check(ctx, ctx->stream));
+  HIP_TRY(hipMemcpy(out, io + xb, (size_t)L.H * 2, hipMemcpyDeviceToHost));
+  if (top_ids) HIP_TRY(hipMemcpy(top_ids, io + 2 * xb, (size_t)n_layers * L.top_k * 4, hipMemcpyDeviceToHost));
+  if (top_weights)
+    HIP_TRY(hipMemcpy(top_weights, io + 2 * xb + rb, (size_t)n_layers * L.top_k * 4, hipMemcpyDeviceToHost));
+  return RMOE_OK;
+}
+
+int rmoe_moe_decode_dev(rmoe_ctx* ctx, int layer, const void* x_dev, void* out_dev, int residual, int act,
+                        float gate_beta, float value_beta, void* top_ids_dev, void* top_weights_dev, void* stream) {
+  return rmoe_moe_decode_stack_dev(ctx, &layer, 1, x_dev, out_dev, residual, act, gate_beta, value_beta, top_ids_dev,
+                                   top_weights_dev, stream);
 }
 
 int rmoe_moe_decode_stage_dev(rmoe_ctx* ctx, int layer, int stage, const void* x_dev, void* out_dev, int residual,
@@ -613,21 +698,7 @@ int rmoe_moe_decode_stage_dev(rmoe_ctx* ctx, int layer, int stage, const void* x
 
 int rmoe_moe_decode(rmoe_ctx* ctx, int layer, const uint16_t* x, uint16_t* out, int residual, int act,
                     float gate_beta, float value_beta, int32_t* top_ids, float* top_weights) {
-  RmoeLayer* L;
-  TRY(check_layer(ctx, layer, &L));
-  if (!x || !out) return fail(RMOE_EINVAL, "null argument");
-  HIP_TRY(hipSetDevice(ctx->device));
-  TRY(reserve_layer(ctx, *L, 1, L->top_k));
-  const size_t xb = align_up((size_t)L->H * 2, 256);
-  uint8_t* io;
-  TRY(io_area(ctx, 2 * xb, &io));
-  HIP_TRY(hipMemcpyAsync(io, x, (size_t)L->H * 2, hipMemcpyHostToDevice, ctx->stream));
-  TRY(rmoe_moe_decode_dev(ctx, layer, io, io + xb, residual, act, gate_beta, value_beta, nullptr, nullptr, nullptr));
-  HIP_TRY(hipMemcpyAsync(out, io + xb, (size_t)L->H * 2, hipMemcpyDeviceToHost, ctx->stream));
-  if (top_ids) HIP_TRY(hipMemcpyAsync(top_ids, ctx->s.ids, (size_t)L->top_k * 4, hipMemcpyDeviceToHost, ctx->stream));
-  if (top_weights) HIP_TRY(hipMemcpyAsync(top_weights, ctx->s.wts, (size_t)L->top_k * 4, hipMemcpyDeviceToHost, ctx->stream));
-  HIP_TRY(hipStreamSynchronize(ctx->stream));
-  return RMOE_OK;
+  return rmoe_moe_decode_stack(ctx, &layer, 1, x, out, residual, act, gate_beta, value_beta, top_ids, top_weights);
 }
 
 int rmoe_dispatch(rmoe_ctx* ctx, const int32_t* top_ids, int T, int k, int n_experts, int32_t* order, int32_t* offsets) {

@@ -217,10 +217,16 @@ struct RmoeScratch {
   uint8_t* staging = nullptr;    // upload staging
   size_t staging_bytes = 0;
   int max_tokens = 0;
+  // persistent decode stack (moe_decode_stack.hip)
+  uint8_t* stack = nullptr;      // per-layer hand-off buffers
+  size_t stack_bytes = 0;
+  unsigned* stack_cnt = nullptr; // counters; zero between launches
+  size_t stack_cnt_n = 0;
 };
 
 struct rmoe_ctx {
   int device = 0;
+  int n_cu = 0;  // compute units: the grid of the persistent decode kernel
   hipStream_t stream = nullptr;
   std::map<int, RmoeMatrix> mats;
   int next_handle = 1;
@@ -267,6 +273,18 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
 hipError_t launch_router_gemm(const uint16_t* x, int T, int H, const uint16_t* w, int E, float* logits, hipStream_t st);
 hipError_t launch_topk(const float* logits, int T, int E, int k, int score, const float* bias, int renorm,
                        float scaling, int32_t* ids, float* wts, hipStream_t st);
+
+// Persistent decode of n_layers (<= kMaxStack) layers of one geometry for one token
+// (moe_decode_stack.hip).  One workgroup per CU (grid n_cu).  ids_out/wts_out: [n_layers, k]
+// or null.  Scratch: stack_scratch_bytes / stack_counter_count; counters must be zero.
+constexpr int kMaxStack = 64;
+size_t stack_scratch_bytes(const RmoeLayer& L, int n_layers);
+size_t stack_counter_count(const RmoeLayer& L, int n_layers);
+hipError_t stack_check(const RmoeLayer& L, int n_cu);
+hipError_t decode_stack_occupancy(int* blocks_per_cu);
+hipError_t launch_decode_stack(const RmoeLayer* const* layers, int n_layers, const uint16_t* x, uint16_t* out,
+                               bool residual, int act, float gb, float vb, int32_t* ids_out, float* wts_out,
+                               RmoeScratch& s, int n_cu, hipStream_t st);
 
 // Scratch requirements (bytes) for the launch wrappers above.
 size_t decode_scratch_floats(const RmoeLayer& L);

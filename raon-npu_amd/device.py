@@ -103,6 +103,44 @@ class Context:
         call("rmoe_layer_create", self._h, int(layer), geom.hidden, geom.inter, geom.n_routed, geom.n_shared, geom.top_k)
         return MoeLayer(self, int(layer), geom)
 
+    # ------------------------------------------------------- decode stack --
+    @staticmethod
+    def _layer_ids(layers) -> np.ndarray:
+        ids = np.ascontiguousarray([l.layer if isinstance(l, MoeLayer) else int(l) for l in layers], dtype=np.int32)
+        if ids.size < 1:
+            raise ValueError("a decode stack needs at least one layer")
+        return ids
+
+    def reserve_decode_stack(self, layers):
+        """Size the hand-off buffers of the persistent decode kernel for these layers."""
+        ids = self._layer_ids(layers)
+        call("rmoe_reserve_decode_stack", self._h, ptr(ids), ids.size)
+
+    def decode_stack(self, layers, x, residual: bool = True, gate_beta=None, value_beta=None):
+        """One token through every layer in ``layers`` (one persistent launch).
+        Returns (out u16[H], top_ids int32[L, k], weights f32[L, k])."""
+        ids = self._layer_ids(layers)
+        lyr0 = layers[0] if isinstance(layers[0], MoeLayer) else None
+        xa = _u16(x, "x").reshape(-1)
+        k = lyr0.geom.top_k if lyr0 else None
+        if k is None:
+            raise ValueError("decode_stack takes MoeLayer objects")
+        act, gb, vb = act_code(gate_beta, value_beta)
+        out = np.empty(xa.size, np.uint16)
+        top = np.empty((ids.size, k), np.int32)
+        w = np.empty((ids.size, k), np.float32)
+        call("rmoe_moe_decode_stack", self._h, ptr(ids), ids.size, ptr(xa), ptr(out), int(bool(residual)), act, gb, vb,
+             ptr(top), ptr(w))
+        return out, top, w
+
+    def decode_stack_dev(self, layers, x_dev, out_dev, residual: bool = True, gate_beta=None, value_beta=None,
+                         ids_dev=None, wts_dev=None, stream=None):
+        """Device-pointer form of ``decode_stack`` (no allocation; capturable in a HIP graph)."""
+        ids = self._layer_ids(layers)
+        act, gb, vb = act_code(gate_beta, value_beta)
+        call("rmoe_moe_decode_stack_dev", self._h, ptr(ids), ids.size, ptr(x_dev), ptr(out_dev), int(bool(residual)),
+             act, gb, vb, ptr(ids_dev), ptr(wts_dev), _stream_ptr(stream))
+
     def dispatch(self, top_ids, n_experts: int) -> tuple[np.ndarray, np.ndarray]:
         ids = np.ascontiguousarray(top_ids, dtype=np.int32)
         if ids.ndim != 2:

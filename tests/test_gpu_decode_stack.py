@@ -1,0 +1,242 @@
+"""GPU: the persistent decode kernel over a stack of MoE layers (BASELINE config 4 path).
+
+One launch carries a token through every layer: router, top-k, routed + shared experts,
+ordered combine and residual add per layer.  Checked against the oracle's
+``residual_stack`` (routing of every layer bit-exact unless the k/k+1 selection gap is a
+near-tie; hidden state within the bf16-ulp bound of the residual stream), against
+layer-by-layer launches of the same kernel (bit-identical), and under HIP-graph replay.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import raon_npu_amd.geometry as G
+from oracle import moe as om
+from oracle.bf16 import bf16_to_f32, f32_to_bf16
+
+from moe_fixtures import make_layer, random_tokens
+
+pytestmark = pytest.mark.gpu
+
+TOL_ABS, TOL_REL = 1e-2, 1e-3
+MARGIN = 1e-6
+
+
+def _check_ulp(out, ref, label):
+    """Residual-stream values reach |x| >= 2, where one bf16 ulp exceeds the 1e-2 max-abs bar:
+    the bound is max(1e-2, two ulps of the reference value), with rel-L2 <= 1e-3."""
+    a = bf16_to_f32(out).astype(np.float64)
+    b = bf16_to_f32(ref).astype(np.float64)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(b), 1e-30))) - 7)
+    bound = np.maximum(TOL_ABS, 2 * ulp)
+    rel = np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30)
+    print(f"{label}: max |d|/bound {np.max(np.abs(a - b) / bound):.3f} rel-L2 {rel:.3e} "
+          f"bit-identical {np.mean(out == ref):.4f}")
+    assert np.all(np.abs(a - b) <= bound) and rel <= TOL_REL, label
+
+
+def _oracle_stack(oracle_layers, x, gate_beta=None, value_beta=None):
+    """Per layer: (top ids, selection margin) and the final hidden state (om.residual_stack)."""
+    h = np.asarray(x, dtype=np.uint16)
+    routes = []
+    for lyr in oracle_layers:
+        out, top, _, logits = om.moe_token(lyr.bank, lyr.router, h, gate_beta, value_beta, lyr.shared_id,
+                                           lyr.router_f32())
+        sc = om.router_scores(logits, lyr.router.score)
+        choice = sc if lyr.router.bias is None else sc + lyr.router.bias
+        s = np.sort(choice)[::-1]
+        routes.append((top, float(s[lyr.router.top_k - 1] - s[lyr.router.top_k])))
+        h = f32_to_bf16(bf16_to_f32(h) + bf16_to_f32(out))
+    return h, routes
+
+
+def _small_stack(ctx, n, base, geom=None, score="softmax", bias_seed=None, scaling=1.0):
+    geom = geom or G.MoeGeometry(hidden=512, inter=256, n_routed=16, n_shared=1, top_k=4)
+    layers, oracle_layers = [], []
+    for li in range(n):
+        bias = None
+        if bias_seed is not None:
+            bias = (np.random.default_rng(bias_seed + li).standard_normal(geom.n_routed) * 0.01).astype(np.float32)
+        syn = make_layer(geom, seed=base + li, score=score, bias=bias)
+        lyr = ctx.create_layer(base + li, geom)
+        lyr.upload_experts(syn.gate_up, syn.down)
+        lyr.set_router(syn.router, bias=bias, score=score, scaling=scaling)
+        layers.append(lyr)
+        ol = syn.oracle_layer()
+        ol.router.scaling = scaling
+        oracle_layers.append(ol)
+    return geom, layers, oracle_layers
+
+
+def test_stack_matches_oracle(gpu_ctx):
+    """Eight layers of a small geometry in one launch.  The launch equals eight chained
+    1-layer launches bit for bit; every 1-layer launch matches the oracle on the same
+    input (routing exact, output within the bar); the first four layers also match the
+    free-running oracle stack.  (Free-running over all eight layers, single bf16 rounding
+    flips compound through the residual stream past rel-L2 1e-3.)"""
+    import torch
+
+    geom, layers, oracle_layers = _small_stack(gpu_ctx, 8, 1200)
+    gpu_ctx.reserve_decode_stack(layers)
+    xs = random_tokens(5, geom.hidden, 1210)
+    s = torch.cuda.current_stream()
+    for t, x in enumerate(xs):
+        out, top, _ = gpu_ctx.decode_stack(layers, x, residual=True)
+        h = x
+        for li, (lyr, ol) in enumerate(zip(layers, oracle_layers)):
+            got, ids, _ = lyr.moe_decode(h, residual=True)
+            ref, rtop, _, logits = om.moe_token(ol.bank, ol.router, h, None, None, ol.shared_id, ol.router_f32())
+            ref = f32_to_bf16(bf16_to_f32(h) + bf16_to_f32(ref))
+            sc = om.router_scores(logits, "softmax")
+            srt = np.sort(sc)[::-1]
+            if srt[geom.top_k - 1] - srt[geom.top_k] > MARGIN:
+                assert ids.tolist() == rtop.tolist() == top[li].tolist(), (t, li)
+            _check_ulp(got, ref, f"token {t} layer {li}")
+            h = got
+        assert np.array_equal(out, h), f"token {t}: stack differs from chained layers"
+        ref4, routes = _oracle_stack(oracle_layers[:4], x)
+        out4, top4, _ = gpu_ctx.decode_stack(layers[:4], x, residual=True)
+        for li, (rtop, margin) in enumerate(routes):
+            if margin > MARGIN:
+                assert top4[li].tolist() == rtop.tolist(), (t, li)
+        _check_ulp(out4, ref4, f"4-layer stack token {t}")
+    for lyr in layers:
+        lyr.free()
+
+
+def test_stack_equals_layer_by_layer(gpu_ctx):
+    """BASELINE geometry: a 6-layer launch is bit-identical to six 1-layer launches."""
+    import torch
+
+    geom = G.BASELINE
+    layers = []
+    for li in range(6):
+        lyr = gpu_ctx.create_layer(1300 + li, geom)
+        lyr.synthesize(77 + li, 0.02)
+        gen = torch.Generator(device="cuda").manual_seed(1300 + li)
+        rw = (torch.randn(geom.n_routed, geom.hidden, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+        lyr.set_router(rw.contiguous(), score="softmax")
+        layers.append(lyr)
+    gpu_ctx.reserve_decode_stack(layers)
+    x = random_tokens(3, geom.hidden, 1310)
+    s = torch.cuda.current_stream()
+    for t in range(3):
+        h = torch.from_numpy(x[t].view(np.int16)).cuda()
+        ids_l = torch.empty((6, geom.top_k), dtype=torch.int32, device="cuda")
+        for li, lyr in enumerate(layers):
+            nxt = torch.empty_like(h)
+            lyr.moe_decode_dev(h, nxt, residual=True, ids_dev=ids_l[li], stream=s)
+            h = nxt
+        out = torch.empty_like(h)
+        ids_s = torch.empty((6, geom.top_k), dtype=torch.int32, device="cuda")
+        x_dev = torch.from_numpy(x[t].view(np.int16)).cuda()
+        gpu_ctx.decode_stack_dev(layers, x_dev, out, residual=True, ids_dev=ids_s, stream=s)
+        torch.cuda.synchronize()
+        assert torch.equal(ids_s, ids_l)
+        assert torch.equal(out, h), f"token {t}: stack differs from layer-by-layer"
+    for lyr in layers:
+        lyr.free()
+
+
+def test_stack_baseline_matches_oracle(gpu_ctx):
+    """BASELINE shape (H=2048, I=768, 128 + 1 experts, softmax top-8), 3 layers: the launch
+    equals the chained 1-layer launches, and each layer matches the oracle on its input."""
+    import torch
+
+    geom = G.BASELINE
+    layers, oracle_layers = [], []
+    for li in range(3):
+        lyr = gpu_ctx.create_layer(1400 + li, geom)
+        lyr.synthesize(500 + li, 0.02)
+        gen = torch.Generator(device="cuda").manual_seed(1400 + li)
+        rw = (torch.randn(geom.n_routed, geom.hidden, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+        router = rw.view(torch.int16).cpu().numpy().view(np.uint16)
+        lyr.set_router(router, score="softmax")
+        parts = [lyr.download_expert(e) for e in range(geom.n_experts)]
+        bank = om.ExpertBank(b"".join(p[0] for p in parts), b"".join(p[1] for p in parts), geom.n_experts,
+                             geom.hidden, geom.inter, cache=geom.n_experts)
+        oracle_layers.append(om.Layer(bank, om.RouterSpec(router, geom.top_k, score="softmax"), geom.shared_id))
+        layers.append(lyr)
+    gpu_ctx.reserve_decode_stack(layers)
+    for t, x in enumerate(random_tokens(2, geom.hidden, 1410)):
+        out, top, _ = gpu_ctx.decode_stack(layers, x, residual=True)
+        h = x
+        for li, (lyr, ol) in enumerate(zip(layers, oracle_layers)):
+            got, ids, _ = lyr.moe_decode(h, residual=True)
+            ref, routes = _oracle_stack([ol], h)
+            if routes[0][1] > MARGIN:
+                assert ids.tolist() == routes[0][0].tolist() == top[li].tolist(), (t, li)
+            _check_ulp(got, ref, f"baseline token {t} layer {li}")
+            h = got
+        assert np.array_equal(out, h), f"token {t}: stack differs from chained layers"
+    for lyr in layers:
+        lyr.free()
+
+
+def test_stack_reference_model_shape(gpu_ctx):
+    """The reference model's numerics (host/raon.py:1224-1247, host/backend.py:47-62): H=2560,
+    I=1088 (down input padded to 1280), top-6, sigmoid router with selection bias and
+    routed_scaling_factor 2.5, SiTU-GLU; 3 layers, 16 routed + shared experts."""
+    geom = G.MoeGeometry(hidden=2560, inter=1088, n_routed=16, n_shared=1, top_k=6)
+    geom, layers, oracle_layers = _small_stack(gpu_ctx, 3, 1500, geom=geom, score="sigmoid", bias_seed=1550,
+                                               scaling=2.5)
+    gpu_ctx.reserve_decode_stack(layers)
+    for t, x in enumerate(random_tokens(2, geom.hidden, 1510)):
+        out, top, _ = gpu_ctx.decode_stack(layers, x, residual=True, gate_beta=4.0, value_beta=25.0)
+        h = x
+        for li, (lyr, ol) in enumerate(zip(layers, oracle_layers)):
+            got, ids, _ = lyr.moe_decode(h, residual=True, gate_beta=4.0, value_beta=25.0)
+            ref, routes = _oracle_stack([ol], h, 4.0, 25.0)
+            if routes[0][1] > MARGIN:
+                assert ids.tolist() == routes[0][0].tolist() == top[li].tolist(), (t, li)
+            _check_ulp(got, ref, f"reference-shape token {t} layer {li}")
+            h = got
+        assert np.array_equal(out, h), f"token {t}: stack differs from chained layers"
+    for lyr in layers:
+        lyr.free()
+
+
+def test_stack_graph_replays_match_eager(gpu_ctx):
+    """Captured in a HIP graph: every replay equals an eager launch (counters are cleared by
+    the kernel itself, so replays need no memset node)."""
+    import torch
+
+    geom, layers, _ = _small_stack(gpu_ctx, 4, 1600)
+    gpu_ctx.reserve_decode_stack(layers)
+    xs = torch.from_numpy(random_tokens(4, geom.hidden, 1610).view(np.int16)).cuda()
+    x = xs[0].clone()
+    out = torch.empty_like(x)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            gpu_ctx.decode_stack_dev(layers, x, out, residual=True, stream=s)
+    torch.cuda.current_stream().wait_stream(s)
+    eager = torch.empty_like(x)
+    for r in range(4):
+        x.copy_(xs[r])
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        gpu_ctx.decode_stack_dev(layers, xs[r], eager, residual=True, stream=torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {r}"
+    for lyr in layers:
+        lyr.free()
+
+
+def test_stack_rejects_mixed_geometry(gpu_ctx):
+    a = gpu_ctx.create_layer(1700, G.MoeGeometry(hidden=512, inter=256, n_routed=16, n_shared=1, top_k=4))
+    b = gpu_ctx.create_layer(1701, G.MoeGeometry(hidden=512, inter=128, n_routed=16, n_shared=1, top_k=4))
+    rng = np.random.default_rng(0)
+    for lyr in (a, b):
+        lyr.set_router(f32_to_bf16(rng.standard_normal((16, 512)).astype(np.float32) * 0.02), score="softmax")
+    with pytest.raises(ValueError):
+        gpu_ctx.reserve_decode_stack([a, b])
+    with pytest.raises(KeyError):
+        gpu_ctx.reserve_decode_stack([a, 123456])
+    a.free()
+    b.free()
