@@ -29,6 +29,11 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+# HBM bytes per launch of the decode stack kernel measured with rocprofv3 FETCH_SIZE and
+# WRITE_SIZE (calibrated against a 512 MiB copy) over `bench.py --profile-pass`; the
+# summary and commands are in profiles/decode_prefill_hbm_counters.txt.  Re-measure
+# after changing the kernel.
+DECODE_TRAFFIC_BYTES = 1364872343
 
 
 def log(msg: str) -> None:
@@ -48,6 +53,9 @@ def parse_args():
     ap.add_argument("--prefill-reps", type=int, default=10)
     ap.add_argument("--zipf-tau", type=float, default=0.02)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="short run for hardware counters: 2 decode launches, 1 prefill layer and a "
+                         "512 MiB device copy (the calibration kernel of known size); prints no JSON")
     return ap.parse_args()
 
 
@@ -174,6 +182,34 @@ def cpu_baseline(lyr, geom, budget_s: float, seed: int):
     return per_layer, n, threads
 
 
+def profile_pass(ctx, layers, geom, args, stream, gen) -> int:
+    """A short, fixed sequence of kernels for per-dispatch hardware counters: a plain
+    device copy of 512 MiB (twice; its FETCH_SIZE / WRITE_SIZE per dispatch calibrate the
+    counters against a known byte count), two decode launches of the 48-layer stack and
+    one prefill layer of config 5."""
+    import torch
+
+    n = 512 * 1024 * 1024
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    x = torch.randn(2, geom.hidden, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
+    out = torch.empty_like(x)
+    ctx.reserve_decode_stack(layers)
+    for i in range(2):
+        ctx.decode_stack_dev(layers, x[i], out[i], residual=True, stream=stream)
+    torch.cuda.synchronize()
+    if not args.no_prefill:
+        prefill_bench(ctx, geom, args.prefill_tokens, args.seed, 1, args.zipf_tau, stream)
+    torch.cuda.synchronize()
+    log("profile pass done: copy 512 MiB x2, decode stack x2, prefill x1")
+    ctx.close()
+    return 0
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -197,6 +233,8 @@ def main() -> int:
 
     stream = torch.cuda.Stream()
     gen = torch.Generator(device="cuda").manual_seed(args.seed + 7)
+    if args.profile_pass:
+        return profile_pass(ctx, layers, geom, args, stream, gen)
     n_launch = 32
     x_pool = torch.randn(n_launch, geom.hidden, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
     out_pool = torch.empty_like(x_pool)
@@ -287,7 +325,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": DECODE_TRAFFIC_BYTES if args.layers == 48 else None,
             "bytes_per_launch": nbytes,
             "us_per_launch": round(per_launch * 1e6, 3),
         },

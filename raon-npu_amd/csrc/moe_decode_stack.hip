@@ -495,28 +495,28 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
         if (2 * idx < Hp)
           xv[i] = l == 0 ? reinterpret_cast<const uint64_t*>(a.x0)[idx] : ld_hand_u64(xin + 2 * idx);
       }
+      // x_l into LDS first (the compiler keeps its loads in registers only briefly).
+#pragma unroll
+      for (int i = 0; i < kMaxH / 4 / kThreads; ++i) {
+        const int idx = tid + kThreads * i;
+        if (2 * idx < Hp) {
+          xs[2 * idx] = (uint32_t)xv[i];
+          xs[2 * idx + 1] = (uint32_t)(xv[i] >> 32);
+        }
+      }
       const int nbc = kLRow / a.Ep;  // bands per chunk
       float lacc = 0.f;
       for (int b0 = 0; b0 < a.nb2; b0 += nbc) {
         const int nf4 = (min(nbc, a.nb2 - b0) * a.Ep) / 4;
         const uint4* src = reinterpret_cast<const uint4*>(lpart + (size_t)b0 * a.Ep);
-        uint4 lv[kLRow / 4 / kThreads];
-#pragma unroll
-        for (int i = 0; i < kLRow / 4 / kThreads; ++i)
-          if (tid + kThreads * i < nf4) lv[i] = src[tid + kThreads * i];
-        if (b0 == 0) {
-#pragma unroll
-          for (int i = 0; i < kMaxH / 4 / kThreads; ++i) {
-            const int idx = tid + kThreads * i;
-            if (2 * idx < Hp) {
-              xs[2 * idx] = (uint32_t)xv[i];
-              xs[2 * idx + 1] = (uint32_t)(xv[i] >> 32);
-            }
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < kLRow / 4 / kThreads; ++i)
-          if (tid + kThreads * i < nf4) reinterpret_cast<uint4*>(lrow)[tid + kThreads * i] = lv[i];
+        uint4* dst = reinterpret_cast<uint4*>(lrow);
+        // Two 16-byte loads per thread (kLRow = 4096 floats), both issued before either store.
+        static_assert(kLRow / 4 == 2 * kThreads, "two 16-byte pieces per thread");
+        const bool h0 = tid < nf4, h1 = tid + kThreads < nf4;
+        const uint4 v0 = h0 ? src[tid] : make_uint4(0u, 0u, 0u, 0u);
+        const uint4 v1 = h1 ? src[tid + kThreads] : make_uint4(0u, 0u, 0u, 0u);
+        if (h0) dst[tid] = v0;
+        if (h1) dst[tid + kThreads] = v1;
         __syncthreads();
         if (tid < a.E) {
           // In band order; eight LDS reads in flight at a time.
@@ -704,8 +704,8 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
       __syncthreads();
       if (wave == 0) {
         // Expert outputs of both units, then both arrivals (issued together).
-        unsigned* cnt_d[kMaxDnUnits];
-        int nd = 0;
+        static_assert(kMaxDnUnits == 2, "two DN units per workgroup");
+        const bool has0 = dn_d[0][0] >= 0, has1 = dn_d[1][0] >= 0;
 #pragma unroll
         for (int d = 0; d < kMaxDnUnits; ++d) {
           if (dn_d[d][0] < 0) continue;
@@ -713,17 +713,19 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
 #pragma unroll
           for (int w = 1; w < kWaves; ++w) dd += red[w][d][lane];
           st_dev(&dout[(size_t)dn_d[d][0] * a.H + 64 * dn_d[d][1] + lane], bf16_round(dd));
-          cnt_d[nd++] = &c_band[dn_d[d][1]];
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_s_waitcnt(0);
-        unsigned prev[kMaxDnUnits] = {0u, 0u};
-        if (lane == 0)
-          for (int d = 0; d < nd; ++d)
-            prev[d] = __hip_atomic_fetch_add(cnt_d[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        for (int d = 0; d < kMaxDnUnits; ++d) {
-          const unsigned pv = __builtin_amdgcn_readfirstlane(prev[d]);
-          if (lane == 0) band_last_d[d] = (d < nd && pv + 1u == (unsigned)a.S) ? 1u : 0u;
+        unsigned prev0 = 0u, prev1 = 0u;
+        if (lane == 0) {
+          if (has0) prev0 = __hip_atomic_fetch_add(&c_band[dn_d[0][1]], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (has1) prev1 = __hip_atomic_fetch_add(&c_band[dn_d[1][1]], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        prev0 = __builtin_amdgcn_readfirstlane(prev0);
+        prev1 = __builtin_amdgcn_readfirstlane(prev1);
+        if (lane == 0) {
+          band_last_d[0] = (has0 && prev0 + 1u == (unsigned)a.S) ? 1u : 0u;
+          band_last_d[1] = (has1 && prev1 + 1u == (unsigned)a.S) ? 1u : 0u;
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
       }
