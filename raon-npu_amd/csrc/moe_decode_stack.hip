@@ -128,9 +128,21 @@ __device__ __forceinline__ float tile_dot(const TileRegs& r, const uint32_t* xw,
 }
 
 // Counters of layer l: [0] ready, [1, 1+S) slot, [1+S, 1+S+nb2) band, then pair[S*nb1].
-__device__ __forceinline__ unsigned* layer_cnt(const StackArgs& a, int l) { return a.cnt + (size_t)l * a.cnt_stride; }
-__device__ __forceinline__ unsigned* exit_cnt(const StackArgs& a) { return a.cnt + (size_t)a.L * a.cnt_stride; }
-__device__ __forceinline__ unsigned* abort_flag(const StackArgs& a) { return exit_cnt(a) + 1; }
+// Every counter sits on its own 256-byte line: atomics and polls on one line are served
+// one at a time at the memory side, and a layer's counters see hundreds of them.
+constexpr int kCntPad = 64;  // uint32 per counter line
+__device__ __forceinline__ unsigned* cnt_at(const StackArgs& a, int l, int i) {
+  return a.cnt + ((size_t)l * a.cnt_stride + i) * kCntPad;
+}
+// `ready` of a layer is kept in kReadyCopies copies: a band publishes to every copy and
+// workgroup g polls copy g % kReadyCopies, so 32 rather than 256 workgroups poll a line.
+constexpr int kReadyCopies = 8;
+__device__ __forceinline__ void publish_ready(const StackArgs& a, int l) {
+  for (int c = 0; c < kReadyCopies; ++c)
+    __hip_atomic_fetch_add(cnt_at(a, l, c), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned* exit_cnt(const StackArgs& a) { return cnt_at(a, a.L, 0); }
+__device__ __forceinline__ unsigned* abort_flag(const StackArgs& a) { return cnt_at(a, a.L, 1); }
 
 // Hand-off protocol.  Data handed to other workgroups is stored with device-scope
 // stores (st_dev); the storing wave waits until its stores are acknowledged
@@ -186,13 +198,13 @@ __device__ __forceinline__ bool block_arrive(unsigned* counter, unsigned n, unsi
   return last;
 }
 
-// Block-wide publication without a result: every wave waits for its own stores, then
-// thread 0 posts one arrival.
-__device__ __forceinline__ void block_publish(unsigned* counter) {
+// Block-wide publication of layer l's readiness share: every wave waits for its own
+// stores, then thread 0 posts one arrival to every copy of ready[l].
+__device__ __forceinline__ void block_publish_ready(const StackArgs& a, int l) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) publish_ready(a, l);
 }
 
 // Block-wide wait until *p >= target (thread 0 polls).  Bounded: after kSpinLimit polls
@@ -466,20 +478,20 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     load_router_slice<NIT>(a, a.rw[0], g, true, dummy, wv);
     __syncthreads();
     band_logits<NIT>(a, xband, wv, reinterpret_cast<float*>(a.scratch + a.off_lpart), g);
-    block_publish(&layer_cnt(a, 0)[0]);
+    block_publish_ready(a, 0);
   }
 
   for (int l = 0; l < a.L; ++l) {
-    unsigned* cl = layer_cnt(a, l);
-    unsigned* c_slot = cl + 1;
-    unsigned* c_band = cl + 1 + a.S;
+    unsigned* c_ready = cnt_at(a, l, g % kReadyCopies);
+    auto c_slot = [&](int s) { return cnt_at(a, l, kReadyCopies + s); };
+    auto c_band = [&](int b) { return cnt_at(a, l, kReadyCopies + a.S + b); };
     uint8_t* lay = a.scratch + (size_t)l * a.layer_bytes;
     const uint32_t* xin = reinterpret_cast<const uint32_t*>(lay);
     const float* lpart = reinterpret_cast<const float*>(lay + a.off_lpart);
     float* gpart = reinterpret_cast<float*>(lay + a.off_gpart);
     float* dout = reinterpret_cast<float*>(lay + a.off_dout);
 
-    if (!wait_geq(a, &cl[0], (unsigned)a.nb2, &flag)) return;
+    if (!wait_geq(a, c_ready, (unsigned)a.nb2, &flag)) return;
 
     // ---- x_l and the routing of this layer.  Every device-scope load of a thread is
     // issued before the first use, so the latencies overlap.
@@ -615,7 +627,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
         }
         st_dev(&gp[lane], sg);
         st_dev(&gp[64 + lane], su);
-        wave_arrive(&c_slot[s], false);
+        wave_arrive(c_slot(s), false);
       }
     };
     if (gu_d[0] >= 0) gu_unit(gu_d[0], gu_d[1], gu_d[2], gu_d[3], gu_d[4]);
@@ -636,8 +648,8 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     // ---- DN units, both of a workgroup at once, and the combine of a band by the last
     // slot to finish it.
     if (n_dn_t > 0) {
-      if (!wait_geq(a, &c_slot[dn_d[0][0]], gu_parts, &flag)) return;
-      if (dn_d[1][0] >= 0 && !wait_geq(a, &c_slot[dn_d[1][0]], gu_parts, &flag)) return;
+      if (!wait_geq(a, c_slot(dn_d[0][0]), gu_parts, &flag)) return;
+      if (dn_d[1][0] >= 0 && !wait_geq(a, c_slot(dn_d[1][0]), gu_parts, &flag)) return;
       if (wave > 0) {
         // h for columns 128kt + 2*lane (+1) of each of this wave's tiles: the GU partials
         // of both columns for every K part (64-bit loads, all issued before the sums),
@@ -718,8 +730,8 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
         __builtin_amdgcn_s_waitcnt(0);
         unsigned prev0 = 0u, prev1 = 0u;
         if (lane == 0) {
-          if (has0) prev0 = __hip_atomic_fetch_add(&c_band[dn_d[0][1]], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          if (has1) prev1 = __hip_atomic_fetch_add(&c_band[dn_d[1][1]], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (has0) prev0 = __hip_atomic_fetch_add(c_band(dn_d[0][1]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (has1) prev1 = __hip_atomic_fetch_add(c_band(dn_d[1][1]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         prev0 = __builtin_amdgcn_readfirstlane(prev0);
         prev1 = __builtin_amdgcn_readfirstlane(prev1);
@@ -778,7 +790,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
           __syncthreads();
           float* lnext = reinterpret_cast<float*>(lay + a.layer_bytes + a.off_lpart);
           band_logits<NIT>(a, xband, rwv[d], lnext, b);
-          block_publish(&layer_cnt(a, l + 1)[0]);
+          block_publish_ready(a, l + 1);
         }
         __syncthreads();  // xband / cmb are reused by the next band
       }
@@ -789,7 +801,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
   // itself out; the last workgroup out clears every counter for the next launch.
   if (block_arrive(exit_cnt(a), (unsigned)G, &flag)) {
     const int n = a.L * a.cnt_stride;
-    for (int i = tid; i < n; i += kThreads) st_dev_u32(&a.cnt[i], 0u);
+    for (int i = tid; i < n; i += kThreads) st_dev_u32(a.cnt + (size_t)i * kCntPad, 0u);
     if (tid == 0) {
       st_dev_u32(abort_flag(a), 0u);
       st_dev_u32(exit_cnt(a), 0u);
@@ -828,7 +840,7 @@ StackShape stack_shape(const RmoeLayer& L) {
   sh.off_dout = off;
   off += al256((size_t)sh.S * L.H * 4);
   sh.layer_bytes = off;
-  sh.cnt_stride = 1 + sh.S + sh.nb2;
+  sh.cnt_stride = kReadyCopies + sh.S + sh.nb2;
   return sh;
 }
 
@@ -841,7 +853,7 @@ size_t stack_scratch_bytes(const RmoeLayer& L, int n_layers) {
 }
 
 size_t stack_counter_count(const RmoeLayer& L, int n_layers) {
-  return (size_t)stack_shape(L).cnt_stride * n_layers + 2;
+  return ((size_t)stack_shape(L).cnt_stride * n_layers + 2) * kCntPad;
 }
 
 hipError_t stack_check(const RmoeLayer& L, int n_cu) {
