@@ -587,17 +587,22 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
       load_tile_or(ut, ok, pu, dummy, lane);
     }
     // DN tiles of both units, flattened as t = d * nkt2 + kt: wave 1 + t % 7 copies tile t
-    // into LDS slot t at its position t / 7.
+    // into LDS slot t at its position t / 7.  A workgroup with a GU unit issues them
+    // after its GU tiles have arrived, so the gate/up stream (on the critical path) does
+    // not share HBM with the down stream; the others issue them at once.
     const int n_dn_t = (dn_d[0][0] >= 0 ? a.nkt2 : 0) + (dn_d[1][0] >= 0 ? a.nkt2 : 0);
+    auto issue_dn = [&]() {
 #pragma unroll
-    for (int p = 0; p < DNPOS; ++p) {
-      const int t = wave - 1 + (kWaves - 1) * p;
-      const bool ok = wave > 0 && t < n_dn_t;
-      const int d = ok ? t / a.nkt2 : 0, kt = ok ? t % a.nkt2 : 0;
-      const uint8_t* W = dn_l + (size_t)sl.id[ok ? dn_d[d][0] : 0] * a.dn_bytes;
-      dma_tile(ok, W + ((size_t)dn_d[d][1] * a.nkt2 + kt) * kTileBytes, dummy, dn_lds + (size_t)t * kTileBytes,
-               dn_sink, lane);
-    }
+      for (int p = 0; p < DNPOS; ++p) {
+        const int t = wave - 1 + (kWaves - 1) * p;
+        const bool ok = wave > 0 && t < n_dn_t;
+        const int d = ok ? t / a.nkt2 : 0, kt = ok ? t % a.nkt2 : 0;
+        const uint8_t* W = dn_l + (size_t)sl.id[ok ? dn_d[d][0] : 0] * a.dn_bytes;
+        dma_tile(ok, W + ((size_t)dn_d[d][1] * a.nkt2 + kt) * kTileBytes, dummy, dn_lds + (size_t)t * kTileBytes,
+                 dn_sink, lane);
+      }
+    };
+    if (gu_d[0] < 0) issue_dn();
     uint4 rwv[kMaxDnUnits][NIT][2];
 #pragma unroll
     for (int d = 0; d < kMaxDnUnits; ++d)
@@ -630,7 +635,10 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
         wave_arrive(c_slot(s), false);
       }
     };
-    if (gu_d[0] >= 0) gu_unit(gu_d[0], gu_d[1], gu_d[2], gu_d[3], gu_d[4]);
+    if (gu_d[0] >= 0) {
+      gu_unit(gu_d[0], gu_d[1], gu_d[2], gu_d[3], gu_d[4]);
+      issue_dn();
+    }
     for (int u = g + G; u < a.n_gu; u += G) {
       const int s = u / (a.nb1 * a.nq1), rem = u % (a.nb1 * a.nq1);
       const int j = rem / a.nq1, q = rem % a.nq1;
