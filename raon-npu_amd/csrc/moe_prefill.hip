@@ -265,8 +265,6 @@ struct GemmArgs {
   float gb, vb;
 };
 
-constexpr int kXStride = 128 + 8;  // bf16 elements per LDS row (pad: 16 B)
-
 __device__ __forceinline__ int group_end(const GemmArgs& a, int e) {
   return e < a.n_routed ? a.offsets[e + 1] : a.shared_base + a.shared_rows;
 }
@@ -284,13 +282,54 @@ __device__ __forceinline__ const uint32_t* ssum_row(const GemmArgs& a, int e, in
   return a.ssum + (size_t)tok * G * 2;
 }
 
+// LDS ring of the grouped GEMM: per K step (128 columns) the workgroup's 128 activation
+// rows (256 B each, 16-byte chunks XOR-swizzled by row) and its four 64-row weight
+// tiles (copied verbatim), three steps deep.
+constexpr int kStages = 3;
+constexpr int kXBytes = kBM * 256;
+constexpr int kWBytes = 4 * kTileBytes;
+constexpr int kStageBytes = kXBytes + kWBytes;
+constexpr int kGemmLds = kStages * kStageBytes;  // 159,744 of the 163,840 bytes of a CU
+constexpr int kOutStride = 136;                  // bf16 per row of the epilogue staging tile
+
+// 16 bytes per lane from global memory straight into LDS: lane L writes lds + 16 L.
+// Written as inline assembly so that the compiler does not treat every later LDS read
+// as dependent on it (it would wait for all outstanding loads before each one); the
+// ring's own waits (ring_wait) order the copies.  M0 is saved and restored.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+      : "memory");
+}
+// Wait until at most `pending` of this wave's copies are in flight, then meet the
+// workgroup.  The count is an immediate, so each value is a branch of its own.
+__device__ __forceinline__ void ring_wait(int pending) {
+  switch (pending) {
+    case 7: asm volatile("s_waitcnt vmcnt(7) lgkmcnt(0)" ::: "memory"); break;
+    case 6: asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory"); break;
+  }
+  asm volatile("s_barrier" ::: "memory");
+}
+
 // Grid: n_tiles * tile_cap workgroups (rounded to a multiple of 8), 512 threads (8 waves).
-// A workgroup multiplies 128 sorted rows by 256 weight rows: gate/up mode takes 128
-// intermediate units (gate rows + the matching up rows), wave w units 128*nt + 16w..+15;
-// down mode takes 256 output rows, wave w rows 256*nt + 16w and 256*nt + 128 + 16w.
+// A workgroup multiplies 128 sorted rows by 256 weight rows; wave w takes rows
+// 64*(w&1)..+63 and a quarter of the weight rows (w>>1), as 4 x 4 MFMA fragments.
+//   gate/up: the workgroup takes intermediate units 128*nt..+127 (gate rows and the
+//            matching up rows); the wave's quarter is units 32*(w>>1)..+31, fragments
+//            0,1 = gate, 2,3 = up, so the activation and the 32-column group sums of h
+//            stay inside the wave.
+//   down:    the workgroup takes output rows 256*nt..+255, the wave 64*(w>>1)..+63.
+// K loop: a three-deep LDS ring filled by global->LDS copies; per K step one
+// barrier, then the copy for step kt+2 into the slot step kt-1 used.
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void grouped_gemm_kernel(GemmArgs a, int tile_cap) {
-  __shared__ __attribute__((aligned(16))) uint16_t xs[2][kBM * kXStride];
-  __shared__ float hsum[8][kBM];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kGemmLds];
   // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs; make each XCD
   // take a contiguous range of (n-tile, m-tile) so m-tiles sharing a weight tile meet
   // in the same L2.
@@ -306,171 +345,136 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int nrows = min(kBM, rend - row0);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lq = lane >> 4;
+  const int wm = wave & 1, wn = wave >> 1;
   const int nkt = a.K / kTileCols;
   const uint8_t* W = a.wbase + (size_t)e * a.wstride;
-  // The wave's two n-fragments: rows within the weight matrix.
-  int wrow[2];
-  if (a.mode == 0) {
-    wrow[0] = 128 * nt + 16 * wave;            // gate
-    wrow[1] = a.inter + 128 * nt + 16 * wave;  // up
-  } else {
-    wrow[0] = 256 * nt + 16 * wave;
-    wrow[1] = 256 * nt + 128 + 16 * wave;
-  }
-  // Gate/up: when I is not a multiple of 128 the last n-tile has waves past I; they
-  // read valid rows (unit 0) and store nothing.
-  const bool active = a.mode == 1 || 128 * nt + 16 * wave < a.inter;
-  if (!active) {
-    wrow[0] = 0;
-    wrow[1] = a.inter;
-  }
+  const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
 
-  // X staging: a K step is 128 rows x 128 columns = 2,048 16-byte pieces, 8 per thread.
-  // Global loads for step kt+1 go to registers at the top of step kt and are written
-  // to the other LDS buffer after the MFMA work, so their latency hides behind it.
-  int xoff[4];  // element offset of the thread's piece in a.src, or -1 past the group
+  // The workgroup's four 64-row weight bands.  Gate/up: gate bands 2nt, 2nt+1, up bands
+  // I/64 + 2nt, +1; a band past I (last n-tile when I % 128 != 0) reads band 0 instead
+  // and its results are not stored.
+  int band[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int r = (tid + 512 * q) >> 4;
-    xoff[q] = r < nrows ? (int)(src_row(a, e, row0 + r) - a.src) + 8 * ((tid + 512 * q) & 15) : -1;
-  }
-  auto load_x = [&](uint4 (&v)[4], int kt) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      v[q] = xoff[q] >= 0 ? *reinterpret_cast<const uint4*>(a.src + xoff[q] + kt * 128) : make_uint4(0u, 0u, 0u, 0u);
-  };
-  auto store_x = [&](const uint4 (&v)[4], int buf) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int piece = tid + 512 * q;
-      *reinterpret_cast<uint4*>(&xs[buf][(piece >> 4) * kXStride + 8 * (piece & 15)]) = v[q];
+  for (int t = 0; t < 4; ++t) {
+    if (a.mode == 0) {
+      const int gb_ = 2 * nt + (t & 1);
+      band[t] = 64 * gb_ < a.inter ? (t < 2 ? gb_ : a.inter / 64 + gb_) : 0;
+    } else {
+      band[t] = 4 * nt + t;
     }
-  };
-  // Weight fragments of one K tile for the wave's two n-fragments (codes + scale/min).
-  const uint8_t* wtile[2];
-  int r_in[2];
-#pragma unroll
-  for (int f = 0; f < 2; ++f) {
-    wtile[f] = W + (size_t)(wrow[f] / 64) * nkt * kTileBytes;
-    r_in[f] = wrow[f] % 64 + l16;
   }
-  auto load_w = [&](uint32_t (&code)[2][4], uint4 (&smv)[2], int kt) {
+  // Fragment f of this wave: weight tile ft[f] (0..3) and first row fr[f] inside it.
+  int ft[4], fr[4];
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
-      const uint8_t* tile = wtile[f] + (size_t)kt * kTileBytes;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) code[f][j] = *reinterpret_cast<const uint32_t*>(tile + j * 1024 + r_in[f] * 16 + 4 * lq);
-      smv[f] = *reinterpret_cast<const uint4*>(tile + kCodeBytes + r_in[f] * 16);
+  for (int f = 0; f < 4; ++f) {
+    if (a.mode == 0) {
+      ft[f] = (f < 2 ? 0 : 2) + (wn >> 1);
+      fr[f] = 32 * (wn & 1) + 16 * (f & 1);
+    } else {
+      ft[f] = wn;
+      fr[f] = 16 * f;
     }
-  };
+  }
+  const bool active = a.mode == 1 || 128 * nt + 32 * wn < a.inter;
 
-  f32x4_t acc[8][2];
+  // Copy descriptors.  Activations: copy q = wave + 8i (i < 4) fills LDS rows 4q..4q+3;
+  // lane L brings row 4q + L/16, chunk (L%16) ^ (row%16).  Rows past the tile read the
+  // tile's first row (their results are not stored).
+  const uint8_t* xg[4];
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    acc[m][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    acc[m][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < 4; ++i) {
+    const int q = wave + 8 * i, r = 4 * q + (lane >> 4);
+    const int c = (lane & 15) ^ (r & 15);
+    xg[i] = reinterpret_cast<const uint8_t*>(src_row(a, e, row0 + (r < nrows ? r : 0))) + 16 * c;
   }
-  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-
-  uint4 xv[4];
-  uint32_t code[2][4], code_n[2][4];
-  uint4 smv[2], smv_n[2];
-  load_x(xv, 0);
-  load_w(code, smv, 0);
-  store_x(xv, 0);
-  __syncthreads();
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < nkt;
-    if (more) {
-      load_x(xv, kt + 1);
-      load_w(code_n, smv_n, kt + 1);
-    }
-#pragma unroll 1  // one group at a time keeps 16 MFMA results live, not 64
-    for (int j = 0; j < 4; ++j) {
-      uint4 b[2];
-      float s16[2];
+  // Weights: copy v = wave + 8i (i < 3, v < 20) is 1 KB piece v%5 of tile v/5.
+  const int n_wcopy = wave < 4 ? 3 : 2;
+  const uint8_t* wg[3];
 #pragma unroll
-      for (int f = 0; f < 2; ++f) {
-        uint32_t p0, p1, p2, p3;
-        unpack_codes(code[f][j], p0, p1, p2, p3);
-        b[f] = make_uint4(p0, p1, p2, p3);
-        const uint32_t smw = j == 0 ? smv[f].x : (j == 1 ? smv[f].y : (j == 2 ? smv[f].z : smv[f].w));
-        s16[f] = 16.f * bf16_to_f32(smw & 0xffffu);
-      }
+  for (int i = 0; i < 3; ++i) {
+    const int v = min(wave + 8 * i, 19), t = v / 5, p = v % 5;
+    wg[i] = W + (size_t)band[t] * nkt * kTileBytes + 1024 * p + 16 * lane;
+  }
+  auto issue = [&](int kt) {
+    const uint32_t sb = lds0 + (uint32_t)((kt % kStages) * kStageBytes);
 #pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const uint4 av = *reinterpret_cast<const uint4*>(&xs[cur][(16 * m + l16) * kXStride + 32 * j + 8 * lq]);
+    for (int i = 0; i < 4; ++i) dma16(xg[i] + (size_t)kt * 256, sb + 1024u * (uint32_t)(wave + 8 * i));
 #pragma unroll
-        for (int f = 0; f < 2; ++f) {
-          const f32x4_t c = mfma16(av, b[f], zero);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[m][f][i] = fmaf(s16[f], c[i], acc[m][f][i]);
-        }
+    for (int i = 0; i < 3; ++i) {
+      if (i < n_wcopy) {
+        const int v = wave + 8 * i, t = v / 5, p = v % 5;
+        dma16(wg[i] + (size_t)kt * kTileBytes, sb + (uint32_t)(kXBytes + t * kTileBytes + 1024 * p));
       }
     }
-    if (more) {
-      store_x(xv, cur ^ 1);
-#pragma unroll
-      for (int f = 0; f < 2; ++f) {
-        smv[f] = smv_n[f];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) code[f][j] = code_n[f][j];
-      }
-    }
-    __syncthreads();
-  }
+  };
+  const int per_stage = 4 + n_wcopy;
 
-  // Correction: y += sum_g (min - 16*scale)[r, g] * S[m, g] over blocks of 32 groups,
-  // both factors split exactly into 3 bf16 parts; the 6 leading products are kept.
+  issue(0);
+  if (nkt > 1) issue(1);
+
+  // Correction first, while the first copies are in flight:
+  //   acc = sum_g (min - 16*scale)[r, g] * S[m, g]
+  // over blocks of 32 groups, both factors split exactly into 3 bf16 parts; the 6
+  // leading products are kept.
+  f32x4_t acc[4][4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int f = 0; f < 4; ++f) acc[m][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const int G = a.K / 32;
-  auto pack8 = [](const uint32_t* v) {
-    return make_uint4(v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16), v[6] | (v[7] << 16));
-  };
-  for (int g0 = 0; g0 < G; g0 += 32) {
-    uint4 bc[2][3];
+  const uint32_t* srow[4];
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
+  for (int m = 0; m < 4; ++m) {
+    const int r = 64 * wm + 16 * m + l16;
+    srow[m] = r < nrows ? ssum_row(a, e, row0 + r) : nullptr;
+  }
+  for (int g0 = 0; g0 < G; g0 += 32) {
+    const int gl = g0 + 8 * lq;  // the lane's first group; groups gl..gl+7
+    uint4 bc[4][3];
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      uint4 smw[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int kt = gl / 4 + h;
+        smw[h] = 4 * kt < G ? *reinterpret_cast<const uint4*>(W + ((size_t)band[ft[f]] * nkt + kt) * kTileBytes + kCodeBytes +
+                                                              (fr[f] + l16) * 16)
+                            : make_uint4(0u, 0u, 0u, 0u);
+      }
+      const uint32_t sv[8] = {smw[0].x, smw[0].y, smw[0].z, smw[0].w, smw[1].x, smw[1].y, smw[1].z, smw[1].w};
       uint32_t hv[8], mv[8], lv[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int g = g0 + 8 * lq + i;
-        float coef = 0.f;
-        if (g < G) {
-          const uint8_t* tile = wtile[f] + (size_t)(g / 4) * kTileBytes;
-          const uint32_t smw = *reinterpret_cast<const uint32_t*>(tile + kCodeBytes + r_in[f] * 16 + 4 * (g % 4));
-          const float sc = bf16_to_f32(smw & 0xffffu), mn = bf16_to_f32(smw >> 16);
-          coef = mn - 16.f * sc;
-        }
+        const float coef = bf16_to_f32(sv[i] >> 16) - 16.f * bf16_to_f32(sv[i] & 0xffffu);
         split3_bf16(coef, hv[i], mv[i], lv[i]);
       }
-      bc[f][0] = pack8(hv);
-      bc[f][1] = pack8(mv);
-      bc[f][2] = pack8(lv);
+      bc[f][0] = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
+      bc[f][1] = make_uint4(mv[0] | (mv[1] << 16), mv[2] | (mv[3] << 16), mv[4] | (mv[5] << 16), mv[6] | (mv[7] << 16));
+      bc[f][2] = make_uint4(lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16), lv[4] | (lv[5] << 16), lv[6] | (lv[7] << 16));
     }
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      // Keep each iteration's loads next to its MFMAs: hoisting all of them exhausts
-      // the register file.
-      __builtin_amdgcn_sched_barrier(0);
-      const int r = 16 * m + l16;
-      uint32_t sh[8], sm2[8], sl[8];
-      const uint32_t* sp = r < nrows ? ssum_row(a, e, row0 + r) : nullptr;
+    for (int m = 0; m < 4; ++m) {
+      // 8 groups x (hi|mid, lo) = 16 dwords; pairs of groups past G read as zero.
+      uint4 sv[4];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int g = g0 + 8 * lq + i;
-        uint32_t v0 = 0u, v1 = 0u;
-        if (sp && g < G) {
-          v0 = sp[2 * g];
-          v1 = sp[2 * g + 1];
-        }
-        sh[i] = v0 & 0xffffu;
-        sm2[i] = v0 >> 16;
-        sl[i] = v1 & 0xffffu;
-      }
-      const uint4 ah = pack8(sh), am = pack8(sm2), al = pack8(sl);
+      for (int h = 0; h < 4; ++h)
+        sv[h] = srow[m] && gl + 2 * h < G ? *reinterpret_cast<const uint4*>(srow[m] + 2 * (gl + 2 * h))
+                                          : make_uint4(0u, 0u, 0u, 0u);
+      uint4 ah, am, al;
+      ah.x = __builtin_amdgcn_perm(sv[0].z, sv[0].x, 0x05040100u);
+      ah.y = __builtin_amdgcn_perm(sv[1].z, sv[1].x, 0x05040100u);
+      ah.z = __builtin_amdgcn_perm(sv[2].z, sv[2].x, 0x05040100u);
+      ah.w = __builtin_amdgcn_perm(sv[3].z, sv[3].x, 0x05040100u);
+      am.x = __builtin_amdgcn_perm(sv[0].z, sv[0].x, 0x07060302u);
+      am.y = __builtin_amdgcn_perm(sv[1].z, sv[1].x, 0x07060302u);
+      am.z = __builtin_amdgcn_perm(sv[2].z, sv[2].x, 0x07060302u);
+      am.w = __builtin_amdgcn_perm(sv[3].z, sv[3].x, 0x07060302u);
+      al.x = __builtin_amdgcn_perm(sv[0].w, sv[0].y, 0x05040100u);
+      al.y = __builtin_amdgcn_perm(sv[1].w, sv[1].y, 0x05040100u);
+      al.z = __builtin_amdgcn_perm(sv[2].w, sv[2].y, 0x05040100u);
+      al.w = __builtin_amdgcn_perm(sv[3].w, sv[3].y, 0x05040100u);
 #pragma unroll
-      for (int f = 0; f < 2; ++f) {
+      for (int f = 0; f < 4; ++f) {
         f32x4_t c = acc[m][f];
         c = mfma16(al, bc[f][0], c);
         c = mfma16(am, bc[f][1], c);
@@ -483,44 +487,101 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   }
 
-  // Epilogue.  C layout: lane holds rows 16m + 4*lq + i, column l16 of the fragment.
-  if (a.mode == 0) {
-    const int col = 128 * nt + 16 * wave + l16;  // intermediate unit
+  // Main K loop:  acc += 16*scale[r, g] * sum_k x[m,k] (1 + n[r,k]/16)  per group g.
+  for (int kt = 0; kt < nkt; ++kt) {
+    ring_wait(kt + 1 < nkt ? per_stage : 0);
+    if (kt + 2 < nkt) issue(kt + 2);
+    const uint8_t* xs = lds + (kt % kStages) * kStageBytes;
+    const uint8_t* ws = xs + kXBytes;
+    float s16[4][4];
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
+    for (int f = 0; f < 4; ++f) {
+      const uint4 smv = *reinterpret_cast<const uint4*>(ws + ft[f] * kTileBytes + kCodeBytes + (fr[f] + l16) * 16);
+      s16[f][0] = 16.f * bf16_to_f32(smv.x & 0xffffu);
+      s16[f][1] = 16.f * bf16_to_f32(smv.y & 0xffffu);
+      s16[f][2] = 16.f * bf16_to_f32(smv.z & 0xffffu);
+      s16[f][3] = 16.f * bf16_to_f32(smv.w & 0xffffu);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint4 b[4], av[4];
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        const uint32_t code =
+            *reinterpret_cast<const uint32_t*>(ws + ft[f] * kTileBytes + j * 1024 + (fr[f] + l16) * 16 + 4 * lq);
+        unpack_codes(code, b[f].x, b[f].y, b[f].z, b[f].w);
+      }
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int r = 64 * wm + 16 * m + l16;
+        av[m] = *reinterpret_cast<const uint4*>(xs + r * 256 + 16 * ((4 * j + lq) ^ (r & 15)));
+      }
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+          const f32x4_t c = mfma16(av[m], b[f], f32x4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[m][f][i] = fmaf(s16[f][j], c[i], acc[m][f][i]);
+        }
+    }
+  }
+  // Every wave is past its last ring read: slots 0 and 1 become the output staging.
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  // Epilogue.  C layout: lane holds rows 16m + 4*lq + i (of the wave's 64), column l16
+  // of the fragment.  Results go through LDS so that global stores are 16-byte rows.
+  uint16_t* stage0 = reinterpret_cast<uint16_t*>(lds);
+  if (a.mode == 0) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 16 * m + 4 * lq + i;
-        const float g = bf16_round(acc[m][0][i]), u = bf16_round(acc[m][1][i]);
-        const uint32_t h = f32_to_bf16(act_apply(a.act, g, u, a.gb, a.vb));
-        if (active && r < nrows) a.out[(size_t)(row0 + r) * a.out_ld + col] = (uint16_t)h;
-        // Group sums of h: reduce the 16 columns of this wave, then 2 waves per group.
-        float hv = r < nrows ? bf16_to_f32(h) : 0.f;
+        const int r = 64 * wm + 16 * m + 4 * lq + i;
+        float hv = 0.f;
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+          const float g = bf16_round(acc[m][f][i]), u = bf16_round(acc[m][2 + f][i]);
+          const uint32_t h = f32_to_bf16(act_apply(a.act, g, u, a.gb, a.vb));
+          stage0[r * kOutStride + 32 * wn + 16 * f + l16] = (uint16_t)h;
+          hv += bf16_to_f32(h);
+        }
+        // The wave's 32 units are one group of h: reduce over the 16 lanes of l16.
 #pragma unroll
         for (int off = 8; off > 0; off >>= 1) hv += __shfl_xor(hv, off, 16);
-        if (l16 == 0) hsum[wave][r] = hv;
+        if (l16 == 0 && active && r < nrows)
+          store_split3(a.out_ssum + ((size_t)(row0 + r) * (a.out_ld / 32) + 4 * nt + wn) * 2, hv);
       }
     }
     __syncthreads();
-    // Group (32 columns) = waves {0,1} and {2,3}; 64*nt + 32*q is group 2*nt + q.
-    for (int idx = tid; idx < kBM * 4; idx += 512) {
-      const int r = idx >> 2, q = idx & 3;  // group 4*nt + q = waves 2q, 2q+1
-      if (r < nrows && 128 * nt + 32 * q < a.inter) {
-        const float s = hsum[2 * q][r] + hsum[2 * q + 1][r];
-        store_split3(a.out_ssum + ((size_t)(row0 + r) * (a.out_ld / 32) + 4 * nt + q) * 2, s);
-      }
+    // 128 rows x 16 chunks of 8 units.
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int cid = tid + 512 * q, r = cid >> 4, c = cid & 15;
+      if (r < nrows && 128 * nt + 8 * c < a.inter)
+        *reinterpret_cast<uint4*>(a.out + (size_t)(row0 + r) * a.out_ld + 128 * nt + 8 * c) =
+            *reinterpret_cast<const uint4*>(stage0 + r * kOutStride + 8 * c);
     }
   } else {
+    // Columns 0..127 of the 256 in slot 0, 128..255 in slot 1.
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
+    for (int m = 0; m < 4; ++m)
 #pragma unroll
-      for (int f = 0; f < 2; ++f) {
+      for (int f = 0; f < 4; ++f)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int r = 16 * m + 4 * lq + i;
-          if (r < nrows) a.out[(size_t)(row0 + r) * a.out_ld + wrow[f] + l16] = (uint16_t)f32_to_bf16(acc[m][f][i]);
+          const int r = 64 * wm + 16 * m + 4 * lq + i;
+          uint16_t* st = stage0 + (wn >> 1) * (kStageBytes / 2);
+          st[r * kOutStride + 64 * (wn & 1) + 16 * f + l16] = (uint16_t)f32_to_bf16(acc[m][f][i]);
         }
-      }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int cid = tid + 512 * q, r = cid >> 5, c = cid & 31;
+      const uint16_t* st = stage0 + (c >> 4) * (kStageBytes / 2);
+      if (r < nrows)
+        *reinterpret_cast<uint4*>(a.out + (size_t)(row0 + r) * a.out_ld + 256 * nt + 8 * c) =
+            *reinterpret_cast<const uint4*>(st + r * kOutStride + 8 * (c & 15));
     }
   }
 }

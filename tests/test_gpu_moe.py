@@ -26,9 +26,19 @@ MARGIN = 1e-6
 
 
 def _check(out, ref, label, same_min=0.95):
+    """max-abs 1e-2 and rel-L2 1e-3.  A layer output passes two bf16 roundings in sequence
+    (the routed sum, then + shared) whose ties the fp32 summation order decides -- the
+    oracle's own BLAS order included -- for a few per cent of elements.  Near |ref| = 1..2
+    two such flips, and above 2 a single one, exceed 1e-2 by construction, so the
+    per-element bound is max(1e-2, two ulps of the reference value)."""
     err, rel, same = compare_bf16(out, ref)
-    print(f"{label}: max-abs {err:.3e} rel-L2 {rel:.3e} bit-identical {same:.4f}")
-    assert err <= TOL_ABS and rel <= TOL_REL and same >= same_min, (label, err, rel, same)
+    b = bf16_to_f32(ref).astype(np.float64)
+    d = np.abs(bf16_to_f32(out).astype(np.float64) - b)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(b), 1e-30))) - 7)
+    bound = np.maximum(TOL_ABS, 2 * ulp)
+    print(f"{label}: max-abs {err:.3e} (max |d|/bound {np.max(d / bound):.3f}) rel-L2 {rel:.3e} "
+          f"bit-identical {same:.4f}")
+    assert np.all(d <= bound) and rel <= TOL_REL and same >= same_min, (label, err, rel, same)
 
 
 def _check_ulp(out, ref, label):
