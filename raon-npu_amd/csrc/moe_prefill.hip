@@ -32,12 +32,16 @@ __device__ __forceinline__ void split3_bf16(float v, uint32_t& hi, uint32_t& mid
   mid = f32_to_bf16(r);
   lo = f32_to_bf16(r - bf16_to_f32(mid));
 }
-// Group sums are stored as two dwords per (row, group): (hi | mid << 16), lo.
-__device__ __forceinline__ void store_split3(uint32_t* dst, float v) {
+// Group sums are stored planar per row: planes hi, mid, lo of Gp = round_up(G, 8) bf16
+// each (G = groups per row; the padding groups hold 0), so that 8 consecutive groups of
+// one plane are one 16-byte MFMA operand.
+__host__ __device__ inline int sum_planes_gp(int G) { return (G + 7) & ~7; }
+__device__ __forceinline__ void store_split3_planar(uint16_t* dst, int Gp, float v) {
   uint32_t hi, mid, lo;
   split3_bf16(v, hi, mid, lo);
-  dst[0] = hi | (mid << 16);
-  dst[1] = lo;
+  dst[0] = (uint16_t)hi;
+  dst[Gp] = (uint16_t)mid;
+  dst[2 * Gp] = (uint16_t)lo;
 }
 
 // ---------------------------------------------------------------- router GEMM --
@@ -186,13 +190,20 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
 }
 
 // ------------------------------------------------------------ row group sums --
-// S[row, g] = sum of the 32 bf16 values of group g of row `row`, stored as an exact
-// 3-way bf16 split in dwords dst32[(row*G + g)*2 + {0,1}].  Thread per (row, group).
-__global__ void group_sums_kernel(const uint16_t* __restrict__ src, int rows, int K, uint32_t* __restrict__ dst) {
-  const int G = K / 32;
+// S[row, g] = sum of the 32 bf16 values of group g of row `row`, as an exact 3-way bf16
+// split in the planar layout of store_split3_planar.  Thread per (row, padded group).
+__global__ void group_sums_kernel(const uint16_t* __restrict__ src, int rows, int K, uint16_t* __restrict__ dst) {
+  const int G = K / 32, Gp = sum_planes_gp(G);
   const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (size_t)rows * G) return;
-  const uint32_t* p = reinterpret_cast<const uint32_t*>(src + idx * 32);
+  if (idx >= (size_t)rows * Gp) return;
+  const size_t row = idx / Gp;
+  const int g = (int)(idx % Gp);
+  uint16_t* d = dst + row * 3 * Gp + g;
+  if (g >= G) {
+    d[0] = d[Gp] = d[2 * Gp] = 0;
+    return;
+  }
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(src + row * K + 32 * g);
   float s = 0.f;
 #pragma unroll
   for (int c = 0; c < 16; ++c) {
@@ -200,7 +211,7 @@ __global__ void group_sums_kernel(const uint16_t* __restrict__ src, int rows, in
     s += bf16_to_f32(v & 0xffffu);
     s += bf16_to_f32(v >> 16);
   }
-  store_split3(dst + idx * 2, s);
+  store_split3_planar(d, Gp, s);
 }
 
 // ----------------------------------------------------------------- tile table --
@@ -252,7 +263,7 @@ struct GemmArgs {
   int k_routes;
   int n_routed;             // group id n_routed = shared expert (rows identity tokens / sorted)
   int shared_base;          // sorted row index of the first shared row
-  const uint32_t* ssum;     // row group sums, 2 dwords each: mode 0 [T, K/32] by token; mode 1 [rows, K/32] by row
+  const uint16_t* ssum;     // row group sums (planar, store_split3_planar): mode 0 by token; mode 1 by row
   const uint32_t* tiles;
   const int* ntiles;
   const int32_t* offsets;   // group row ends: offsets[e+1] (routed); shared end = shared_base + shared_rows
@@ -260,26 +271,13 @@ struct GemmArgs {
   // outputs
   uint16_t* out;            // mode 0: h [rows, out_ld]; mode 1: D [rows, out_ld]
   int out_ld;
-  uint32_t* out_ssum;       // mode 0: group sums of h rows [rows, out_ld/32], 2 dwords each
+  uint16_t* out_ssum;       // mode 0: group sums of the h rows (planar, out_ld/32 groups)
   int act;
   float gb, vb;
 };
 
 __device__ __forceinline__ int group_end(const GemmArgs& a, int e) {
   return e < a.n_routed ? a.offsets[e + 1] : a.shared_base + a.shared_rows;
-}
-
-// Source row of sorted row p.
-__device__ __forceinline__ const uint16_t* src_row(const GemmArgs& a, int e, int p) {
-  if (a.mode == 1) return a.src + (size_t)p * a.K;
-  const int tok = e < a.n_routed ? a.order[p] / a.k_routes : p - a.shared_base;
-  return a.src + (size_t)tok * a.K;
-}
-__device__ __forceinline__ const uint32_t* ssum_row(const GemmArgs& a, int e, int p) {
-  const int G = a.K / 32;
-  if (a.mode == 1) return a.ssum + (size_t)p * G * 2;
-  const int tok = e < a.n_routed ? a.order[p] / a.k_routes : p - a.shared_base;
-  return a.ssum + (size_t)tok * G * 2;
 }
 
 // LDS ring of the grouped GEMM: per K step (128 columns) the workgroup's 128 activation
@@ -291,11 +289,16 @@ constexpr int kWBytes = 4 * kTileBytes;
 constexpr int kStageBytes = kXBytes + kWBytes;
 constexpr int kGemmLds = kStages * kStageBytes;  // 159,744 of the 163,840 bytes of a CU
 constexpr int kOutStride = 136;                  // bf16 per row of the epilogue staging tile
+// Group sums of one block of 32 groups for the tile's rows: [row][hi, mid, lo][32] bf16.
+constexpr int kSRow = 3 * 32 * 2;
+constexpr int kSBlock = kBM * kSRow;  // 24,576: two blocks fit in ring slot 2
+
+typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
 
 // 16 bytes per lane from global memory straight into LDS: lane L writes lds + 16 L.
 // Written as inline assembly so that the compiler does not treat every later LDS read
 // as dependent on it (it would wait for all outstanding loads before each one); the
-// ring's own waits (ring_wait) order the copies.  M0 is saved and restored.
+// kernel's own waits order the copies.  M0 is saved and restored.
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
   uint32_t saved;
   asm volatile(
@@ -307,29 +310,62 @@ __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
       : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
       : "memory");
 }
-// Wait until at most `pending` of this wave's copies are in flight, then meet the
+// A 16-byte global load the compiler does not count: its result may be used only after
+// a wait_tied() on it (compiler-counted loads would make the compiler wait for every
+// copy issued after them).
+__device__ __forceinline__ u32x4v gload16(const void* p) {
+  u32x4v v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+// Wait until at most `pending` of this wave's loads are in flight, then meet the
 // workgroup.  The count is an immediate, so each value is a branch of its own.
 __device__ __forceinline__ void ring_wait(int pending) {
   switch (pending) {
-    case 7: asm volatile("s_waitcnt vmcnt(7) lgkmcnt(0)" ::: "memory"); break;
-    case 6: asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)" ::: "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory"); break;
+    case 7: asm volatile("s_waitcnt vmcnt(7) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    case 6: asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
   }
-  asm volatile("s_barrier" ::: "memory");
+}
+// The same, tying the coefficient registers of gload16() to the wait.
+#define RMOE_WAIT_TIED(N, c)                                                                             \
+  asm volatile("s_waitcnt vmcnt(" #N ") lgkmcnt(0)\n\ts_barrier"                                        \
+               : "+v"(c[0][0]), "+v"(c[0][1]), "+v"(c[1][0]), "+v"(c[1][1])::"memory")
+// (x & m) | o in one instruction (the compiler keeps the two-instruction form).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(o));
+  return r;
+}
+
+// SiLU-GLU g*sigmoid(g)*u with the overflow-free sigmoid of the oracle, on the hardware
+// exp2 and reciprocal (one Newton step): within a few fp32 ulps of the correctly
+// rounded form, far below the bf16 rounding that follows.
+__device__ __forceinline__ float swiglu_fast(float g, float u) {
+  const float e = __builtin_amdgcn_exp2f(-fabsf(g) * 1.44269504088896341f);
+  const float d = 1.0f + e;
+  float r = __builtin_amdgcn_rcpf(d);
+  r = fmaf(r, fmaf(-d, r, 1.0f), r);
+  const float sig = g >= 0.f ? r : e * r;
+  return (g * sig) * u;
 }
 
 // Grid: n_tiles * tile_cap workgroups (rounded to a multiple of 8), 512 threads (8 waves).
-// A workgroup multiplies 128 sorted rows by 256 weight rows; wave w takes rows
-// 64*(w&1)..+63 and a quarter of the weight rows (w>>1), as 4 x 4 MFMA fragments.
-//   gate/up: the workgroup takes intermediate units 128*nt..+127 (gate rows and the
-//            matching up rows); the wave's quarter is units 32*(w>>1)..+31, fragments
-//            0,1 = gate, 2,3 = up, so the activation and the 32-column group sums of h
-//            stay inside the wave.
-//   down:    the workgroup takes output rows 256*nt..+255, the wave 64*(w>>1)..+63.
-// K loop: a three-deep LDS ring filled by global->LDS copies; per K step one
-// barrier, then the copy for step kt+2 into the slot step kt-1 used.
+// A workgroup multiplies 128 sorted rows by 256 weight rows; wave w takes all 128 rows
+// (8 MFMA fragments) and two 16-row weight fragments:
+//   gate/up: intermediate units 128*nt + 16w..+15: fragment 0 the gate rows, 1 the up
+//            rows, so the activation stays in the lane;
+//   down:    output rows 256*nt + 16w and 256*nt + 128 + 16w.
+// Per group the MFMA runs on the codes as exact bf16 values 16 + n; the group's scale
+// is applied by one fp32 FMA per output:
+//   y = sum_g scale_g * sum_k x_k (16 + n_k) + sum_g (min_g - 16 scale_g) * S_g.
+// The second sum (the correction) runs first, from group sums copied into ring slot 2
+// while the first two K steps' copies are in flight.  K loop: a three-deep LDS ring
+// filled by global->LDS copies; per K step one barrier, then the copy for step kt+2
+// into the slot step kt-1 used.
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void grouped_gemm_kernel(GemmArgs a, int tile_cap) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kGemmLds];
+  __shared__ int rowidx[kBM];
   // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs; make each XCD
   // take a contiguous range of (n-tile, m-tile) so m-tiles sharing a weight tile meet
   // in the same L2.
@@ -345,14 +381,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int nrows = min(kBM, rend - row0);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lq = lane >> 4;
-  const int wm = wave & 1, wn = wave >> 1;
   const int nkt = a.K / kTileCols;
   const uint8_t* W = a.wbase + (size_t)e * a.wstride;
   const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
 
+  // Source row of each tile row (token for gate/up, sorted row for down); rows past the
+  // tile use the tile's first row (their results are not stored).
+  if (tid < kBM) {
+    const int p = row0 + (tid < nrows ? tid : 0);
+    rowidx[tid] = a.mode == 1 ? p : (e < a.n_routed ? a.order[p] / a.k_routes : p - a.shared_base);
+  }
+  __syncthreads();
+
   // The workgroup's four 64-row weight bands.  Gate/up: gate bands 2nt, 2nt+1, up bands
   // I/64 + 2nt, +1; a band past I (last n-tile when I % 128 != 0) reads band 0 instead
-  // and its results are not stored.
+  // and its results are not stored.  Down: bands 4nt..4nt+3.
   int band[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
@@ -363,29 +406,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       band[t] = 4 * nt + t;
     }
   }
-  // Fragment f of this wave: weight tile ft[f] (0..3) and first row fr[f] inside it.
-  int ft[4], fr[4];
-#pragma unroll
-  for (int f = 0; f < 4; ++f) {
-    if (a.mode == 0) {
-      ft[f] = (f < 2 ? 0 : 2) + (wn >> 1);
-      fr[f] = 32 * (wn & 1) + 16 * (f & 1);
-    } else {
-      ft[f] = wn;
-      fr[f] = 16 * f;
-    }
-  }
-  const bool active = a.mode == 1 || 128 * nt + 32 * wn < a.inter;
+  // Fragment f of this wave: weight tile (w/4) + 2f of the four, rows 16*(w%4)..+15.
+  const int ft0 = wave >> 2, frow = 16 * (wave & 3) + l16;
 
   // Copy descriptors.  Activations: copy q = wave + 8i (i < 4) fills LDS rows 4q..4q+3;
-  // lane L brings row 4q + L/16, chunk (L%16) ^ (row%16).  Rows past the tile read the
-  // tile's first row (their results are not stored).
+  // lane L brings row 4q + L/16, chunk (L%16) ^ (row%16).
   const uint8_t* xg[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int q = wave + 8 * i, r = 4 * q + (lane >> 4);
     const int c = (lane & 15) ^ (r & 15);
-    xg[i] = reinterpret_cast<const uint8_t*>(src_row(a, e, row0 + (r < nrows ? r : 0))) + 16 * c;
+    xg[i] = reinterpret_cast<const uint8_t*>(a.src + (size_t)rowidx[r] * a.K) + 16 * c;
   }
   // Weights: copy v = wave + 8i (i < 3, v < 20) is 1 KB piece v%5 of tile v/5.
   const int n_wcopy = wave < 4 ? 3 : 2;
@@ -395,8 +426,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int v = min(wave + 8 * i, 19), t = v / 5, p = v % 5;
     wg[i] = W + (size_t)band[t] * nkt * kTileBytes + 1024 * p + 16 * lane;
   }
-  auto issue = [&](int kt) {
-    const uint32_t sb = lds0 + (uint32_t)((kt % kStages) * kStageBytes);
+  auto issue_to = [&](int kt, int slot) {
+    const uint32_t sb = lds0 + (uint32_t)(slot * kStageBytes);
 #pragma unroll
     for (int i = 0; i < 4; ++i) dma16(xg[i] + (size_t)kt * 256, sb + 1024u * (uint32_t)(wave + 8 * i));
 #pragma unroll
@@ -407,153 +438,217 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
   };
+  auto issue = [&](int kt) { issue_to(kt, kt % kStages); };
   const int per_stage = 4 + n_wcopy;
 
-  issue(0);
-  if (nkt > 1) issue(1);
-
-  // Correction first, while the first copies are in flight:
-  //   acc = sum_g (min - 16*scale)[r, g] * S[m, g]
-  // over blocks of 32 groups, both factors split exactly into 3 bf16 parts; the 6
-  // leading products are kept.
-  f32x4_t acc[4][4];
+  // Group sums, planar per row: [hi | mid | lo] planes of Gp (G rounded up to 8) bf16.
+  // Block b (groups 32b..32b+31) goes to half (b & 1) of ring slot 2 as 24 copies of
+  // 1 KB, 3 per wave; chunks past Gp read the row's first chunk (coefficient 0).
+  const int G = a.K / 32, Gp = (G + 7) & ~7, nblk = (G + 31) / 32;
+  const uint32_t sbase = lds0 + 2u * kStageBytes;
+  auto issue_s = [&](int blk) {
 #pragma unroll
-  for (int m = 0; m < 4; ++m)
+    for (int i = 0; i < 3; ++i) {
+      const int o = 1024 * (wave + 8 * i) + 16 * lane;
+      const int r = o / kSRow, rem = o - r * kSRow, part = rem >> 6, g = 32 * blk + 8 * ((rem & 63) >> 4);
+      dma16(a.ssum + (size_t)rowidx[r] * 3 * Gp + part * Gp + (g < Gp ? g : 0),
+            sbase + (uint32_t)((blk & 1) * kSBlock + 1024 * (wave + 8 * i)));
+    }
+  };
+  // Correction coefficients: scale|min words of the lane's row for groups gl..gl+7 of a
+  // block (gl = 32*blk + 8*lq) from the weight tiles in global memory; past G they are
+  // masked to zero after the wait.
+  auto load_coef = [&](int blk, u32x4v (&c)[2][2]) {
+    const int gl = 32 * blk + 8 * lq;
 #pragma unroll
-    for (int f = 0; f < 4; ++f) acc[m][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const int G = a.K / 32;
-  const uint32_t* srow[4];
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int r = 64 * wm + 16 * m + l16;
-    srow[m] = r < nrows ? ssum_row(a, e, row0 + r) : nullptr;
-  }
-  for (int g0 = 0; g0 < G; g0 += 32) {
-    const int gl = g0 + 8 * lq;  // the lane's first group; groups gl..gl+7
-    uint4 bc[4][3];
-#pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      uint4 smw[2];
+    for (int f = 0; f < 2; ++f)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int kt = gl / 4 + h;
-        smw[h] = 4 * kt < G ? *reinterpret_cast<const uint4*>(W + ((size_t)band[ft[f]] * nkt + kt) * kTileBytes + kCodeBytes +
-                                                              (fr[f] + l16) * 16)
-                            : make_uint4(0u, 0u, 0u, 0u);
+        c[f][h] = gload16(W + ((size_t)band[ft0 + 2 * f] * nkt + (4 * kt < G ? kt : 0)) * kTileBytes + kCodeBytes +
+                          frow * 16);
       }
-      const uint32_t sv[8] = {smw[0].x, smw[0].y, smw[0].z, smw[0].w, smw[1].x, smw[1].y, smw[1].z, smw[1].w};
+  };
+  // Issue order per wave (fixed counts for the waits below): coefficients of blocks 0
+  // and 1 (8 loads), group-sum blocks 0 and 1 (3 + 3), K steps 0 and 1 (2 x per_stage).
+  // With one block, block 1 repeats block 0; with one K step, step 1 repeats step 0
+  // into slot 1 (unused then).
+  u32x4v cf0[2][2], cf1[2][2];
+  load_coef(0, cf0);
+  load_coef(nblk > 1 ? 1 : 0, cf1);
+  issue_s(0);
+  issue_s(nblk > 1 ? 1 : 0);
+  issue(0);
+  issue_to(nkt > 1 ? 1 : 0, 1);
+
+  f32x4_t acc[8][2];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    acc[m][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    acc[m][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  const uint32_t xrow = (uint32_t)l16 * 256u;  // A row 16m + l16: m*4096 + xrow
+
+  // acc += sum_g (min - 16*scale)[r, g] * S[m, g] over one block of 32 groups, both
+  // factors split exactly into 3 bf16 parts; the 6 leading products are kept.
+  auto corr_block = [&](int blk, const u32x4v (&c)[2][2]) {
+    const int gl = 32 * blk + 8 * lq;
+    uint4 bc[2][3];
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const uint32_t sv[8] = {c[f][0].x, c[f][0].y, c[f][0].z, c[f][0].w, c[f][1].x, c[f][1].y, c[f][1].z, c[f][1].w};
       uint32_t hv[8], mv[8], lv[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float coef = bf16_to_f32(sv[i] >> 16) - 16.f * bf16_to_f32(sv[i] & 0xffffu);
+        const float coef =
+            gl + i < G ? bf16_to_f32(sv[i] >> 16) - 16.f * bf16_to_f32(sv[i] & 0xffffu) : 0.f;
         split3_bf16(coef, hv[i], mv[i], lv[i]);
       }
       bc[f][0] = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
       bc[f][1] = make_uint4(mv[0] | (mv[1] << 16), mv[2] | (mv[3] << 16), mv[4] | (mv[5] << 16), mv[6] | (mv[7] << 16));
       bc[f][2] = make_uint4(lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16), lv[4] | (lv[5] << 16), lv[6] | (lv[7] << 16));
     }
+    const uint8_t* ss = lds + 2 * kStageBytes + (blk & 1) * kSBlock + l16 * kSRow + 16 * lq;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      // 8 groups x (hi|mid, lo) = 16 dwords; pairs of groups past G read as zero.
-      uint4 sv[4];
+    for (int m = 0; m < 8; ++m) {
+      __builtin_amdgcn_sched_barrier(0);
+      const uint4 ah = *reinterpret_cast<const uint4*>(ss + m * 16 * kSRow);
+      const uint4 am = *reinterpret_cast<const uint4*>(ss + m * 16 * kSRow + 64);
+      const uint4 al = *reinterpret_cast<const uint4*>(ss + m * 16 * kSRow + 128);
 #pragma unroll
-      for (int h = 0; h < 4; ++h)
-        sv[h] = srow[m] && gl + 2 * h < G ? *reinterpret_cast<const uint4*>(srow[m] + 2 * (gl + 2 * h))
-                                          : make_uint4(0u, 0u, 0u, 0u);
-      uint4 ah, am, al;
-      ah.x = __builtin_amdgcn_perm(sv[0].z, sv[0].x, 0x05040100u);
-      ah.y = __builtin_amdgcn_perm(sv[1].z, sv[1].x, 0x05040100u);
-      ah.z = __builtin_amdgcn_perm(sv[2].z, sv[2].x, 0x05040100u);
-      ah.w = __builtin_amdgcn_perm(sv[3].z, sv[3].x, 0x05040100u);
-      am.x = __builtin_amdgcn_perm(sv[0].z, sv[0].x, 0x07060302u);
-      am.y = __builtin_amdgcn_perm(sv[1].z, sv[1].x, 0x07060302u);
-      am.z = __builtin_amdgcn_perm(sv[2].z, sv[2].x, 0x07060302u);
-      am.w = __builtin_amdgcn_perm(sv[3].z, sv[3].x, 0x07060302u);
-      al.x = __builtin_amdgcn_perm(sv[0].w, sv[0].y, 0x05040100u);
-      al.y = __builtin_amdgcn_perm(sv[1].w, sv[1].y, 0x05040100u);
-      al.z = __builtin_amdgcn_perm(sv[2].w, sv[2].y, 0x05040100u);
-      al.w = __builtin_amdgcn_perm(sv[3].w, sv[3].y, 0x05040100u);
-#pragma unroll
-      for (int f = 0; f < 4; ++f) {
-        f32x4_t c = acc[m][f];
-        c = mfma16(al, bc[f][0], c);
-        c = mfma16(am, bc[f][1], c);
-        c = mfma16(ah, bc[f][2], c);
-        c = mfma16(am, bc[f][0], c);
-        c = mfma16(ah, bc[f][1], c);
-        c = mfma16(ah, bc[f][0], c);
-        acc[m][f] = c;
+      for (int f = 0; f < 2; ++f) {
+        f32x4_t cc = acc[m][f];
+        cc = mfma16(al, bc[f][0], cc);
+        cc = mfma16(am, bc[f][1], cc);
+        cc = mfma16(ah, bc[f][2], cc);
+        cc = mfma16(am, bc[f][0], cc);
+        cc = mfma16(ah, bc[f][1], cc);
+        cc = mfma16(ah, bc[f][0], cc);
+        acc[m][f] = cc;
       }
     }
+  };
+  // Block 0: past it are in flight group-sum block 1 (3) and K steps 0 and 1.
+  if (per_stage == 7) RMOE_WAIT_TIED(17, cf0); else RMOE_WAIT_TIED(15, cf0);
+  corr_block(0, cf0);
+  if (nblk > 1) {
+    if (per_stage == 7) RMOE_WAIT_TIED(14, cf1); else RMOE_WAIT_TIED(12, cf1);
+    corr_block(1, cf1);
+  }
+  for (int blk = 2; blk < nblk; ++blk) {  // K > 2048: blocks reuse the halves of slot 2
+    asm volatile("s_barrier" ::: "memory");
+    u32x4v cfb[2][2];
+    load_coef(blk, cfb);
+    issue_s(blk);
+    RMOE_WAIT_TIED(0, cfb);
+    corr_block(blk, cfb);
   }
 
-  // Main K loop:  acc += 16*scale[r, g] * sum_k x[m,k] (1 + n[r,k]/16)  per group g.
-  for (int kt = 0; kt < nkt; ++kt) {
+  // Main K loop:  acc += scale[r, g] * sum_k x[m,k] (16 + n[r,k])  per group g.
+  uint32_t kmask, kone;  // in registers so that v_and_or_b32 can take them
+  asm volatile("v_mov_b32 %0, 0x780078" : "=v"(kmask));
+  asm volatile("v_mov_b32 %0, 0x41804180" : "=v"(kone));
+  const uint32_t wrow0 = (uint32_t)(ft0 * kTileBytes + frow * 16);
+  auto kstep = [&](int kt, const int slot) {
+    // After this barrier every wave is past step kt-1 (and the correction), so slot
+    // (kt+2) % 3 is free.
     ring_wait(kt + 1 < nkt ? per_stage : 0);
     if (kt + 2 < nkt) issue(kt + 2);
-    const uint8_t* xs = lds + (kt % kStages) * kStageBytes;
-    const uint8_t* ws = xs + kXBytes;
-    float s16[4][4];
+    const uint8_t* xs = lds + slot * kStageBytes;
+    const uint8_t* ws = xs + kXBytes + wrow0;
+    float sc[2][4];
+    uint4 smv[2];
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      const uint4 smv = *reinterpret_cast<const uint4*>(ws + ft[f] * kTileBytes + kCodeBytes + (fr[f] + l16) * 16);
-      s16[f][0] = 16.f * bf16_to_f32(smv.x & 0xffffu);
-      s16[f][1] = 16.f * bf16_to_f32(smv.y & 0xffffu);
-      s16[f][2] = 16.f * bf16_to_f32(smv.z & 0xffffu);
-      s16[f][3] = 16.f * bf16_to_f32(smv.w & 0xffffu);
+    for (int f = 0; f < 2; ++f) smv[f] = *reinterpret_cast<const uint4*>(ws + 2 * f * kTileBytes + kCodeBytes);
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      sc[f][0] = bf16_to_f32(smv[f].x & 0xffffu);
+      sc[f][1] = bf16_to_f32(smv[f].y & 0xffffu);
+      sc[f][2] = bf16_to_f32(smv[f].z & 0xffffu);
+      sc[f][3] = bf16_to_f32(smv[f].w & 0xffffu);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      uint4 b[4], av[4];
+      uint4 b[2];
 #pragma unroll
-      for (int f = 0; f < 4; ++f) {
-        const uint32_t code =
-            *reinterpret_cast<const uint32_t*>(ws + ft[f] * kTileBytes + j * 1024 + (fr[f] + l16) * 16 + 4 * lq);
-        unpack_codes(code, b[f].x, b[f].y, b[f].z, b[f].w);
+      for (int f = 0; f < 2; ++f) {
+        const uint32_t v = *reinterpret_cast<const uint32_t*>(ws + 2 * f * kTileBytes + j * 1024 + 4 * lq);
+        b[f].x = and_or(v << 3, kmask, kone);
+        b[f].y = and_or(v >> 1, kmask, kone);
+        b[f].z = and_or(v >> 5, kmask, kone);
+        b[f].w = and_or(v >> 9, kmask, kone);
       }
+      const uint32_t xc = 16u * (uint32_t)((4 * j + lq) ^ l16);  // row % 16 == l16
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const int r = 64 * wm + 16 * m + l16;
-        av[m] = *reinterpret_cast<const uint4*>(xs + r * 256 + 16 * ((4 * j + lq) ^ (r & 15)));
-      }
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int f = 0; f < 4; ++f) {
-          const f32x4_t c = mfma16(av[m], b[f], f32x4_t{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[m][f][i] = fmaf(s16[f][j], c[i], acc[m][f][i]);
-        }
-    }
-  }
-  // Every wave is past its last ring read: slots 0 and 1 become the output staging.
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-
-  // Epilogue.  C layout: lane holds rows 16m + 4*lq + i (of the wave's 64), column l16
-  // of the fragment.  Results go through LDS so that global stores are 16-byte rows.
-  uint16_t* stage0 = reinterpret_cast<uint16_t*>(lds);
-  if (a.mode == 0) {
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 64 * wm + 16 * m + 4 * lq + i;
-        float hv = 0.f;
+      for (int m = 0; m < 8; ++m) {
+        const uint4 av = *reinterpret_cast<const uint4*>(xs + m * 4096 + xrow + xc);
 #pragma unroll
         for (int f = 0; f < 2; ++f) {
-          const float g = bf16_round(acc[m][f][i]), u = bf16_round(acc[m][2 + f][i]);
-          const uint32_t h = f32_to_bf16(act_apply(a.act, g, u, a.gb, a.vb));
-          stage0[r * kOutStride + 32 * wn + 16 * f + l16] = (uint16_t)h;
-          hv += bf16_to_f32(h);
-        }
-        // The wave's 32 units are one group of h: reduce over the 16 lanes of l16.
+          const f32x4_t c = mfma16(av, b[f], f32x4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-        for (int off = 8; off > 0; off >>= 1) hv += __shfl_xor(hv, off, 16);
-        if (l16 == 0 && active && r < nrows)
-          store_split3(a.out_ssum + ((size_t)(row0 + r) * (a.out_ld / 32) + 4 * nt + wn) * 2, hv);
+          for (int i = 0; i < 4; ++i) acc[m][f][i] = fmaf(sc[f][j], c[i], acc[m][f][i]);
+        }
+      }
+    }
+  };
+  for (int kt = 0; kt < nkt; kt += kStages) {
+    kstep(kt, 0);
+    if (kt + 1 < nkt) kstep(kt + 1, 1);
+    if (kt + 2 < nkt) kstep(kt + 2, 2);
+  }
+  // Every wave is past its last ring read: the slots become the output staging.
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  // Epilogue.  C layout: lane holds rows 16m + 4*lq + i, column l16 of the fragment.
+  // Results go through LDS so that global stores are 16-byte rows.
+  uint16_t* stage0 = reinterpret_cast<uint16_t*>(lds);
+  if (a.mode == 0) {
+    // h tile [128 rows][128 units] in slot 0.
+    if (a.act == 1) {
+#pragma unroll
+      for (int m = 0; m < 8; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 16 * m + 4 * lq + i;
+          const float g = bf16_round(acc[m][0][i]), u = bf16_round(acc[m][1][i]);
+          stage0[r * kOutStride + 16 * wave + l16] = (uint16_t)f32_to_bf16(swiglu_fast(g, u));
+        }
+    } else {
+      // SiTU-GLU: g and u (bf16) go through slots 1 and 2 and the activation runs in a
+      // rolled loop, which keeps the kernel's code small.
+      uint16_t* gs = reinterpret_cast<uint16_t*>(lds + kStageBytes);
+      uint16_t* us = reinterpret_cast<uint16_t*>(lds + 2 * kStageBytes);
+#pragma unroll
+      for (int m = 0; m < 8; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 16 * m + 4 * lq + i;
+          gs[r * kOutStride + 16 * wave + l16] = (uint16_t)f32_to_bf16(acc[m][0][i]);
+          us[r * kOutStride + 16 * wave + l16] = (uint16_t)f32_to_bf16(acc[m][1][i]);
+        }
+      __syncthreads();
+      for (int idx = tid; idx < kBM * 128; idx += 512) {
+        const int o = (idx >> 7) * kOutStride + (idx & 127);
+        stage0[o] = (uint16_t)f32_to_bf16(act_situ(bf16_to_f32(gs[o]), bf16_to_f32(us[o]), a.gb, a.vb));
       }
     }
     __syncthreads();
+    // Group 4nt + q of h = units 32q..32q+31 of the tile: one (row, group) per thread.
+    {
+      const int r = tid >> 2, q = tid & 3;
+      if (r < nrows && 128 * nt + 32 * q < a.inter) {
+        float hs = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const uint4 v = *reinterpret_cast<const uint4*>(stage0 + r * kOutStride + 32 * q + 8 * c);
+          const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int d = 0; d < 4; ++d) hs += bf16_to_f32(w4[d] & 0xffffu) + bf16_to_f32(w4[d] >> 16);
+        }
+        const int Gpo = ((a.out_ld / 32) + 7) & ~7;
+        store_split3_planar(a.out_ssum + (size_t)(row0 + r) * 3 * Gpo + 4 * nt + q, Gpo, hs);
+      }
+    }
     // 128 rows x 16 chunks of 8 units.
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -563,16 +658,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             *reinterpret_cast<const uint4*>(stage0 + r * kOutStride + 8 * c);
     }
   } else {
-    // Columns 0..127 of the 256 in slot 0, 128..255 in slot 1.
+    // Output columns 0..127 of the 256 in slot 0 (fragment 0), 128..255 in slot 1.
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+    for (int m = 0; m < 8; ++m)
 #pragma unroll
-      for (int f = 0; f < 4; ++f)
+      for (int f = 0; f < 2; ++f)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int r = 64 * wm + 16 * m + 4 * lq + i;
-          uint16_t* st = stage0 + (wn >> 1) * (kStageBytes / 2);
-          st[r * kOutStride + 64 * (wn & 1) + 16 * f + l16] = (uint16_t)f32_to_bf16(acc[m][f][i]);
+          const int r = 16 * m + 4 * lq + i;
+          uint16_t* st = stage0 + f * (kStageBytes / 2);
+          st[r * kOutStride + 16 * wave + l16] = (uint16_t)f32_to_bf16(acc[m][f][i]);
         }
     __syncthreads();
 #pragma unroll
@@ -632,25 +727,29 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
 }
 
 // Zero h[:, I:Ipad] and the group sums of those columns (thread per row).
-__global__ void zero_pad_cols_kernel(uint16_t* __restrict__ h, uint32_t* __restrict__ hsum, int rows, int I, int Ipad) {
+__global__ void zero_pad_cols_kernel(uint16_t* __restrict__ h, uint16_t* __restrict__ hsum, int rows, int I, int Ipad) {
   const int r = blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= rows) return;
   for (int c = I; c < Ipad; ++c) h[(size_t)r * Ipad + c] = 0;
-  // Groups entirely past I; a group straddling I gets its sum from the GEMM epilogue
-  // only when I is a multiple of 32 (guaranteed: I % 64 == 0).
-  for (int g = I / 32; g < Ipad / 32; ++g) {
-    hsum[((size_t)r * (Ipad / 32) + g) * 2] = 0u;
-    hsum[((size_t)r * (Ipad / 32) + g) * 2 + 1] = 0u;
-  }
+  // Groups entirely past I (and the planes' padding); a group straddling I gets its sum
+  // from the GEMM epilogue only when I is a multiple of 32 (guaranteed: I % 64 == 0).
+  const int Gp = sum_planes_gp(Ipad / 32);
+  uint16_t* d = hsum + (size_t)r * 3 * Gp;
+  for (int g = I / 32; g < Gp; ++g) d[g] = d[Gp + g] = d[2 * Gp + g] = 0;
 }
 
 // h[shared_base + t] = RTNE(act(shared_gu[t])) (padded to Ipad) and its group sums.
 __global__ void shared_act_kernel(const uint16_t* __restrict__ gu, int T, int I, int Ipad, int act, float gb, float vb,
-                                  uint16_t* __restrict__ h, uint32_t* __restrict__ hsum) {
-  const int G = Ipad / 32;
+                                  uint16_t* __restrict__ h, uint16_t* __restrict__ hsum) {
+  const int G = Ipad / 32, Gp = sum_planes_gp(G);
   const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (size_t)T * G) return;
-  const int t = (int)(idx / G), g = (int)(idx % G);
+  if (idx >= (size_t)T * Gp) return;
+  const int t = (int)(idx / Gp), g = (int)(idx % Gp);
+  uint16_t* d = hsum + (size_t)t * 3 * Gp + g;
+  if (g >= G) {
+    d[0] = d[Gp] = d[2 * Gp] = 0;
+    return;
+  }
   float s = 0.f;
   for (int c = 0; c < 32; ++c) {
     const int col = 32 * g + c;
@@ -663,7 +762,7 @@ __global__ void shared_act_kernel(const uint16_t* __restrict__ gu, int T, int I,
     h[(size_t)t * Ipad + col] = v;
     s += bf16_to_f32(v);
   }
-  store_split3(hsum + ((size_t)t * G + g) * 2, s);
+  store_split3_planar(d, Gp, s);
 }
 
 }  // namespace
@@ -700,12 +799,12 @@ hipError_t launch_topk(const float* logits, int T, int E, int k, int score, cons
 size_t prefill_scratch_bytes(const RmoeLayer& L, int T) {
   const size_t A = (size_t)T * L.top_k, R = A + T;
   const size_t tiles = A / kBM + L.n_routed + T / kBM + 4;
-  return R * L.Ipad * 2                  // h
-         + R * (L.Ipad / 32) * 8         // h group sums
-         + R * L.H * 2                   // D
-         + (size_t)T * (L.H / 32) * 8    // x group sums
-         + (size_t)T * L.n_routed * 4    // logits
-         + tiles * 4 + 256 * 3;          // tile table, counts
+  return R * L.Ipad * 2                                  // h
+         + R * 3 * sum_planes_gp(L.Ipad / 32) * 2        // h group sums
+         + R * L.H * 2                                   // D
+         + (size_t)T * 3 * sum_planes_gp(L.H / 32) * 2   // x group sums
+         + (size_t)T * L.n_routed * 4                    // logits
+         + tiles * 4 + 256 * 9;                          // tile table, counts, carve rounding
 }
 
 hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, const int32_t* ids_in, const float* wts_in,
@@ -723,9 +822,10 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
     return q;
   };
   uint16_t* h = (uint16_t*)carve(R * L.Ipad * 2);
-  uint32_t* hsum = (uint32_t*)carve(R * (L.Ipad / 32) * 8);
+  const int Gph = sum_planes_gp(L.Ipad / 32), Gpx = sum_planes_gp(L.H / 32);
+  uint16_t* hsum = (uint16_t*)carve(R * 3 * Gph * 2);
   uint16_t* D = (uint16_t*)carve(R * L.H * 2);
-  uint32_t* xsum = (uint32_t*)carve((size_t)T * (L.H / 32) * 8);
+  uint16_t* xsum = (uint16_t*)carve((size_t)T * 3 * Gpx * 2);
   float* logits = (float*)carve((size_t)T * E * 4);
   const int tile_cap = (int)(A / kBM + E + T / kBM + 4);
   uint32_t* tiles = (uint32_t*)carve((size_t)tile_cap * 4);
@@ -744,7 +844,7 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   err = launch_dispatch(ids, T, k, E, s.order, s.inv, s.offsets, s, st);
   if (err != hipSuccess) return err;
   {
-    const size_t n = (size_t)T * (L.H / 32);
+    const size_t n = (size_t)T * Gpx;
     hipLaunchKernelGGL(group_sums_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, T, L.H, xsum);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
@@ -782,9 +882,9 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(512), 0, st, s.offsets, E, g.shared_rows, tiles, ntiles, tile_cap);
   if ((err = hipGetLastError()) != hipSuccess) return err;
   if (shared_gu) {
-    const size_t n = (size_t)T * (L.Ipad / 32);
+    const size_t n = (size_t)T * Gph;
     hipLaunchKernelGGL(shared_act_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, shared_gu, T, L.I,
-                       L.Ipad, act, gb, vb, h + A * L.Ipad, hsum + A * (L.Ipad / 32) * 2);
+                       L.Ipad, act, gb, vb, h + A * L.Ipad, hsum + A * 3 * Gph);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
   {
