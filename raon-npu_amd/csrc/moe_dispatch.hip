@@ -3,9 +3,10 @@
 // Produces the flattened job order of build_plan (kernels/moe_grouped/planner.py:76-108):
 // assignments (token, route) sorted by expert id ascending and, inside one expert,
 // in row-major (token, route) order.  Chunks of 1,024 assignments are counted in
-// parallel; a single workgroup turns the per-chunk counts into per-chunk bases; each
-// chunk then places its assignments expert by expert in chunk order, which keeps the
-// sort stable without any atomics on the output.
+// parallel; one workgroup turns the per-chunk counts into per-chunk bases; each chunk
+// then places its assignments: its 4 waves take 256 consecutive assignments each, rank
+// lanes of equal expert with ballots (64 at a time, in order) and offset by the counts
+// of the waves before, so the sort is stable without atomics on the output.
 #include "rmoe_internal.h"
 
 namespace rmoe {
@@ -17,42 +18,55 @@ __global__ __launch_bounds__(256) void dispatch_count_kernel(const int32_t* __re
                                                              int32_t* __restrict__ counts, int* err) {
   __shared__ int hist[256];
   const int c = blockIdx.x;
-  for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
+  hist[threadIdx.x] = 0;
   __syncthreads();
-  const int begin = c * kChunk, end = min(n, begin + kChunk);
-  for (int i = begin + threadIdx.x; i < end; i += blockDim.x) {
-    const int e = ids[i];
-    if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
+  const int begin = c * kChunk;
+  int ev[kChunk / 256];
+#pragma unroll
+  for (int j = 0; j < kChunk / 256; ++j) {
+    const int i = begin + 256 * j + threadIdx.x;
+    ev[j] = i < n ? ids[i] : 0x7fffffff;
+  }
+#pragma unroll
+  for (int j = 0; j < kChunk / 256; ++j) {
+    if (ev[j] == 0x7fffffff) continue;
+    if (ev[j] >= 0 && ev[j] < E) atomicAdd(&hist[ev[j]], 1);
     else atomicOr(err, 4);
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x) counts[(size_t)c * E + e] = hist[e];
+  if ((int)threadIdx.x < E) counts[(size_t)c * E + threadIdx.x] = hist[threadIdx.x];
 }
 
-// One workgroup: counts[c][e] -> bases[c][e] in place; offsets[e] (E + 1 entries).
-__global__ __launch_bounds__(256) void dispatch_scan_kernel(int32_t* __restrict__ counts, int nchunks, int E,
+// One workgroup of 1,024 threads: counts[c][e] -> bases[c][e] in place; offsets[e]
+// (E + 1 entries).  Thread (e, p) handles the p-th quarter of the chunks of expert e.
+__global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t* __restrict__ counts, int nchunks, int E,
                                                             int32_t* __restrict__ offsets) {
-  __shared__ int tot[257];
-  const int e = threadIdx.x;
-  int total = 0;
+  __shared__ int part[4][256];
+  __shared__ int tot[256];
+  const int e = threadIdx.x & 255, p = threadIdx.x >> 8;
+  const int per = (nchunks + 3) / 4, c0 = min(nchunks, p * per), c1 = min(nchunks, c0 + per);
+  int sum = 0;
   if (e < E)
-    for (int c = 0; c < nchunks; ++c) total += counts[(size_t)c * E + e];
-  if (e < E) tot[e] = total;
+    for (int c = c0; c < c1; ++c) sum += counts[(size_t)c * E + e];
+  part[p][e] = sum;
   __syncthreads();
-  if (e == 0) {
-    int run = 0;
-    for (int q = 0; q < E; ++q) {
-      const int v = tot[q];
-      tot[q] = run;
-      offsets[q] = run;
-      run += v;
-    }
-    offsets[E] = run;
+  if (p == 0) tot[e] = e < E ? part[0][e] + part[1][e] + part[2][e] + part[3][e] : 0;
+  __syncthreads();
+  for (int d = 1; d < 256; d <<= 1) {  // inclusive scan of tot (Hillis-Steele)
+    int v = 0;
+    if (p == 0 && e >= d) v = tot[e - d];
+    __syncthreads();
+    if (p == 0) tot[e] += v;
+    __syncthreads();
   }
-  __syncthreads();
   if (e < E) {
-    int run = tot[e];
-    for (int c = 0; c < nchunks; ++c) {
+    int run = (e ? tot[e - 1] : 0);
+    if (p == 0) {
+      offsets[e] = run;
+      if (e == E - 1) offsets[E] = tot[e];
+    }
+    for (int q = 0; q < p; ++q) run += part[q][e];
+    for (int c = c0; c < c1; ++c) {
       const int v = counts[(size_t)c * E + e];
       counts[(size_t)c * E + e] = run;
       run += v;
@@ -60,24 +74,58 @@ __global__ __launch_bounds__(256) void dispatch_scan_kernel(int32_t* __restrict_
   }
 }
 
-// Thread e walks the chunk in order and places its assignments.
 __global__ __launch_bounds__(256) void dispatch_scatter_kernel(const int32_t* __restrict__ ids, int n, int E,
                                                                const int32_t* __restrict__ bases,
                                                                int32_t* __restrict__ order, int32_t* __restrict__ inv) {
-  __shared__ int cid[kChunk];
-  const int c = blockIdx.x;
-  const int begin = c * kChunk, len = min(n - begin, kChunk);
-  for (int i = threadIdx.x; i < len; i += blockDim.x) cid[i] = ids[begin + i];
+  __shared__ int slot[4][256];  // per wave: counts, then next output slot per expert
+  const int c = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  for (int i = tid; i < 4 * 256; i += 256) (&slot[0][0])[i] = 0;
+  const int begin = c * kChunk + 256 * wave;
+  int ev[4];
+  unsigned long long same[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = begin + 64 * j + lane;
+    ev[j] = i < n ? ids[i] : -1;
+  }
   __syncthreads();
-  const int e = threadIdx.x;
-  if (e >= E) return;
-  int pos = bases[(size_t)c * E + e];
-  for (int i = 0; i < len; ++i) {
-    if (cid[i] == e) {
-      order[pos] = begin + i;
-      if (inv) inv[begin + i] = pos;
-      ++pos;
+  // Lanes of one round with the same expert agree on every bit of the id.
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = ev[j];
+    const bool ok = e >= 0 && e < E;
+    unsigned long long m = __ballot(ok);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const unsigned long long bb = __ballot((e >> b) & 1);
+      m &= ((e >> b) & 1) ? bb : ~bb;
     }
+    same[j] = ok ? m : 0ull;
+    // The last lane of each expert group adds the group's size (one writer per expert).
+    if (ok && (m >> lane) == 1ull) slot[wave][e] += __popcll(m);
+  }
+  __syncthreads();
+  // Expert e's first slot for wave w: chunk base + counts of waves 0..w-1.
+  if (tid < E) {
+    int run = bases[(size_t)c * E + tid];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int v = slot[w][tid];
+      slot[w][tid] = run;
+      run += v;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = ev[j];
+    if (same[j]) {
+      const int pos = slot[wave][e] + __popcll(same[j] & ((1ull << lane) - 1ull));
+      const int i = begin + 64 * j + lane;
+      order[pos] = i;
+      if (inv) inv[i] = pos;
+    }
+    if (same[j] && (same[j] >> lane) == 1ull) slot[wave][e] += __popcll(same[j]);
   }
 }
 
@@ -89,16 +137,14 @@ hipError_t launch_dispatch(const int32_t* ids, int T, int k, int n_experts, int3
   const int nchunks = (n + kChunk - 1) / kChunk;
   if (n_experts < 1 || n_experts > 256) return hipErrorInvalidValue;
   if ((size_t)nchunks * n_experts > s.chunk_elems) return hipErrorInvalidValue;
-  const int threads = ((n_experts + 63) / 64) * 64;
-  hipLaunchKernelGGL(dispatch_count_kernel, dim3(nchunks), dim3(256), 0, st, ids, n, n_experts, s.chunk_counts,
-                     s.err);
+  hipLaunchKernelGGL(dispatch_count_kernel, dim3(nchunks), dim3(256), 0, st, ids, n, n_experts, s.chunk_counts, s.err);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(256), 0, st, s.chunk_counts, nchunks, n_experts, offsets);
+  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, st, s.chunk_counts, nchunks, n_experts, offsets);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nchunks), dim3(threads), 0, st, ids, n, n_experts, s.chunk_counts,
-                     order, inv);
+  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nchunks), dim3(256), 0, st, ids, n, n_experts, s.chunk_counts, order,
+                     inv);
   return hipGetLastError();
 }
 

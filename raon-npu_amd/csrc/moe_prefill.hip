@@ -46,59 +46,55 @@ __device__ __forceinline__ void store_split3_planar(uint16_t* dst, int Gp, float
 
 // ---------------------------------------------------------------- router GEMM --
 // logits[T, E] = x[T, H] . Wr[E, H]^T on MFMA (exact bf16 products, fp32 sums).
-// Block: 4 waves x 64 tokens; a 64-column chunk of Wr for all experts is staged in LDS
-// and shared by the 4 waves; A fragments come straight from the token rows.
+// Block: 32 tokens x all E experts, split over K: wave w takes columns w*H/4..+H/4 and
+// loads its A (token rows) and B (router rows) fragments straight from global memory
+// (the 0.5 MB router stays in L2); the four partial sums meet in LDS and are added in
+// wave order.
 constexpr int kMaxEFrags = 16;  // E <= 256
-constexpr int kRouterChunk = 64;
-constexpr int kRouterStride = kRouterChunk + 8;  // bf16 per LDS row (16-byte pad)
+constexpr int kRouterTok = 32;
 
 template <int NFR>
 __global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __restrict__ x, int T, int H,
                                                           const uint16_t* __restrict__ w, int E,
                                                           float* __restrict__ logits) {
-  __shared__ __attribute__((aligned(16))) uint16_t ws[256 * kRouterStride];
+  __shared__ float part[4][kRouterTok][NFR * 16 + 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lq = lane >> 4;
-  const int t0 = blockIdx.x * 256 + wave * 64;
-  f32x4_t acc[4][NFR];
+  const int t0 = blockIdx.x * kRouterTok;
+  const int kq = H / 4, k0 = wave * kq;
+  f32x4_t acc[2][NFR];
 #pragma unroll
-  for (int m = 0; m < 4; ++m)
+  for (int m = 0; m < 2; ++m)
 #pragma unroll
     for (int f = 0; f < NFR; ++f) acc[m][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const uint16_t* xr[4];
+  const uint16_t* xr[2];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) xr[m] = x + (size_t)min(t0 + 16 * m + l16, T - 1) * H + 8 * lq;
-  for (int k0 = 0; k0 < H; k0 += kRouterChunk) {
-    __syncthreads();
-    for (int i = tid; i < E * (kRouterChunk / 8); i += 256) {
-      const int e = i / (kRouterChunk / 8), c = i % (kRouterChunk / 8);
-      *reinterpret_cast<uint4*>(&ws[e * kRouterStride + 8 * c]) =
-          *reinterpret_cast<const uint4*>(w + (size_t)e * H + k0 + 8 * c);
-    }
-    __syncthreads();
+  for (int m = 0; m < 2; ++m) xr[m] = x + (size_t)min(t0 + 16 * m + l16, T - 1) * H + k0 + 8 * lq;
+  const uint16_t* wr = w + (size_t)l16 * H + k0 + 8 * lq;
+#pragma unroll 2
+  for (int kk = 0; kk < kq; kk += 32) {
+    uint4 a[2], b[NFR];
 #pragma unroll
-    for (int kk = 0; kk < kRouterChunk; kk += 32) {
-      uint4 a[4];
+    for (int m = 0; m < 2; ++m) a[m] = *reinterpret_cast<const uint4*>(xr[m] + kk);
 #pragma unroll
-      for (int m = 0; m < 4; ++m) a[m] = *reinterpret_cast<const uint4*>(xr[m] + k0 + kk);
+    for (int f = 0; f < NFR; ++f) b[f] = *reinterpret_cast<const uint4*>(wr + (size_t)16 * f * H + kk);
 #pragma unroll
-      for (int f = 0; f < NFR; ++f) {
-        const uint4 b = *reinterpret_cast<const uint4*>(&ws[(16 * f + l16) * kRouterStride + kk + 8 * lq]);
+    for (int f = 0; f < NFR; ++f)
 #pragma unroll
-        for (int m = 0; m < 4; ++m) acc[m][f] = mfma16(a[m], b, acc[m][f]);
-      }
-    }
+      for (int m = 0; m < 2; ++m) acc[m][f] = mfma16(a[m], b[f], acc[m][f]);
   }
 #pragma unroll
-  for (int m = 0; m < 4; ++m)
+  for (int m = 0; m < 2; ++m)
 #pragma unroll
-    for (int f = 0; f < NFR; ++f) {
+    for (int f = 0; f < NFR; ++f)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = t0 + 16 * m + 4 * lq + i;
-        if (t < T) logits[(size_t)t * E + 16 * f + l16] = acc[m][f][i];
-      }
-    }
+      for (int i = 0; i < 4; ++i) part[wave][16 * m + 4 * lq + i][16 * f + l16] = acc[m][f][i];
+  __syncthreads();
+  for (int idx = tid; idx < kRouterTok * E; idx += 256) {
+    const int r = idx / E, c = idx % E;
+    const int t = t0 + r;
+    if (t < T) logits[(size_t)t * E + c] = ((part[0][r][c] + part[1][r][c]) + part[2][r][c]) + part[3][r][c];
+  }
 }
 
 // numpy float32 sum order (pairwise_sum, n <= 128 per block of 8 partial sums).
@@ -690,39 +686,61 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
                                                       uint16_t* __restrict__ out, uint16_t* __restrict__ routed,
                                                       uint16_t* __restrict__ shared_out, int has_shared) {
   const int t = blockIdx.x;
-  __shared__ int ord[16];
-  if (threadIdx.x == 0) {
-    int prev = -1;
-    for (int r = 0; r < k; ++r) {
-      int best = 0x7fffffff, bs = 0;
-      for (int q = 0; q < k; ++q) {
-        const int eq = ids[(size_t)t * k + q];
-        if (eq > prev && eq < best) {
-          best = eq;
-          bs = q;
-        }
-      }
-      prev = best;
-      ord[r] = bs;
+  __shared__ int s_pos[16];
+  __shared__ float s_w[16];
+  // Route q goes to slot rank(q) = its place in ascending expert order.
+  if ((int)threadIdx.x < k) {
+    const int q = threadIdx.x, eq = ids[(size_t)t * k + q];
+    int rank = 0;
+    for (int q2 = 0; q2 < k; ++q2) {
+      const int e2 = ids[(size_t)t * k + q2];
+      rank += (e2 < eq) || (e2 == eq && q2 < q);
     }
+    s_pos[rank] = inv[(size_t)t * k + q];
+    s_w[rank] = wts[(size_t)t * k + q];
   }
   __syncthreads();
-  for (int c = threadIdx.x; c < H; c += blockDim.x) {
-    float acc = 0.f;
+  // 8 columns (16 bytes) per thread per pass.
+  for (int c0 = 8 * threadIdx.x; c0 < H; c0 += 8 * blockDim.x) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int r = 0; r < k; ++r) {
-      const int q = ord[r];
-      const int pos = inv[(size_t)t * k + q];
-      acc = __fadd_rn(acc, __fmul_rn(bf16_to_f32(D[(size_t)pos * H + c]), wts[(size_t)t * k + q]));
+      const uint4 v = *reinterpret_cast<const uint4*>(D + (size_t)s_pos[r] * H + c0);
+      const float w = s_w[r];
+      const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] = __fadd_rn(acc[2 * i], __fmul_rn(bf16_to_f32(vw[i] & 0xffffu), w));
+        acc[2 * i + 1] = __fadd_rn(acc[2 * i + 1], __fmul_rn(bf16_to_f32(vw[i] >> 16), w));
+      }
     }
-    uint32_t o = f32_to_bf16(acc);
-    if (routed) routed[(size_t)t * H + c] = (uint16_t)o;
+    uint32_t o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = f32_to_bf16(acc[i]);
+    if (routed)
+      *reinterpret_cast<uint4*>(routed + (size_t)t * H + c0) =
+          make_uint4(o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16));
     if (has_shared) {
-      const uint16_t sd = D[(size_t)(shared_base + t) * H + c];
-      if (shared_out) shared_out[(size_t)t * H + c] = sd;
-      o = f32_to_bf16(__fadd_rn(bf16_to_f32(o), bf16_to_f32(sd)));
+      const uint4 sv = *reinterpret_cast<const uint4*>(D + (size_t)(shared_base + t) * H + c0);
+      if (shared_out) *reinterpret_cast<uint4*>(shared_out + (size_t)t * H + c0) = sv;
+      const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o[2 * i] = f32_to_bf16(__fadd_rn(bf16_to_f32(o[2 * i]), bf16_to_f32(sw[i] & 0xffffu)));
+        o[2 * i + 1] = f32_to_bf16(__fadd_rn(bf16_to_f32(o[2 * i + 1]), bf16_to_f32(sw[i] >> 16)));
+      }
     }
-    if (x) o = f32_to_bf16(__fadd_rn(bf16_to_f32(x[(size_t)t * H + c]), bf16_to_f32(o)));
-    if (out) out[(size_t)t * H + c] = (uint16_t)o;
+    if (x) {
+      const uint4 xv = *reinterpret_cast<const uint4*>(x + (size_t)t * H + c0);
+      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o[2 * i] = f32_to_bf16(__fadd_rn(bf16_to_f32(xw[i] & 0xffffu), bf16_to_f32(o[2 * i])));
+        o[2 * i + 1] = f32_to_bf16(__fadd_rn(bf16_to_f32(xw[i] >> 16), bf16_to_f32(o[2 * i + 1])));
+      }
+    }
+    if (out)
+      *reinterpret_cast<uint4*>(out + (size_t)t * H + c0) =
+          make_uint4(o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16));
   }
 }
 
@@ -769,9 +787,8 @@ __global__ void shared_act_kernel(const uint16_t* __restrict__ gu, int T, int I,
 
 // ------------------------------------------------------------------ launchers --
 hipError_t launch_router_gemm(const uint16_t* x, int T, int H, const uint16_t* w, int E, float* logits, hipStream_t st) {
-  if (E % 16 || E > 16 * kMaxEFrags || H % 32) return hipErrorInvalidValue;
-  if (H % kRouterChunk) return hipErrorInvalidValue;
-  const dim3 grid((T + 255) / 256), block(256);
+  if (E % 16 || E > 16 * kMaxEFrags || H % 128) return hipErrorInvalidValue;
+  const dim3 grid((T + kRouterTok - 1) / kRouterTok), block(256);
   switch (E / 16) {
 #define RMOE_ROUTER_CASE(n) \
   case n:                   \
