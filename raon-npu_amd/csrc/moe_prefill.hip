@@ -362,15 +362,16 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void grouped_gemm_kernel(GemmArgs a, int tile_cap) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kGemmLds];
   __shared__ int rowidx[kBM];
-  // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs; make each XCD
-  // take a contiguous range of (n-tile, m-tile) so m-tiles sharing a weight tile meet
-  // in the same L2.
-  const int nb = gridDim.x, per = nb / 8;
-  const int lid = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs; each XCD takes a
+  // contiguous eighth of the tiles that exist (the grid is sized for the worst case, the
+  // tile count is known only here), so m-tiles sharing a weight tile meet in the same
+  // L2 and every XCD gets the same share.
+  const int n_act = a.n_tiles * *a.ntiles, per = (n_act + 7) / 8;
+  const int slot8 = blockIdx.x / 8, lid = (blockIdx.x % 8) * per + slot8;
+  if (slot8 >= per || lid >= n_act) return;
   // m-tile major: the n-tiles of one m-tile (sharing the gathered rows) and consecutive
   // m-tiles of one expert (sharing its weights) run back to back on one XCD.
   const int mt = lid / a.n_tiles, nt = lid % a.n_tiles;
-  if (nt >= a.n_tiles || mt >= *a.ntiles) return;
   const uint32_t te = a.tiles[mt];
   const int e = (int)(te & 511u), row0 = (int)(te >> 9);
   const int rend = group_end(a, e);
