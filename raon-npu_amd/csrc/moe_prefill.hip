@@ -553,10 +553,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (kt + 2 < nkt) issue(kt + 2);
     const uint8_t* xs = lds + slot * kStageBytes;
     const uint8_t* ws = xs + kXBytes + wrow0;
-    float sc[2][4];
+    // Operands of group j+1 (8 A fragments, 2 code words) are read while group j's
+    // MFMAs run.
+    auto read_a = [&](int j, uint4 (&av)[8]) {
+      const uint32_t xc = 16u * (uint32_t)((4 * j + lq) ^ l16);  // row % 16 == l16
+#pragma unroll
+      for (int m = 0; m < 8; ++m) av[m] = *reinterpret_cast<const uint4*>(xs + m * 4096 + xrow + xc);
+    };
+    auto read_codes = [&](int j, uint32_t (&cv)[2]) {
+#pragma unroll
+      for (int f = 0; f < 2; ++f) cv[f] = *reinterpret_cast<const uint32_t*>(ws + 2 * f * kTileBytes + j * 1024 + 4 * lq);
+    };
     uint4 smv[2];
 #pragma unroll
     for (int f = 0; f < 2; ++f) smv[f] = *reinterpret_cast<const uint4*>(ws + 2 * f * kTileBytes + kCodeBytes);
+    uint4 av[8];
+    uint32_t cv[2];
+    read_a(0, av);
+    read_codes(0, cv);
+    float sc[2][4];
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
       sc[f][0] = bf16_to_f32(smv[f].x & 0xffffu);
@@ -566,25 +581,34 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      uint4 avn[8];
+      uint32_t cvn[2];
+      if (j < 3) {
+        read_a(j + 1, avn);
+        read_codes(j + 1, cvn);
+      }
       uint4 b[2];
 #pragma unroll
       for (int f = 0; f < 2; ++f) {
-        const uint32_t v = *reinterpret_cast<const uint32_t*>(ws + 2 * f * kTileBytes + j * 1024 + 4 * lq);
-        b[f].x = and_or(v << 3, kmask, kone);
-        b[f].y = and_or(v >> 1, kmask, kone);
-        b[f].z = and_or(v >> 5, kmask, kone);
-        b[f].w = and_or(v >> 9, kmask, kone);
+        b[f].x = and_or(cv[f] << 3, kmask, kone);
+        b[f].y = and_or(cv[f] >> 1, kmask, kone);
+        b[f].z = and_or(cv[f] >> 5, kmask, kone);
+        b[f].w = and_or(cv[f] >> 9, kmask, kone);
       }
-      const uint32_t xc = 16u * (uint32_t)((4 * j + lq) ^ l16);  // row % 16 == l16
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
-        const uint4 av = *reinterpret_cast<const uint4*>(xs + m * 4096 + xrow + xc);
 #pragma unroll
         for (int f = 0; f < 2; ++f) {
-          const f32x4_t c = mfma16(av, b[f], f32x4_t{0.f, 0.f, 0.f, 0.f});
+          const f32x4_t c = mfma16(av[m], b[f], f32x4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[m][f][i] = fmaf(sc[f][j], c[i], acc[m][f][i]);
         }
+      }
+      if (j < 3) {
+#pragma unroll
+        for (int m = 0; m < 8; ++m) av[m] = avn[m];
+        cv[0] = cvn[0];
+        cv[1] = cvn[1];
       }
     }
   };
