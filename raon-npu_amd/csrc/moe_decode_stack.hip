@@ -32,6 +32,8 @@
 // taken in a fixed order.
 #include "rmoe_internal.h"
 
+#include <type_traits>
+
 namespace rmoe {
 namespace {
 
@@ -239,8 +241,7 @@ __device__ __forceinline__ bool wait_geq(const StackArgs& a, const unsigned* p, 
 
 struct SelectLds {
   float lg[kMaxE];                               // logits, then scores
-  __attribute__((aligned(16))) uint32_t key[kMaxE];  // ordered selection keys
-  int rank[kMaxE];
+  __attribute__((aligned(16))) uint64_t key[kMaxE];  // selection key << 8 | (255 - id): distinct, ordered
   int id[kMaxSlots];  // slot -> expert (routed slots by rank, then shared)
   float w[kMaxSlots];
   int ord[kMaxSlots]; // routed slots in ascending expert id
@@ -257,10 +258,27 @@ __device__ __forceinline__ uint32_t order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+// Wave-wide (64 lanes) max and sum on DPP: quad swaps, then the half-row and row
+// mirrors leave each row of 16 lanes holding its row's result; the four rows are
+// combined from lanes 0, 16, 32, 48 (a fixed order; every lane gets the same value).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_f32(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f32<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f32<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, dpp_f32<0x140>(v));  // row_mirror
+  return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = v + dpp_f32<0xB1>(v);
+  v = v + dpp_f32<0x4E>(v);
+  v = v + dpp_f32<0x141>(v);
+  v = v + dpp_f32<0x140>(v);
+  return (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
 }
 
 // Scores, top-k and weights of one token from sl.lg (every thread of the block):
@@ -271,99 +289,106 @@ __device__ __forceinline__ float wave_max(float v) {
 // renormalisation by (sum + 1e-20), scaling).  The softmax denominator and the
 // renormalisation sum are wave tree sums (a fixed order; numpy's pairwise order differs
 // in the last bit at most, and the selection does not depend on either sum).
-// rank(i) = #{j : key_j > key_i, or key_j == key_i and j < i} is counted by the whole
-// block, each thread over a contiguous quarter (or half) of the keys read 16 bytes at a
-// time; the selected ranks are then ordered by expert id from ballots.
+// Wave 0 computes the scores and keys; then rank(i) = #{j : key_j > key_i, or
+// key_j == key_i and j < i} is counted for 16 keys per wave and pass (lane l: key
+// 16g + l%16 against quarter l/16 of the keys, the quarters added by shuffles); the
+// keys of rank < k write their slot; wave 0 then orders the slots by expert id and
+// renormalises.
 __device__ __forceinline__ void select_topk(const SelectParams a, const float* __restrict__ bias, SelectLds& sl) {
   constexpr int NC = kMaxE / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int E = a.E;
+  const int E = a.E, K = a.k;
+  const int nc = (E + 63) >> 6;  // 64-key chunks; keys in [E, 64*nc) are 0
   if (wave == 0) {
     float sc[NC];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) sc[c] = lane + 64 * c < E ? sl.lg[lane + 64 * c] : -__builtin_inff();
+    for (int c = 0; c < NC; ++c) sc[c] = c < nc && lane + 64 * c < E ? sl.lg[lane + 64 * c] : -__builtin_inff();
     if (a.score == 0) {
 #pragma unroll
-      for (int c = 0; c < NC; ++c) sc[c] = 1.0f / (1.0f + expf(-sc[c]));
+      for (int c = 0; c < NC; ++c)
+        if (c < nc) sc[c] = 1.0f / (1.0f + expf(-sc[c]));
     } else {
       float m = sc[0];
 #pragma unroll
       for (int c = 1; c < NC; ++c) m = fmaxf(m, sc[c]);
-      m = wave_max(m);
+      m = wave_max_dpp(m);
       float z = 0.f;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        sc[c] = lane + 64 * c < E ? expf(sc[c] - m) : 0.f;
-        z += sc[c];
+        if (c < nc) {
+          sc[c] = lane + 64 * c < E ? expf(sc[c] - m) : 0.f;
+          z += sc[c];
+        }
       }
-      z = wave_sum(z);
+      z = wave_sum_dpp(z);
 #pragma unroll
-      for (int c = 0; c < NC; ++c) sc[c] = sc[c] / z;
+      for (int c = 0; c < NC; ++c)
+        if (c < nc) sc[c] = sc[c] / z;
     }
+    const int ncp = nc <= 2 ? 2 : 4;  // the rank pass reads 128 or 256 keys
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int e = lane + 64 * c;
-      // Padded entries (e >= E) sort below every real key and are never counted.
-      sl.key[e] = e < E ? order_key(bias ? __fadd_rn(sc[c], bias[e]) : sc[c]) : 0u;
-      sl.lg[e] = sc[c];
-      sl.rank[e] = 0;
+      if (c < ncp) {
+        const int e = lane + 64 * c;
+        // Padded entries (e >= E) sort below every real key and are never selected.
+        const uint32_t k32 = e < E ? order_key(bias ? __fadd_rn(sc[c], bias[e]) : sc[c]) : 0u;
+        sl.key[e] = e < E ? ((uint64_t)k32 << 8) | (uint64_t)(255 - e) : 0ull;
+        sl.lg[e] = sc[c];
+      }
     }
   }
   __syncthreads();
   {
-    const int Ep = E <= 128 ? 128 : 256;
-    const int P = kThreads / Ep;  // parts of the key range
-    const int i = tid % Ep, p = tid / Ep;
-    const int len = Ep / P;       // 32 or 128 keys per part
-    const uint32_t ki = sl.key[i];
-    const uint4* kp = reinterpret_cast<const uint4*>(sl.key + p * len);
-    int cnt = 0;
-    for (int j0 = 0; j0 < len; j0 += 32) {
-      uint4 kv[8];
+    // rank(i) = #{j : key_j > key_i}; the id in the low bits breaks ties toward the lower
+    // id.  Keys are counted over 128 (E <= 128) or 256 entries.  All of a lane's quarter
+    // is read before the compares (one LDS round trip).
+    auto rank_pass = [&](auto QW) {
+      constexpr int qw = decltype(QW)::value;  // uint4 words (2 keys each) per quarter
+      const int q = lane >> 4;
+      const uint4* kq = reinterpret_cast<const uint4*>(sl.key) + q * qw;
+      for (int g = wave; g < qw / 2; g += kWaves) {  // 8*qw keys = qw/2 groups of 16
+        const int i = 16 * g + (lane & 15);
+        const uint64_t ki = sl.key[i];
+        uint4 kv[qw];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) kv[q] = kp[j0 / 4 + q];
+        for (int j2 = 0; j2 < qw; ++j2) kv[j2] = kq[j2];
+        int cnt = 0;
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const uint32_t kk[4] = {kv[q].x, kv[q].y, kv[q].z, kv[q].w};
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = p * len + j0 + 4 * q + r;
-          cnt += (kk[r] > ki || (kk[r] == ki && j < i)) ? 1 : 0;
+        for (int j2 = 0; j2 < qw; ++j2) {
+          const uint64_t k0 = (uint64_t)kv[j2].x | ((uint64_t)kv[j2].y << 32);
+          const uint64_t k1 = (uint64_t)kv[j2].z | ((uint64_t)kv[j2].w << 32);
+          cnt += (k0 > ki) ? 1 : 0;
+          cnt += (k1 > ki) ? 1 : 0;
+        }
+        cnt += __shfl_xor(cnt, 16, 64);
+        cnt += __shfl_xor(cnt, 32, 64);
+        if (lane < 16 && i < E && cnt < K) {
+          sl.id[cnt] = i;
+          sl.w[cnt] = sl.lg[i];
         }
       }
-    }
-    if (i < E) atomicAdd(&sl.rank[i], cnt);
+    };
+    if (nc <= 2) rank_pass(std::integral_constant<int, 16>{});
+    else rank_pass(std::integral_constant<int, 32>{});
   }
   __syncthreads();
   if (wave == 0) {
-    unsigned long long sel[NC];
-    int below = 0;
+    // Slots past k hold a sentinel id while the selected ones are ordered by id (the
+    // shared expert's slot is written afterwards).
+    if (lane >= K && lane < kMaxSlots) sl.id[lane] = 0x7fffffff;
+    if (lane < K) {
+      const int id = sl.id[lane];
+      int pos = 0;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int e = lane + 64 * c;
-      const int r = e < E ? sl.rank[e] : a.k;
-      sel[c] = __ballot(r < a.k);
-      if (r < a.k) {
-        sl.id[r] = e;
-        sl.w[r] = sl.lg[e];
-        sl.ord[below + __popcll(sel[c] & ((1ull << lane) - 1ull))] = r;
-      }
-      below += __popcll(sel[c]);
+      for (int r = 0; r < kMaxSlots; ++r) pos += sl.id[r] < id ? 1 : 0;
+      sl.ord[pos] = lane;
     }
-    if (below != a.k && lane == 0) {
-      // Only unordered keys (NaN) can leave ranks unfilled: name valid experts, weight 0.
-      for (int r = 0; r < a.k; ++r) {
-        sl.id[r] = r;
-        sl.w[r] = 0.f;
-        sl.ord[r] = r;
-      }
-    }
-    const float wr = lane < a.k ? sl.w[lane] : 0.f;
-    const float denom = a.renorm ? __fadd_rn(wave_sum(wr), 1e-20f) : 1.f;
-    if (lane < a.k) sl.w[lane] = __fmul_rn(a.renorm ? wr / denom : wr, a.scaling);
-    if (lane == 0 && a.S > a.k) {
-      sl.id[a.k] = a.E;  // shared expert
-      sl.w[a.k] = 1.f;
+    const float wr = lane < K ? sl.w[lane] : 0.f;
+    const float denom = a.renorm ? __fadd_rn(wave_sum_dpp(wr), 1e-20f) : 1.f;
+    if (lane < K) sl.w[lane] = __fmul_rn(a.renorm ? wr / denom : wr, a.scaling);
+    if (lane == 0 && a.S > K) {
+      sl.id[K] = a.E;  // shared expert
+      sl.w[K] = 1.f;
     }
   }
   __syncthreads();
