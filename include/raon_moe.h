@@ -50,6 +50,10 @@ extern "C" {
 #define RMOE_SCORE_SIGMOID 0
 #define RMOE_SCORE_SOFTMAX 1
 
+/* Weight formats of a dense matrix (BundleMeta.fmt, npu/backend.py:104-117). */
+#define RMOE_FMT_Q4NX 0  /* "q4nx_gemv": 5 bits per weight (quant/q4nx.py:335-393)       */
+#define RMOE_FMT_BFP16 1 /* "bfp16_gemv": bfp16ebs8, 9 bits per weight (quant/bfp16.py) */
+
 typedef struct rmoe_ctx rmoe_ctx;
 
 /* Message of the last failed call on this thread ("" if none). */
@@ -67,8 +71,8 @@ int rmoe_synchronize(rmoe_ctx* ctx);
 /* The context's HIP stream, as void*. */
 void* rmoe_stream(rmoe_ctx* ctx);
 
-/* ---------------------------------------------------------------- q4nx matrices --
- * Dense q4nx matrices ("bundles" of npu/backend.py:360-392, e.g. dense_gu) served by
+/* --------------------------------------------------------------- dense matrices --
+ * Dense q4nx or bfp16 matrices ("bundles" of npu/backend.py:360-392, e.g. dense_gu) served by
  * rmoe_linear.  M % 128 == 0 and K % 256 == 0 (quant/q4nx.py:358-366).          */
 
 /* Upload pack_gemv bytes of an [M, K] matrix; returns a handle.  Replaces the bundle
@@ -82,8 +86,18 @@ int rmoe_matrix_download(rmoe_ctx* ctx, int handle, void* pack_gemv_bytes, size_
 int rmoe_matrix_free(rmoe_ctx* ctx, int handle);
 int rmoe_matrix_shape(rmoe_ctx* ctx, int handle, int* M, int* K);
 
+/* Upload the 9-bit bfp16ebs8 GEMV bytes of an [M, K] matrix (pack_bfp16_gemv with the
+ * NPU's 4 core rows, quant/bfp16.py:216-329; M*K*9/8 bytes, M % 128 == 0, K % 256 == 0);
+ * returns a handle served by rmoe_linear / rmoe_linear_dev / rmoe_matrix_download like a
+ * q4nx matrix.  Replaces the "bfp16_gemv" bundle load (npu/backend.py:744-746) and the
+ * GEMV_BFP16 operator's weight argument (kernels/gemv_bfp16/op.py:93-103); the GEMV
+ * decodes m * 2^(max(e,7) - 133) exactly (kernels/gemv_bfp16/bfp16_gemv.cc:8-22). */
+int rmoe_matrix_upload_bfp16(rmoe_ctx* ctx, const void* gemv_bytes, size_t nbytes, int M, int K, int* handle);
+/* RMOE_FMT_* of a matrix (rmoe_matrix_download returns that format's bytes). */
+int rmoe_matrix_format(rmoe_ctx* ctx, int handle, int* fmt);
+
 /* y[T, M] = RTNE_bf16(x[T, K] @ W^T), fp32 accumulation.  Replaces NpuBackend.linear /
- * _execute_gemv for a q4nx bundle (npu/backend.py:3569-3721, 3908-4021) and
+ * _execute_gemv for a q4nx or bfp16 bundle (npu/backend.py:3569-3721, 3908-4021) and
  * Backend.linear_batch (host/backend.py:71-74).  K_in <= K: columns past K_in are zero
  * padding (comp.padded_k > comp.orig_k, npu/backend.py:3680-3684). */
 int rmoe_linear(rmoe_ctx* ctx, int handle, const uint16_t* x, int T, int K_in, uint16_t* y);

@@ -22,6 +22,8 @@ ACT_SITU = 0
 ACT_SWIGLU = 1
 SCORE_SIGMOID = 0
 SCORE_SOFTMAX = 1
+FMT_Q4NX = 0
+FMT_BFP16 = 1
 
 _p = C.c_void_p
 _i = C.c_int
@@ -42,6 +44,8 @@ SIGNATURES: dict[str, list] = {
     "rmoe_matrix_download": [_p, _i, _p, _sz],
     "rmoe_matrix_free": [_p, _i],
     "rmoe_matrix_shape": [_p, _i, _pi, _pi],
+    "rmoe_matrix_upload_bfp16": [_p, _p, _sz, _i, _i, _pi],
+    "rmoe_matrix_format": [_p, _i, _pi],
     "rmoe_linear": [_p, _i, _p, _i, _i, _p],
     "rmoe_linear_dev": [_p, _i, _p, _i, _p, _p],
     "rmoe_reserve_linear": [_p, _i, _i],

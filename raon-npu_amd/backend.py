@@ -98,9 +98,15 @@ class GpuBackend:
         self._cached_inputs.clear()
 
     # ---------------------------------------------------------- registration --
-    def register_bundle(self, bundle: str, packed: bytes | np.ndarray, M: int, K: int) -> None:
-        """Upload one q4nx bundle (pack_gemv bytes of an [M, K] matrix)."""
-        self._bundles[bundle] = self.ctx.upload_matrix(packed, M, K)
+    _FORMATS = {"q4nx_gemv": "q4nx", "bfp16_gemv": "bfp16"}
+
+    def register_bundle(self, bundle: str, packed: bytes | np.ndarray, M: int, K: int, fmt: str = "q4nx_gemv") -> None:
+        """Upload one dense bundle: GEMV bytes of an [M, K] matrix in the reference's
+        ``BundleMeta.fmt`` (npu/backend.py:104-117): "q4nx_gemv" (quant/q4nx.py pack_gemv)
+        or "bfp16_gemv" (quant/bfp16.py pack_bfp16_gemv)."""
+        if fmt not in self._FORMATS:
+            raise ValueError(f"Unknown bundle format for {bundle}: {fmt!r}")
+        self._bundles[bundle] = self.ctx.upload_matrix(packed, M, K, fmt=self._FORMATS[fmt])
 
     def register_component(self, name: str, bundle: str, row_start: int, row_end: int, orig_k: int | None = None) -> None:
         """Serve weight ``name`` as rows ``[row_start, row_end)`` of ``bundle``."""
@@ -140,7 +146,7 @@ class GpuBackend:
         return self._bundles[comp.bundle], comp
 
     def linear(self, name: str, x: np.ndarray) -> np.ndarray:
-        """``y = x @ W^T`` over a q4nx bundle row slice (npu/backend.py:3569-3721).
+        """``y = x @ W^T`` over a q4nx or bfp16 bundle row slice (npu/backend.py:3569-3721).
 
         bf16 (uint16) input gives bf16 output.  fp32 input is rounded to bf16 for
         the GEMV and the bf16 result is returned as fp32, as the NPU path does.

@@ -274,6 +274,31 @@ int rmoe_matrix_upload(rmoe_ctx* ctx, const void* bytes, size_t nbytes, int M, i
   return RMOE_OK;
 }
 
+int rmoe_matrix_upload_bfp16(rmoe_ctx* ctx, const void* bytes, size_t nbytes, int M, int K, int* handle) {
+  if (!ctx || !bytes || !handle) return fail(RMOE_EINVAL, "null argument");
+  TRY(check_mk(M, K));
+  const size_t need = rmoe::matrix_bytes_bfp16(M, K);
+  if (nbytes != need)
+    return fail(RMOE_EINVAL, "bfp16 GEMV buffer has %zu bytes, expected %zu for [%d, %d]", nbytes, need, M, K);
+  HIP_TRY(hipSetDevice(ctx->device));
+  RmoeMatrix m;
+  m.M = M;
+  m.K = K;
+  m.fmt = RMOE_FMT_BFP16;
+  if (hipMalloc((void**)&m.tiles, need) != hipSuccess) return fail(RMOE_ENOMEM, "hipMalloc of %zu bytes failed", need);
+  int r = grow(ctx->s.staging, ctx->s.staging_bytes, need, ctx);
+  if (r != RMOE_OK) {
+    hipFree(m.tiles);
+    return r;
+  }
+  HIP_TRY(hipMemcpyAsync(ctx->s.staging, bytes, need, hipMemcpyHostToDevice, ctx->stream));
+  HIP_TRY(rmoe::launch_b16_relayout_in(ctx->s.staging, m.tiles, M, K, ctx->stream));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  *handle = ctx->next_handle++;
+  ctx->mats[*handle] = m;
+  return RMOE_OK;
+}
+
 int rmoe_matrix_quantize_dev(rmoe_ctx* ctx, const float* w_dev, int M, int K, int* handle, void* stream) {
   if (!ctx || !w_dev || !handle) return fail(RMOE_EINVAL, "null argument");
   TRY(check_mk(M, K));
@@ -303,14 +328,21 @@ static int find_matrix(rmoe_ctx* ctx, int handle, RmoeMatrix** out) {
   return RMOE_OK;
 }
 
+static size_t stored_bytes(const RmoeMatrix& m) {
+  return m.fmt == RMOE_FMT_BFP16 ? rmoe::matrix_bytes_bfp16(m.M, m.K) : rmoe::matrix_bytes(m.M, m.K);
+}
+
 int rmoe_matrix_download(rmoe_ctx* ctx, int handle, void* bytes, size_t nbytes) {
   RmoeMatrix* m;
   TRY(find_matrix(ctx, handle, &m));
-  const size_t need = rmoe::matrix_bytes(m->M, m->K);
+  const size_t need = stored_bytes(*m);
   if (!bytes || nbytes != need) return fail(RMOE_EINVAL, "download buffer must hold %zu bytes", need);
   HIP_TRY(hipSetDevice(ctx->device));
   TRY(grow(ctx->s.staging, ctx->s.staging_bytes, need, ctx));
-  HIP_TRY(rmoe::launch_relayout_out(m->tiles, ctx->s.staging, m->M, m->K, ctx->stream));
+  if (m->fmt == RMOE_FMT_BFP16)
+    HIP_TRY(rmoe::launch_b16_relayout_out(m->tiles, ctx->s.staging, m->M, m->K, ctx->stream));
+  else
+    HIP_TRY(rmoe::launch_relayout_out(m->tiles, ctx->s.staging, m->M, m->K, ctx->stream));
   HIP_TRY(hipMemcpyAsync(bytes, ctx->s.staging, need, hipMemcpyDeviceToHost, ctx->stream));
   HIP_TRY(hipStreamSynchronize(ctx->stream));
   return RMOE_OK;
@@ -331,6 +363,20 @@ int rmoe_matrix_shape(rmoe_ctx* ctx, int handle, int* M, int* K) {
   if (M) *M = m->M;
   if (K) *K = m->K;
   return RMOE_OK;
+}
+
+int rmoe_matrix_format(rmoe_ctx* ctx, int handle, int* fmt) {
+  RmoeMatrix* m;
+  TRY(find_matrix(ctx, handle, &m));
+  if (!fmt) return fail(RMOE_EINVAL, "null argument");
+  *fmt = m->fmt;
+  return RMOE_OK;
+}
+
+static hipError_t launch_matrix_linear(const RmoeMatrix& m, const uint16_t* x, int T, uint16_t* y, RmoeScratch& s,
+                                       hipStream_t st) {
+  if (m.fmt == RMOE_FMT_BFP16) return rmoe::launch_linear_bfp16(m.tiles, m.M, m.K, x, T, y, s, st);
+  return rmoe::launch_linear(m.tiles, m.M, m.K, x, T, y, s, st);
 }
 
 int rmoe_linear(rmoe_ctx* ctx, int handle, const uint16_t* x, int T, int K_in, uint16_t* y) {
@@ -356,7 +402,7 @@ int rmoe_linear(rmoe_ctx* ctx, int handle, const uint16_t* x, int T, int K_in, u
     HIP_TRY(hipMemcpy2DAsync(xd, (size_t)m->K * 2, x, (size_t)K_in * 2, (size_t)K_in * 2, T, hipMemcpyHostToDevice,
                              ctx->stream));
   }
-  HIP_TRY(rmoe::launch_linear(m->tiles, m->M, m->K, xd, T, yd, ctx->s, ctx->stream));
+  HIP_TRY(launch_matrix_linear(*m, xd, T, yd, ctx->s, ctx->stream));
   HIP_TRY(hipMemcpyAsync(y, yd, yb, hipMemcpyDeviceToHost, ctx->stream));
   HIP_TRY(hipStreamSynchronize(ctx->stream));
   return RMOE_OK;
@@ -370,8 +416,7 @@ int rmoe_linear_dev(rmoe_ctx* ctx, int handle, const void* x_dev, int T, void* y
   linear_needs(m->M, m->K, T, f, c);
   if (f > ctx->s.part_floats || c > ctx->s.n_counters)
     return fail(RMOE_EINVAL, "scratch too small for T=%d: call rmoe_reserve_linear first", T);
-  HIP_TRY(rmoe::launch_linear(m->tiles, m->M, m->K, (const uint16_t*)x_dev, T, (uint16_t*)y_dev, ctx->s,
-                              pick_stream(ctx, stream)));
+  HIP_TRY(launch_matrix_linear(*m, (const uint16_t*)x_dev, T, (uint16_t*)y_dev, ctx->s, pick_stream(ctx, stream)));
   return RMOE_OK;
 }
 

@@ -32,6 +32,11 @@ constexpr int kCodeBytes = 4096;
 
 inline size_t matrix_bytes(int M, int K) { return (size_t)M * (size_t)K * 5 / 8; }
 
+// bfp16ebs8 matrices (bfp16_gemv.hip): 9 bits per weight in tiles of 64 rows x 128
+// columns, 9,216 bytes each (8,192 B of int8 mantissas, then 1,024 B of exponents).
+constexpr int kB16TileBytes = 9216;
+inline size_t matrix_bytes_bfp16(int M, int K) { return (size_t)M * (size_t)K * 9 / 8; }
+
 // ------------------------------------------------------------- device helpers --
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
@@ -171,8 +176,9 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // ------------------------------------------------------------------- context --
 struct RmoeMatrix {
-  uint8_t* tiles = nullptr;  // device, tile layout
+  uint8_t* tiles = nullptr;  // device, tile layout of the format
   int M = 0, K = 0;
+  int fmt = 0;               // RMOE_FMT_Q4NX or RMOE_FMT_BFP16
 };
 
 struct RmoeLayer {
@@ -247,6 +253,14 @@ hipError_t launch_synth_quantize(uint64_t seed, float std, int M, int K, int k_v
 
 hipError_t launch_linear(const uint8_t* tiles, int M, int K, const uint16_t* x, int T, uint16_t* y, RmoeScratch& s,
                          hipStream_t st);
+
+// bfp16ebs8 (bfp16_gemv.hip).  The GEMV splits K over bfp16_ksplit(M, K) workgroups
+// (at most (K/128 + 3)/4, so the q4nx scratch sizing covers it).
+hipError_t launch_b16_relayout_in(const uint8_t* packed, uint8_t* tiles, int M, int K, hipStream_t st);
+hipError_t launch_b16_relayout_out(const uint8_t* tiles, uint8_t* packed, int M, int K, hipStream_t st);
+int bfp16_ksplit(int M, int K);
+hipError_t launch_linear_bfp16(const uint8_t* tiles, int M, int K, const uint16_t* x, int T, uint16_t* y,
+                               RmoeScratch& s, hipStream_t st);
 
 hipError_t launch_route(const RmoeLayer& L, const uint16_t* x, int T, int32_t* ids, float* wts, float* logits,
                         RmoeScratch& s, hipStream_t st);

@@ -85,11 +85,18 @@ class Context:
         call("rmoe_synchronize", self._h)
 
     # ------------------------------------------------------------ matrices --
-    def upload_matrix(self, packed: bytes | np.ndarray, M: int, K: int) -> "Matrix":
+    def upload_matrix(self, packed: bytes | np.ndarray, M: int, K: int, fmt: str = "q4nx") -> "Matrix":
+        """Upload GEMV bytes of an [M, K] matrix: ``fmt`` "q4nx" (quant/q4nx.py pack_gemv)
+        or "bfp16" (quant/bfp16.py pack_bfp16_gemv, 9 bits per weight)."""
         buf = np.frombuffer(packed, dtype=np.uint8) if isinstance(packed, (bytes, bytearray)) else np.ascontiguousarray(packed, dtype=np.uint8)
         h = C.c_int()
-        call("rmoe_matrix_upload", self._h, ptr(buf), buf.size, int(M), int(K), C.byref(h))
-        return Matrix(self, h.value, M, K)
+        if fmt == "q4nx":
+            call("rmoe_matrix_upload", self._h, ptr(buf), buf.size, int(M), int(K), C.byref(h))
+        elif fmt == "bfp16":
+            call("rmoe_matrix_upload_bfp16", self._h, ptr(buf), buf.size, int(M), int(K), C.byref(h))
+        else:
+            raise ValueError(f"unknown matrix format {fmt!r} (expected 'q4nx' or 'bfp16')")
+        return Matrix(self, h.value, M, K, fmt)
 
     def quantize_matrix(self, w_dev, M: int, K: int, stream=None) -> "Matrix":
         """Quantize an fp32 torch tensor [M, K] on the device (bit-exact quant/q4nx.py:127-200)."""
@@ -152,13 +159,20 @@ class Context:
 
 
 class Matrix:
-    """A q4nx matrix resident on the device (tile layout)."""
+    """A q4nx or bfp16 matrix resident on the device (tile layout of its format)."""
 
-    def __init__(self, ctx: Context, handle: int, M: int, K: int):
-        self.ctx, self.handle, self.M, self.K = ctx, handle, int(M), int(K)
+    _BITS = {"q4nx": 5, "bfp16": 9}
+
+    def __init__(self, ctx: Context, handle: int, M: int, K: int, fmt: str = "q4nx"):
+        self.ctx, self.handle, self.M, self.K, self.fmt = ctx, handle, int(M), int(K), fmt
+
+    @property
+    def nbytes(self) -> int:
+        """Bytes of the matrix in its GEMV byte layout (also its device footprint)."""
+        return self.M * self.K * self._BITS[self.fmt] // 8
 
     def download(self) -> bytes:
-        out = np.empty(self.M * self.K * 5 // 8, dtype=np.uint8)
+        out = np.empty(self.nbytes, dtype=np.uint8)
         call("rmoe_matrix_download", self.ctx.handle, self.handle, ptr(out), out.size)
         return out.tobytes()
 
