@@ -103,7 +103,7 @@ __global__ __launch_bounds__(256) void b16_relayout_out_kernel(const uint8_t* __
 
 // ------------------------------------------------------------------------ GEMV --
 constexpr int kNT = 4;         // tokens per workgroup
-constexpr int kMaxRange = 32;  // K tiles per workgroup (x staged in LDS: 32 KB)
+constexpr int kMaxRange = 32;  // K tiles per workgroup (x staged in LDS: <= 32 KB)
 constexpr int kFillGroups = 2048;  // split K until the grid has about this many workgroups
 
 struct B16Args {
@@ -133,7 +133,9 @@ __device__ __forceinline__ void mant_pairs(uint32_t w, uint32_t& p0, uint32_t& p
 __device__ __forceinline__ float exp_scale(uint32_t e) { return __uint_as_float((max(e, 7u) - 6u) << 23); }
 
 __global__ __launch_bounds__(256) void linear_bfp16_kernel(B16Args a) {
-  __shared__ uint32_t xs[kNT][kMaxRange * 64];  // bf16 pairs: 128 columns per tile
+  // Dynamic LDS: x of the K range as bf16 pairs [kNT][per * 64] (128 columns per tile),
+  // sized by the launch for per = the range length.
+  extern __shared__ __attribute__((aligned(16))) uint32_t xs[];
   __shared__ float red[4][kNT][64];
   __shared__ unsigned last_flag;
 
@@ -149,10 +151,11 @@ __global__ __launch_bounds__(256) void linear_bfp16_kernel(B16Args a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nwaves = blockDim.x >> 6;
 
+  const int xstride = per * 64;
   const int xdw = nrange * 64;
   for (int i = tid; i < nt * xdw; i += blockDim.x) {
     const int t = i / xdw, c = i % xdw;
-    xs[t][c] = reinterpret_cast<const uint32_t*>(a.x + (size_t)(tok0 + t) * a.K + kt0 * kTileCols)[c];
+    xs[t * xstride + c] = reinterpret_cast<const uint32_t*>(a.x + (size_t)(tok0 + t) * a.K + kt0 * kTileCols)[c];
   }
   __syncthreads();
 
@@ -179,7 +182,7 @@ __global__ __launch_bounds__(256) void linear_bfp16_kernel(B16Args a) {
 #pragma unroll
         for (int t = 0; t < kNT; ++t) {
           if (t < nt) {
-            const uint4 xv = *reinterpret_cast<const uint4*>(&xs[t][it * 64 + g * 4]);
+            const uint4 xv = *reinterpret_cast<const uint4*>(xs + t * xstride + it * 64 + g * 4);
             float d = dot2_bf16(p[4 * gg], xv.x, 0.f);
             d = dot2_bf16(p[4 * gg + 1], xv.y, d);
             d = dot2_bf16(p[4 * gg + 2], xv.z, d);
@@ -247,7 +250,8 @@ hipError_t launch_linear_bfp16(const uint8_t* tiles, int M, int K, const uint16_
   if (per > kMaxRange) return hipErrorInvalidValue;
   B16Args a{tiles, M, K, x, T, y, s.part, s.counters, ksplit};
   const int threads = 64 * std::min(4, per);
-  hipLaunchKernelGGL(linear_bfp16_kernel, dim3(n_rt * ksplit, ychunks), dim3(threads), 0, st, a);
+  const size_t lds = (size_t)kNT * per * 64 * 4;
+  hipLaunchKernelGGL(linear_bfp16_kernel, dim3(n_rt * ksplit, ychunks), dim3(threads), lds, st, a);
   return hipGetLastError();
 }
 

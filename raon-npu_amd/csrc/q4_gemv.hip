@@ -7,13 +7,16 @@
 // to four waves covers one 64-row band over a range of K tiles; bands split over K
 // write fp32 partials and the last workgroup of a band (device-scope counter) adds
 // them in K order, so the result does not depend on arrival order.
+#include <algorithm>
+
 #include "rmoe_internal.h"
 
 namespace rmoe {
 namespace {
 
-constexpr int kNT = 4;         // tokens per workgroup
-constexpr int kMaxRange = 4;   // K tiles per workgroup (one per wave)
+constexpr int kNT = 4;             // tokens per workgroup
+constexpr int kMaxRange = 32;      // K tiles per workgroup (x and group sums in LDS: <= 34 KB)
+constexpr int kFillGroups = 2048;  // split K until the grid has about this many workgroups
 
 struct LinearArgs {
   const uint8_t* tiles;
@@ -27,8 +30,9 @@ struct LinearArgs {
 };
 
 __global__ __launch_bounds__(256) void linear_kernel(LinearArgs a) {
-  __shared__ uint32_t xs[kNT][kMaxRange * 64];  // bf16 pairs: 128 columns per tile
-  __shared__ float ssum[kNT][kMaxRange * 4];
+  // Dynamic LDS: x of the K range as bf16 pairs [kNT][per * 64] (128 columns per tile),
+  // then the group sums [kNT][per * 4]; sized by the launch for per = the range length.
+  extern __shared__ __attribute__((aligned(16))) uint32_t lin_lds[];
   __shared__ float red[4][kNT][64];
   __shared__ unsigned last_flag;
 
@@ -43,25 +47,26 @@ __global__ __launch_bounds__(256) void linear_kernel(LinearArgs a) {
   const int nrange = max(0, min(per, nkt - kt0));
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nwaves = blockDim.x >> 6;
+  const int xstride = per * 64;
+  uint32_t* xs = lin_lds;
+  float* ssum = reinterpret_cast<float*>(lin_lds + kNT * xstride);
 
   // Stage x (bf16 pairs) for this K range and the per-group sums S.
   const int xdw = nrange * 64;
-  for (int i = tid; i < kNT * xdw; i += blockDim.x) {
+  for (int i = tid; i < nt * xdw; i += blockDim.x) {
     const int t = i / xdw, c = i % xdw;
-    uint32_t v = 0u;
-    if (t < nt) v = reinterpret_cast<const uint32_t*>(a.x + (size_t)(tok0 + t) * a.K + kt0 * kTileCols)[c];
-    xs[t][c] = v;
+    xs[t * xstride + c] = reinterpret_cast<const uint32_t*>(a.x + (size_t)(tok0 + t) * a.K + kt0 * kTileCols)[c];
   }
   __syncthreads();
-  for (int i = tid; i < kNT * nrange * 4; i += blockDim.x) {
+  for (int i = tid; i < nt * nrange * 4; i += blockDim.x) {
     const int t = i / (nrange * 4), gi = i % (nrange * 4);
     float s = 0.f;
     for (int c = 0; c < 16; ++c) {
-      const uint32_t v = xs[t][gi * 16 + c];
+      const uint32_t v = xs[t * xstride + gi * 16 + c];
       s += bf16_to_f32(v & 0xffffu);
       s += bf16_to_f32(v >> 16);
     }
-    ssum[t][gi] = s;
+    ssum[t * per * 4 + gi] = s;
   }
   __syncthreads();
 
@@ -80,8 +85,8 @@ __global__ __launch_bounds__(256) void linear_kernel(LinearArgs a) {
 #pragma unroll
       for (int t = 0; t < kNT; ++t) {
         if (t < nt) {
-          const float d = group_dot(c[j], &xs[t][it * 64 + j * 16]);
-          acc[t] = group_apply(sm[j], d, ssum[t][it * 4 + j], acc[t]);
+          const float d = group_dot(c[j], xs + t * xstride + it * 64 + j * 16);
+          acc[t] = group_apply(sm[j], d, ssum[t * per * 4 + it * 4 + j], acc[t]);
         }
       }
     }
@@ -115,15 +120,20 @@ __global__ __launch_bounds__(256) void linear_kernel(LinearArgs a) {
 hipError_t launch_linear(const uint8_t* tiles, int M, int K, const uint16_t* x, int T, uint16_t* y, RmoeScratch& s,
                          hipStream_t st) {
   const int nkt = K / kTileCols, n_rt = M / kTileRows;
-  int ksplit = (nkt + kMaxRange - 1) / kMaxRange;
+  // Up to 4 K tiles per workgroup (one per wave); tall matrices, whose row bands alone
+  // fill the chip, split K less (down to one workgroup per band) and skip the partials.
+  int ksplit = std::min((nkt + 3) / 4, (kFillGroups + n_rt - 1) / n_rt);
+  ksplit = std::max({1, ksplit, (nkt + kMaxRange - 1) / kMaxRange});
   const int ychunks = (T + kNT - 1) / kNT;
   const size_t need_part = (size_t)ychunks * n_rt * ksplit * kNT * 64;
   const size_t need_cnt = (size_t)ychunks * n_rt;
   if (ksplit > 1 && (need_part > s.part_floats || need_cnt > s.n_counters)) return hipErrorInvalidValue;
   const int per = (nkt + ksplit - 1) / ksplit;
+  if (per > kMaxRange) return hipErrorInvalidValue;
   LinearArgs a{tiles, M, K, x, T, y, s.part, s.counters, ksplit};
   const int threads = 64 * min(4, per);
-  hipLaunchKernelGGL(linear_kernel, dim3(n_rt * ksplit, ychunks), dim3(threads), 0, st, a);
+  const size_t lds = (size_t)kNT * per * (64 + 4) * 4;
+  hipLaunchKernelGGL(linear_kernel, dim3(n_rt * ksplit, ychunks), dim3(threads), lds, st, a);
   return hipGetLastError();
 }
 
