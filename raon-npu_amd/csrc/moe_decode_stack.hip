@@ -241,7 +241,7 @@ __device__ __forceinline__ bool wait_geq(const StackArgs& a, const unsigned* p, 
 
 struct SelectLds {
   float lg[kMaxE];                               // logits, then scores
-  __attribute__((aligned(16))) uint64_t key[kMaxE];  // selection key << 8 | (255 - id): distinct, ordered
+  __attribute__((aligned(16))) uint64_t key[kMaxE + 8];  // selection key << 8 | (255 - id), at key_pos
   int id[kMaxSlots];  // slot -> expert (routed slots by rank, then shared)
   float w[kMaxSlots];
   int ord[kMaxSlots]; // routed slots in ascending expert id
@@ -281,74 +281,92 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
 }
 
-// Scores, top-k and weights of one token from sl.lg (every thread of the block):
-//   sl.id[r], sl.w[r]  the expert and weight of rank r (descending selection key, ties
-//                      to the lower id), then the shared expert in slot k (weight 1)
-//   sl.ord[i]          the rank of the i-th selected expert in ascending id order
-// Scores and weights follow host/raon.py:1224-1247 (softmax / sigmoid, selection bias,
-// renormalisation by (sum + 1e-20), scaling).  The softmax denominator and the
-// renormalisation sum are wave tree sums (a fixed order; numpy's pairwise order differs
-// in the last bit at most, and the selection does not depend on either sum).
-// Wave 0 computes the scores and keys; then rank(i) = #{j : key_j > key_i, or
-// key_j == key_i and j < i} is counted for 16 keys per wave and pass (lane l: key
-// 16g + l%16 against quarter l/16 of the keys, the quarters added by shuffles); the
-// keys of rank < k write their slot; wave 0 then orders the slots by expert id and
-// renormalises.
-__device__ __forceinline__ void select_topk(const SelectParams a, const float* __restrict__ bias, SelectLds& sl) {
+// Top-k of one token from sl.lg, in two parts.
+//
+// select_rank (every thread of the block) finds the selected experts:
+//   sl.id[r]  the expert of rank r (descending selection key, ties to the lower id) for
+//             r < k, then the shared expert (id E) in slot k.
+// The key is the score (+ the selection bias) of host/raon.py:1224-1247.  With softmax
+// scores and no bias the key is the logit itself: softmax is increasing, so the order is
+// the same (ties, as everywhere, to the lower id), and the scores are needed only for
+// the weights.  Wave 0 computes the keys; then rank(i) = #{j : key_j > key_i, or key_j ==
+// key_i and j < i} is counted for 16 keys per wave and pass (lane l: key 16g + l%16
+// against quarter l/16 of the keys, the quarters added by shuffles), and the keys of rank
+// < k write their slot.
+//
+// select_finish (wave 0 only, any time before the weights are read; a later barrier
+// publishes them) computes
+//   sl.w[r]    the weight of slot r: the score, renormalised by (sum + 1e-20) and scaled;
+//              1 for the shared slot
+//   sl.ord[i]  the rank of the i-th selected expert in ascending id order.
+// The softmax denominator and the renormalisation sum are wave tree sums (a fixed order;
+// numpy's pairwise order differs in the last bit at most, and the selection depends on
+// neither).
+//
+// Keys sit in LDS in quarters of 32 (E <= 128) or 64 keys with 16 bytes between
+// quarters, so the four quarter reads of one instruction fall in different banks.
+__device__ __forceinline__ int key_pos(int e, int qkeys) { return e + 2 * (e / qkeys); }
+
+__device__ __forceinline__ bool select_fast(const SelectParams a, const float* bias) {
+  return a.score == 1 && bias == nullptr;
+}
+
+__device__ __forceinline__ void select_rank(const SelectParams a, const float* __restrict__ bias, SelectLds& sl) {
   constexpr int NC = kMaxE / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int E = a.E, K = a.k;
-  const int nc = (E + 63) >> 6;  // 64-key chunks; keys in [E, 64*nc) are 0
+  const int nc = (E + 63) >> 6;     // 64-key chunks; keys in [E, 64*nc) are 0
+  const int ncp = nc <= 2 ? 2 : 4;  // the rank pass reads 128 or 256 keys
+  const int qkeys = 16 * ncp;       // keys per quarter
   if (wave == 0) {
     float sc[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) sc[c] = c < nc && lane + 64 * c < E ? sl.lg[lane + 64 * c] : -__builtin_inff();
-    if (a.score == 0) {
+    if (!select_fast(a, bias)) {
+      if (a.score == 0) {
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
-        if (c < nc) sc[c] = 1.0f / (1.0f + expf(-sc[c]));
-    } else {
-      float m = sc[0];
+        for (int c = 0; c < NC; ++c)
+          if (c < nc) sc[c] = 1.0f / (1.0f + expf(-sc[c]));
+      } else {
+        float m = sc[0];
 #pragma unroll
-      for (int c = 1; c < NC; ++c) m = fmaxf(m, sc[c]);
-      m = wave_max_dpp(m);
-      float z = 0.f;
+        for (int c = 1; c < NC; ++c) m = fmaxf(m, sc[c]);
+        m = wave_max_dpp(m);
+        float z = 0.f;
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        if (c < nc) {
-          sc[c] = lane + 64 * c < E ? expf(sc[c] - m) : 0.f;
-          z += sc[c];
+        for (int c = 0; c < NC; ++c) {
+          if (c < nc) {
+            sc[c] = lane + 64 * c < E ? expf(sc[c] - m) : 0.f;
+            z += sc[c];
+          }
         }
-      }
-      z = wave_sum_dpp(z);
+        z = wave_sum_dpp(z);
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
-        if (c < nc) sc[c] = sc[c] / z;
+        for (int c = 0; c < NC; ++c)
+          if (c < nc) sc[c] = sc[c] / z;
+      }
     }
-    const int ncp = nc <= 2 ? 2 : 4;  // the rank pass reads 128 or 256 keys
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       if (c < ncp) {
         const int e = lane + 64 * c;
         // Padded entries (e >= E) sort below every real key and are never selected.
         const uint32_t k32 = e < E ? order_key(bias ? __fadd_rn(sc[c], bias[e]) : sc[c]) : 0u;
-        sl.key[e] = e < E ? ((uint64_t)k32 << 8) | (uint64_t)(255 - e) : 0ull;
-        sl.lg[e] = sc[c];
+        sl.key[key_pos(e, qkeys)] = e < E ? ((uint64_t)k32 << 8) | (uint64_t)(255 - e) : 0ull;
+        if (e < E) sl.lg[e] = sc[c];  // the scores (the logits on the fast path)
       }
     }
+    if (lane == 0 && a.S > K) sl.id[K] = E;  // shared expert
   }
   __syncthreads();
   {
-    // rank(i) = #{j : key_j > key_i}; the id in the low bits breaks ties toward the lower
-    // id.  Keys are counted over 128 (E <= 128) or 256 entries.  All of a lane's quarter
-    // is read before the compares (one LDS round trip).
     auto rank_pass = [&](auto QW) {
       constexpr int qw = decltype(QW)::value;  // uint4 words (2 keys each) per quarter
       const int q = lane >> 4;
-      const uint4* kq = reinterpret_cast<const uint4*>(sl.key) + q * qw;
+      const uint4* kq = reinterpret_cast<const uint4*>(sl.key) + q * (qw + 1);
       for (int g = wave; g < qw / 2; g += kWaves) {  // 8*qw keys = qw/2 groups of 16
         const int i = 16 * g + (lane & 15);
-        const uint64_t ki = sl.key[i];
+        const uint64_t ki = sl.key[key_pos(i, 2 * qw)];
         uint4 kv[qw];
 #pragma unroll
         for (int j2 = 0; j2 < qw; ++j2) kv[j2] = kq[j2];
@@ -362,36 +380,49 @@ __device__ __forceinline__ void select_topk(const SelectParams a, const float* _
         }
         cnt += __shfl_xor(cnt, 16, 64);
         cnt += __shfl_xor(cnt, 32, 64);
-        if (lane < 16 && i < E && cnt < K) {
-          sl.id[cnt] = i;
-          sl.w[cnt] = sl.lg[i];
-        }
+        if (lane < 16 && i < E && cnt < K) sl.id[cnt] = i;
       }
     };
     if (nc <= 2) rank_pass(std::integral_constant<int, 16>{});
     else rank_pass(std::integral_constant<int, 32>{});
   }
   __syncthreads();
-  if (wave == 0) {
-    // Slots past k hold a sentinel id while the selected ones are ordered by id (the
-    // shared expert's slot is written afterwards).
-    if (lane >= K && lane < kMaxSlots) sl.id[lane] = 0x7fffffff;
-    if (lane < K) {
-      const int id = sl.id[lane];
-      int pos = 0;
+}
+
+__device__ __forceinline__ void select_finish(const SelectParams a, const float* __restrict__ bias, SelectLds& sl) {
+  constexpr int NC = kMaxE / 64;
+  const int lane = threadIdx.x & 63;
+  const int E = a.E, K = a.k;
+  const int nc = (E + 63) >> 6;
+  float wr = 0.f;
+  if (select_fast(a, bias)) {
+    // Softmax of the logits: the same m (the largest logit, rank 0) and the same
+    // per-lane-then-wave order of the denominator as the score path.
+    const float m = sl.lg[sl.id[0]];
+    float z = 0.f;
 #pragma unroll
-      for (int r = 0; r < kMaxSlots; ++r) pos += sl.id[r] < id ? 1 : 0;
-      sl.ord[pos] = lane;
-    }
-    const float wr = lane < K ? sl.w[lane] : 0.f;
-    const float denom = a.renorm ? __fadd_rn(wave_sum_dpp(wr), 1e-20f) : 1.f;
-    if (lane < K) sl.w[lane] = __fmul_rn(a.renorm ? wr / denom : wr, a.scaling);
-    if (lane == 0 && a.S > K) {
-      sl.id[K] = a.E;  // shared expert
-      sl.w[K] = 1.f;
-    }
+    for (int c = 0; c < NC; ++c)
+      if (c < nc && lane + 64 * c < E) z += expf(sl.lg[lane + 64 * c] - m);
+    z = wave_sum_dpp(z);
+    if (lane < K) wr = expf(sl.lg[sl.id[lane]] - m) / z;
+  } else if (lane < K) {
+    wr = sl.lg[sl.id[lane]];
   }
-  __syncthreads();
+  // Slots past the routed ones, other than the shared slot, hold a sentinel id while the
+  // routed slots are ordered by id (the shared id E exceeds every routed id).
+  if (lane >= K && lane < kMaxSlots && !(lane == K && a.S > K)) sl.id[lane] = 0x7fffffff;
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  if (lane < K) {
+    const int id = sl.id[lane];
+    int pos = 0;
+#pragma unroll
+    for (int r = 0; r < kMaxSlots; ++r) pos += sl.id[r] < id ? 1 : 0;
+    sl.ord[pos] = lane;
+  }
+  const float denom = a.renorm ? __fadd_rn(wave_sum_dpp(wr), 1e-20f) : 1.f;
+  if (lane < K) sl.w[lane] = __fmul_rn(a.renorm ? wr / denom : wr, a.scaling);
+  if (lane == 0 && a.S > K) sl.w[K] = 1.f;
 }
 
 // Partial router logits of 64 rows (band b) of x for every expert:
@@ -529,10 +560,12 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
 #pragma unroll
       for (int i = 0; i < kMaxH / 4 / kThreads; ++i) {
         const int idx = tid + kThreads * i;
+        xv[i] = 0ull;
         if (2 * idx < Hp)
           xv[i] = l == 0 ? reinterpret_cast<const uint64_t*>(a.x0)[idx] : ld_hand_u64(xin + 2 * idx);
       }
-      // x_l into LDS first (the compiler keeps its loads in registers only briefly).
+      // x_l into LDS, and the group sums of x_l from the registers: the 32 values of a
+      // group are held by 8 neighbouring lanes (4 each), summed in a fixed tree.
 #pragma unroll
       for (int i = 0; i < kMaxH / 4 / kThreads; ++i) {
         const int idx = tid + kThreads * i;
@@ -540,8 +573,20 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
           xs[2 * idx] = (uint32_t)xv[i];
           xs[2 * idx + 1] = (uint32_t)(xv[i] >> 32);
         }
+        if (i * kThreads < Hp / 2) {  // uniform: H % 256 == 0 keeps groups of 8 lanes whole
+          const uint32_t lo = (uint32_t)xv[i], hi = (uint32_t)(xv[i] >> 32);
+          float sv = (bf16_to_f32(lo & 0xffffu) + bf16_to_f32(lo >> 16)) +
+                     (bf16_to_f32(hi & 0xffffu) + bf16_to_f32(hi >> 16));
+          sv += dpp_f32<0xB1>(sv);  // lane ^ 1
+          sv += dpp_f32<0x4E>(sv);  // lane ^ 2
+          sv += __shfl_xor(sv, 4, 64);
+          if ((idx & 7) == 0 && 2 * idx < Hp) xsum[idx >> 3] = sv;
+        }
       }
       const int nbc = kLRow / a.Ep;  // bands per chunk
+      // P threads per expert (neighbouring lanes) sum every P-th band; then a fixed tree.
+      const int P = a.E <= 128 ? 4 : 2;
+      const int pe = tid / P, pp = tid % P;
       float lacc = 0.f;
       for (int b0 = 0; b0 < a.nb2; b0 += nbc) {
         const int nf4 = (min(nbc, a.nb2 - b0) * a.Ep) / 4;
@@ -555,39 +600,19 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
         if (h0) dst[tid] = v0;
         if (h1) dst[tid + kThreads] = v1;
         __syncthreads();
-        if (tid < a.E) {
-          // In band order; eight LDS reads in flight at a time.
+        if (pe < a.E) {
           const int nb = min(nbc, a.nb2 - b0);
-          int b = 0;
-          for (; b + 8 <= nb; b += 8) {
-            float v[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = lrow[(b + i) * a.Ep + tid];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) lacc += v[i];
-          }
-          for (; b < nb; ++b) lacc += lrow[b * a.Ep + tid];
+          for (int b = pp; b < nb; b += P) lacc += lrow[b * a.Ep + pe];
         }
         __syncthreads();
       }
-      if (tid < a.E) sl.lg[tid] = lacc;
-    }
-    for (int gi = tid; gi < a.H / 32; gi += kThreads) {
-      float sum = 0.f;
-#pragma unroll
-      for (int c = 0; c < 16; ++c) {
-        const uint32_t v = xs[gi * 16 + c];
-        sum += bf16_to_f32(v & 0xffffu);
-        sum += bf16_to_f32(v >> 16);
-      }
-      xsum[gi] = sum;
+      lacc += dpp_f32<0xB1>(lacc);
+      if (P == 4) lacc += dpp_f32<0x4E>(lacc);
+      if (pe < a.E && pp == 0) sl.lg[pe] = lacc;
     }
     __syncthreads();
-    select_topk(SelectParams{a.E, a.k, a.S, a.score, a.renorm, a.scaling}, a.rb[l], sl);
-    if (g == 0 && tid < a.k) {
-      if (a.ids_out) a.ids_out[(size_t)l * a.k + tid] = sl.id[tid];
-      if (a.wts_out) a.wts_out[(size_t)l * a.k + tid] = sl.w[tid];
-    }
+    const SelectParams sp{a.E, a.k, a.S, a.score, a.renorm, a.scaling};
+    select_rank(sp, a.rb[l], sl);
 
     // ---- issue every weight load of this workgroup's units for this layer.
     const uint8_t* gu_l = a.gu[l];
@@ -633,6 +658,16 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     for (int d = 0; d < kMaxDnUnits; ++d)
       load_router_slice<NIT>(a, a.rw[l + 1 < a.L ? l + 1 : l], dn_d[d][1], dn_d[d][0] >= 0 && l + 1 < a.L, dummy,
                              rwv[d]);
+
+    // ---- slot weights and id order (read by the combine, after later barriers), while
+    // the weight loads are in flight.
+    if (wave == 0) {
+      select_finish(sp, a.rb[l], sl);
+      if (g == 0 && tid < a.k) {
+        if (a.ids_out) a.ids_out[(size_t)l * a.k + tid] = sl.id[tid];
+        if (a.wts_out) a.wts_out[(size_t)l * a.k + tid] = sl.w[tid];
+      }
+    }
 
     // ---- GU units: the first one from the registers loaded above (kept out of the loop so
     // the compiler's wait for its tiles does not also cover the DN loads), then any
