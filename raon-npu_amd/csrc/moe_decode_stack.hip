@@ -129,7 +129,8 @@ __device__ __forceinline__ float tile_dot(const TileRegs& r, const uint32_t* xw,
   return acc;
 }
 
-// Counters of layer l: [0] ready, [1, 1+S) slot, [1+S, 1+S+nb2) band, then pair[S*nb1].
+// Counters of layer l: kReadyCopies copies of ready, kSlotCopies copies of each of the S
+// slot counters, then the nb2 band counters.
 // Every counter sits on its own 256-byte line: atomics and polls on one line are served
 // one at a time at the memory side, and a layer's counters see hundreds of them.
 constexpr int kCntPad = 64;  // uint32 per counter line
@@ -139,6 +140,9 @@ __device__ __forceinline__ unsigned* cnt_at(const StackArgs& a, int l, int i) {
 // `ready` of a layer is kept in kReadyCopies copies: a band publishes to every copy and
 // workgroup g polls copy g % kReadyCopies, so 32 rather than 256 workgroups poll a line.
 constexpr int kReadyCopies = 8;
+// Each slot counter likewise has kSlotCopies copies: a GU unit arrives on all of them and
+// DN workgroup g polls copy g % kSlotCopies (about 32 DN units wait on one slot).
+constexpr int kSlotCopies = 4;
 __device__ __forceinline__ void publish_ready(const StackArgs& a, int l) {
   for (int c = 0; c < kReadyCopies; ++c)
     __hip_atomic_fetch_add(cnt_at(a, l, c), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -539,8 +543,8 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
 
   for (int l = 0; l < a.L; ++l) {
     unsigned* c_ready = cnt_at(a, l, g % kReadyCopies);
-    auto c_slot = [&](int s) { return cnt_at(a, l, kReadyCopies + s); };
-    auto c_band = [&](int b) { return cnt_at(a, l, kReadyCopies + a.S + b); };
+    auto c_slot = [&](int s, int copy) { return cnt_at(a, l, kReadyCopies + s * kSlotCopies + copy); };
+    auto c_band = [&](int b) { return cnt_at(a, l, kReadyCopies + a.S * kSlotCopies + b); };
     uint8_t* lay = a.scratch + (size_t)l * a.layer_bytes;
     const uint32_t* xin = reinterpret_cast<const uint32_t*>(lay);
     const float* lpart = reinterpret_cast<const float*>(lay + a.off_lpart);
@@ -692,7 +696,11 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
         }
         st_dev(&gp[lane], sg);
         st_dev(&gp[64 + lane], su);
-        wave_arrive(c_slot(s), false);
+        // One arrival on every copy of the slot counter (posted, after the stores).
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_s_waitcnt(0);
+        if (lane < kSlotCopies)
+          __hip_atomic_fetch_add(c_slot(s, lane), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     };
     if (gu_d[0] >= 0) {
@@ -716,8 +724,8 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     // ---- DN units, both of a workgroup at once, and the combine of a band by the last
     // slot to finish it.
     if (n_dn_t > 0) {
-      if (!wait_geq(a, c_slot(dn_d[0][0]), gu_parts, &flag)) return;
-      if (dn_d[1][0] >= 0 && !wait_geq(a, c_slot(dn_d[1][0]), gu_parts, &flag)) return;
+      if (!wait_geq(a, c_slot(dn_d[0][0], g % kSlotCopies), gu_parts, &flag)) return;
+      if (dn_d[1][0] >= 0 && !wait_geq(a, c_slot(dn_d[1][0], g % kSlotCopies), gu_parts, &flag)) return;
       if (wave > 0) {
         // h for columns 128kt + 2*lane (+1) of each of this wave's tiles: the GU partials
         // of both columns for every K part (64-bit loads, all issued before the sums),
@@ -757,9 +765,13 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
               h1 = bf16_round(act_apply(a.act, bf16_round(g1), bf16_round(u1), a.gb, a.vb));
             }
             hs[wave][p][lane] = f32_to_bf16(h0) | (f32_to_bf16(h1) << 16);
+            // Sum over the 16 lanes of a row (32 columns, one group) on DPP: quad swaps,
+            // then the half-row and row mirrors.
             float gs = h0 + h1;
-#pragma unroll
-            for (int off = 8; off > 0; off >>= 1) gs += __shfl_xor(gs, off, 16);
+            gs += dpp_f32<0xB1>(gs);
+            gs += dpp_f32<0x4E>(gs);
+            gs += dpp_f32<0x141>(gs);
+            gs += dpp_f32<0x140>(gs);
             if ((lane & 15) == 0) hsum[wave][p][lane >> 4] = gs;
           }
         }
@@ -908,7 +920,7 @@ StackShape stack_shape(const RmoeLayer& L) {
   sh.off_dout = off;
   off += al256((size_t)sh.S * L.H * 4);
   sh.layer_bytes = off;
-  sh.cnt_stride = kReadyCopies + sh.S + sh.nb2;
+  sh.cnt_stride = kReadyCopies + sh.S * kSlotCopies + sh.nb2;
   return sh;
 }
 
