@@ -12,23 +12,23 @@
 //
 // One workgroup per CU stays resident for the whole stack.  The work of a layer is cut
 // into units that are the same for every layer:
-//   GU unit (slot s, band pair j, K part q): gate rows 64j..64j+63 and the matching up
-//     rows over K tiles [kb(q), ke(q)); wave w streams the two tiles at K tile kb + w and
-//     the workgroup writes the fp32 partial sums of the 128 rows.
+//   GU unit (slot s, half band hb): the 32 gate rows 32hb..32hb+31 and the matching 32 up
+//     rows over all of K (lanes 0..31 of each wave read gate rows, lanes 32..63 up rows;
+//     wave w streams K tiles w, w + 8, ...).  The workgroup sums its waves, applies the
+//     activation and publishes h of its 32 columns.
 //   DN unit (slot s, output band b of 64 rows): all K tiles of the band; waves 1..7
-//     stream them.  A DN wave reads the GU partials of its 128 columns of h, sums the
-//     parts in q order and applies the activation itself.
-// Workgroups hand results to each other through device-scope counters (per layer):
-//   slot[s]   every GU part of slot s is written                   -> DN units of s
-//   band[b]   every slot has written d of band b; the last one to arrive combines the
-//             band, writes x_{l+1}[band] and the band's share of the router logits of
-//             layer l+1                                              -> ready[l+1]
-//   ready     all bands of x_l and of its partial router logits are written
+//     stream them, each with the h of its 128 columns.
+// Hand-offs between workgroups (per layer):
+//   h         tagged words (below): DN waves poll the words of their own columns
+//   band[b]   counter: every slot has written d of band b; the last one to arrive
+//             combines the band, writes x_{l+1}[band] and the band's share of the router
+//             logits of layer l+1                                   -> ready[l+1]
+//   ready     counter: all bands of x_l and of its partial router logits are written
 // Every workgroup computes the top-k of a layer itself from the partial logits (the
 // same reads in the same order give the same routing everywhere), and loads the weight
-// tiles of all its units into registers as soon as the routing is known, before it
-// waits for anything else in that layer: the HBM stream of a layer is issued at once.
-// Results do not depend on the arrival order: every sum over parts, bands or slots is
+// tiles of all its units as soon as the routing is known, before it waits for anything
+// else in that layer: the HBM stream of a layer is issued at once.
+// Results do not depend on the arrival order: every sum over waves, bands or slots is
 // taken in a fixed order.
 #include "rmoe_internal.h"
 
@@ -44,7 +44,6 @@ constexpr int kMaxE = 256;
 constexpr int kMaxSlots = 17;
 constexpr int kMaxDnPos = 4;      // DN tiles per DN wave (waves 1..7, both units): Ipad <= 1792
 constexpr int kMaxDnUnits = 2;    // DN units per workgroup and layer (prefetched)
-constexpr int kMaxQ = 4;          // GU K parts: H <= 4096
 constexpr int kLRow = 4096;       // floats of partial logits staged in LDS at a time
 constexpr unsigned kSpinLimit = 1u << 21;
 
@@ -52,14 +51,14 @@ struct StackArgs {
   int L, H, I, Ipad, E, k, S, score, renorm, act, residual;
   float scaling, gb, vb;
   size_t gu_bytes, dn_bytes;
-  int nb1, nb2, nkt1, nkt2, nq1, n_gu, n_dn;
+  int nb1, nb2, nkt1, nkt2, nhb, n_gu, n_dn;
   int Ep;  // n_routed rounded up to 32: row stride of the partial router logits
   const uint16_t* x0;
   uint16_t* out;
   int32_t* ids_out;  // [L, k] or null
   float* wts_out;    // [L, k] or null
   uint8_t* scratch;  // per layer: layer_bytes
-  size_t layer_bytes, off_lpart, off_gpart, off_dout;
+  size_t layer_bytes, off_lpart, off_h, off_dout;
   unsigned* cnt;     // per layer cnt_stride counters, then exit, abort
   int cnt_stride;
   int* err;
@@ -86,6 +85,16 @@ __device__ __forceinline__ void load_tile(TileRegs& r, const uint8_t* tile, int 
 __device__ __forceinline__ void load_tile_or(TileRegs& r, bool valid, const uint8_t* tile, const uint8_t* dummy,
                                              int lane) {
   const uint8_t* base = valid ? tile + lane * 16 : dummy;
+  const int step = valid ? 1024 : 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r.c[j] = load_stream16(base + j * step);
+  r.sm = load_stream16(base + 4 * step);
+}
+
+// Five 16-byte pieces at p + 1 KB * j (a lane's share of one tile), or five loads of
+// `dummy` when not valid (the same load count on every path).
+__device__ __forceinline__ void load_rows(TileRegs& r, bool valid, const uint8_t* p, const uint8_t* dummy) {
+  const uint8_t* base = valid ? p : dummy;
   const int step = valid ? 1024 : 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) r.c[j] = load_stream16(base + j * step);
@@ -129,26 +138,38 @@ __device__ __forceinline__ float tile_dot(const TileRegs& r, const uint32_t* xw,
   return acc;
 }
 
-// Counters of layer l: kReadyCopies copies of ready, kSlotCopies copies of each of the S
-// slot counters, then the nb2 band counters.
+// Counters of layer l: kReadyCopies copies of ready, then the nb2 band counters.
 // Every counter sits on its own 256-byte line: atomics and polls on one line are served
 // one at a time at the memory side, and a layer's counters see hundreds of them.
 constexpr int kCntPad = 64;  // uint32 per counter line
+// Line 0 of the counter area holds the launch counter (at a fixed place: launches of
+// different depths share the area); the counters of layer l follow from line 1.
 __device__ __forceinline__ unsigned* cnt_at(const StackArgs& a, int l, int i) {
-  return a.cnt + ((size_t)l * a.cnt_stride + i) * kCntPad;
+  return a.cnt + (1 + (size_t)l * a.cnt_stride + i) * kCntPad;
 }
 // `ready` of a layer is kept in kReadyCopies copies: a band publishes to every copy and
 // workgroup g polls copy g % kReadyCopies, so 32 rather than 256 workgroups poll a line.
 constexpr int kReadyCopies = 8;
-// Each slot counter likewise has kSlotCopies copies: a GU unit arrives on all of them and
-// DN workgroup g polls copy g % kSlotCopies (about 32 DN units wait on one slot).
-constexpr int kSlotCopies = 4;
 __device__ __forceinline__ void publish_ready(const StackArgs& a, int l) {
   for (int c = 0; c < kReadyCopies; ++c)
     __hip_atomic_fetch_add(cnt_at(a, l, c), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ unsigned* exit_cnt(const StackArgs& a) { return cnt_at(a, a.L, 0); }
 __device__ __forceinline__ unsigned* abort_flag(const StackArgs& a) { return cnt_at(a, a.L, 1); }
+// Launch counter: read by every workgroup at the start, advanced by the last one out.
+__device__ __forceinline__ unsigned* epoch_cnt(const StackArgs& a) { return a.cnt; }
+
+// Tagged hand-off words: 32 bits of data and the launch's tag (2 * epoch + 1: odd, so
+// never the zero of fresh memory) in one 64-bit device-scope store; a reader polls each
+// word until it carries this launch's tag.  A 64-bit access is single-copy atomic, so a
+// word with the right tag holds this launch's data, and no counter or store
+// acknowledgement is needed.  Each word is written once per launch (a region per layer).
+__device__ __forceinline__ void st_dev_u64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_dev_u64(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Hand-off protocol.  Data handed to other workgroups is stored with device-scope
 // stores (st_dev); the storing wave waits until its stores are acknowledged
@@ -169,24 +190,6 @@ __device__ __forceinline__ unsigned* abort_flag(const StackArgs& a) { return cnt
 // on its own workgroup's store holds exactly what was stored.
 __device__ __forceinline__ uint64_t ld_hand_u64(const void* p) { return *reinterpret_cast<const uint64_t*>(p); }
 __device__ __forceinline__ float ld_hand_f32(const float* p) { return *p; }
-
-// One wave, after its device-scope stores: count one arrival.  With `ret` the previous
-// count is returned (in every lane) -- one more round trip; without it the add is
-// posted and the wave moves on.
-__device__ __forceinline__ unsigned wave_arrive(unsigned* counter, bool ret) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_s_waitcnt(0);
-  unsigned prev = 0u;
-  if ((threadIdx.x & 63) == 0) {
-    if (ret)
-      prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else
-      __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  prev = __builtin_amdgcn_readfirstlane(prev);
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  return prev;
-}
 
 // Block-wide: every wave waits for its own stores, then thread 0 counts one arrival.
 // Returns true in every thread for the n-th arrival.
@@ -474,7 +477,7 @@ __device__ __forceinline__ void load_router_slice(const StackArgs& a, const uint
 
 // DNPOS: DN tiles per DN wave (waves 1..7 stream the tiles of both DN units:
 // 2 * Ipad/128 <= 7 * DNPOS); NIT: router items per thread (n_routed <= 128 * NIT);
-// QM: GU K parts (nq1 <= QM).  They size register and LDS arrays, so they are template
+// They size register and LDS arrays, so they are template
 // parameters.
 //
 // Wave roles: every wave streams GU tiles; waves 1..7 stream the DN tiles; wave 0 does
@@ -483,7 +486,7 @@ __device__ __forceinline__ void load_router_slice(const StackArgs& a, const uint
 // target read `dummy` instead of being skipped: every wave issues the same number of
 // loads on every path, which keeps the compiler's s_waitcnt counts exact (a GU tile is
 // consumed without waiting for the DN tiles issued after it).
-template <int DNPOS, int NIT, int QM>
+template <int DNPOS, int NIT>
 __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t xs[kMaxH / 2];  // x_l as bf16 pairs
   __shared__ float xsum[kMaxH / 32];                              // group sums of x_l
@@ -499,10 +502,11 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t dn_lds[];
   uint8_t* dn_sink = dn_lds + (size_t)kMaxDnUnits * a.nkt2 * kTileBytes;
 
-  // This workgroup's first GU unit (slot, band pair, K tiles [kb, ke), part q) and its DN
-  // units (slot, band; -1 when absent).  The same in every layer; kept in LDS so that
-  // the index arithmetic does not hold registers across the layer loop.
-  __shared__ int gu_d[5], dn_d[kMaxDnUnits][2];
+  // This workgroup's first GU unit (slot, half band) and its DN units (slot, band; -1
+  // when absent).  The same in every layer; kept in LDS so that the index arithmetic does
+  // not hold registers across the layer loop.  epoch_s: this launch's epoch.
+  __shared__ int gu_d[2], dn_d[kMaxDnUnits][2];
+  __shared__ uint32_t epoch_s;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = blockIdx.x, G = gridDim.x;
@@ -510,16 +514,12 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
   if (tid == 0) {
     const int u = g;
     if (u < a.n_gu) {
-      const int s = u / (a.nb1 * a.nq1), rem = u % (a.nb1 * a.nq1);
-      const int q = rem % a.nq1;
-      gu_d[0] = s;
-      gu_d[1] = rem / a.nq1;
-      gu_d[2] = q * a.nkt1 / a.nq1;
-      gu_d[3] = (q + 1) * a.nkt1 / a.nq1;
-      gu_d[4] = q;
+      gu_d[0] = u / a.nhb;
+      gu_d[1] = u % a.nhb;
     } else {
       gu_d[0] = -1;
     }
+    epoch_s = ld_dev_u32(epoch_cnt(a));
     const int v0 = ((g - a.n_gu) % G + G) % G;  // first DN unit of this workgroup
     for (int d = 0; d < kMaxDnUnits; ++d) {
       const int v = v0 + d * G;
@@ -529,7 +529,8 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
   }
   __syncthreads();
   const uint8_t* dummy = reinterpret_cast<const uint8_t*>(a.x0);
-  const unsigned gu_parts = (unsigned)(a.nb1 * a.nq1);
+  const uint32_t epoch = epoch_s;
+  const uint32_t tag = 2u * epoch + 1u;
 
   // Layer 0: the band share of the router logits of x0 (workgroups b < nb2).
   if (g < a.nb2) {
@@ -543,12 +544,12 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
 
   for (int l = 0; l < a.L; ++l) {
     unsigned* c_ready = cnt_at(a, l, g % kReadyCopies);
-    auto c_slot = [&](int s, int copy) { return cnt_at(a, l, kReadyCopies + s * kSlotCopies + copy); };
-    auto c_band = [&](int b) { return cnt_at(a, l, kReadyCopies + a.S * kSlotCopies + b); };
+    auto c_band = [&](int b) { return cnt_at(a, l, kReadyCopies + b); };
     uint8_t* lay = a.scratch + (size_t)l * a.layer_bytes;
     const uint32_t* xin = reinterpret_cast<const uint32_t*>(lay);
     const float* lpart = reinterpret_cast<const float*>(lay + a.off_lpart);
-    float* gpart = reinterpret_cast<float*>(lay + a.off_gpart);
+    uint64_t* hbuf = reinterpret_cast<uint64_t*>(lay + a.off_h);  // [S][Ipad/2] tagged h pairs
+    const int hstride = a.Ipad / 2;
     float* dout = reinterpret_cast<float*>(lay + a.off_dout);
 
     if (!wait_geq(a, c_ready, (unsigned)a.nb2, &flag)) return;
@@ -619,26 +620,23 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     select_rank(sp, a.rb[l], sl);
 
     // ---- issue every weight load of this workgroup's units for this layer.
+    // A GU unit (slot s, half band hb) is the 32 gate rows 32hb.. and the 32 matching up
+    // rows over all of K: lanes 0..31 of a wave read gate rows, lanes 32..63 the up rows
+    // (each lane its own row of the tile), so one tile_dot covers both.  Wave w takes K
+    // tiles w, w + 8, ...; the first two are loaded here.
     const uint8_t* gu_l = a.gu[l];
     const uint8_t* dn_l = a.dn[l];
-    TileRegs gt, ut;
+    auto gu_row = [&](int s, int hb, int kt) {
+      const uint8_t* W = gu_l + (size_t)sl.id[s] * a.gu_bytes;
+      const size_t band = lane < 32 ? (size_t)(hb >> 1) : (size_t)(a.nb1 + (hb >> 1));
+      return W + (band * a.nkt1 + kt) * kTileBytes + (size_t)(32 * (hb & 1) + (lane & 31)) * 16;
+    };
+    TileRegs mt0, mt1;
     {
-      const uint8_t* pg = dummy;
-      const uint8_t* pu = dummy;
-      bool ok = false;
       const int s = gu_d[0];
-      if (s >= 0) {
-        const int j = gu_d[1], kb = gu_d[2], ke = gu_d[3];
-        const int kt = kb + wave;
-        if (kt < ke) {
-          const uint8_t* W = gu_l + (size_t)sl.id[s] * a.gu_bytes;
-          pg = W + ((size_t)j * a.nkt1 + kt) * kTileBytes;
-          pu = W + ((size_t)(a.nb1 + j) * a.nkt1 + kt) * kTileBytes;
-          ok = true;
-        }
-      }
-      load_tile_or(gt, ok, pg, dummy, lane);
-      load_tile_or(ut, ok, pu, dummy, lane);
+      const bool ok0 = s >= 0 && wave < a.nkt1, ok1 = s >= 0 && wave + kWaves < a.nkt1;
+      load_rows(mt0, ok0, ok0 ? gu_row(s, gu_d[1], wave) : dummy, dummy);
+      load_rows(mt1, ok1, ok1 ? gu_row(s, gu_d[1], wave + kWaves) : dummy, dummy);
     }
     // DN tiles of both units, flattened as t = d * nkt2 + kt: wave 1 + t % 7 copies tile t
     // into LDS slot t at its position t / 7.  A workgroup with a GU unit issues them
@@ -673,98 +671,101 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
       }
     }
 
-    // ---- GU units: the first one from the registers loaded above (kept out of the loop so
-    // the compiler's wait for its tiles does not also cover the DN loads), then any
-    // further ones (more units than workgroups) loaded on the spot.
-    auto gu_unit = [&](int s, int j, int kb, int ke, int q) {
-      const int kt = kb + wave;
-      float ag = 0.f, au = 0.f;
-      if (kt < ke) {
-        ag = tile_dot(gt, xs + kt * 64, xsum + kt * 4, 0.f);
-        au = tile_dot(ut, xs + kt * 64, xsum + kt * 4, 0.f);
+    // ---- GU units: g and u of the unit's rows over all of K (waves summed in order), then
+    // h = RTNE(act(RTNE(g), RTNE(u))) of its 32 columns, published as 16 tagged words of
+    // bf16 pairs.  The first unit uses the tiles loaded above (kept out of the loop so the
+    // compiler's wait for them does not also cover the DN loads); any further ones (more
+    // units than workgroups) load on the spot.
+    auto gu_unit = [&](int s, int hb) {
+      float acc = 0.f;
+      if (wave < a.nkt1) acc = tile_dot(mt0, xs + wave * 64, xsum + wave * 4, acc);
+      if (wave + kWaves < a.nkt1) acc = tile_dot(mt1, xs + (wave + kWaves) * 64, xsum + (wave + kWaves) * 4, acc);
+      for (int kt = wave + 2 * kWaves; kt < a.nkt1; kt += kWaves) {
+        TileRegs r;
+        load_rows(r, true, gu_row(s, hb, kt), dummy);
+        acc = tile_dot(r, xs + kt * 64, xsum + kt * 4, acc);
       }
-      red[wave][0][lane] = ag;
-      red[wave][1][lane] = au;
+      red[wave][0][lane] = acc;
       __syncthreads();
       if (wave == 0) {
-        float* gp = gpart + ((size_t)(s * a.nb1 + j) * a.nq1 + q) * 128;
-        float sg = 0.f, su = 0.f;
+        float gs = 0.f, us = 0.f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
-          sg += red[w][0][lane];
-          su += red[w][1][lane];
+          gs += red[w][0][lane & 31];
+          us += red[w][0][32 + (lane & 31)];
         }
-        st_dev(&gp[lane], sg);
-        st_dev(&gp[64 + lane], su);
-        // One arrival on every copy of the slot counter (posted, after the stores).
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_s_waitcnt(0);
-        if (lane < kSlotCopies)
-          __hip_atomic_fetch_add(c_slot(s, lane), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t hb16 = f32_to_bf16(act_apply(a.act, bf16_round(gs), bf16_round(us), a.gb, a.vb));
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hb16, 0xB1, 0xF, 0xF, false);  // lane ^ 1
+        if (lane < 32 && (lane & 1) == 0)
+          st_dev_u64(&hbuf[(size_t)s * hstride + 16 * hb + (lane >> 1)],
+                     (uint64_t)(hb16 | (hi << 16)) | ((uint64_t)tag << 32));
       }
     };
     if (gu_d[0] >= 0) {
-      gu_unit(gu_d[0], gu_d[1], gu_d[2], gu_d[3], gu_d[4]);
+      gu_unit(gu_d[0], gu_d[1]);
       issue_dn();
     }
     for (int u = g + G; u < a.n_gu; u += G) {
-      const int s = u / (a.nb1 * a.nq1), rem = u % (a.nb1 * a.nq1);
-      const int j = rem / a.nq1, q = rem % a.nq1;
-      const int kb = q * a.nkt1 / a.nq1, ke = (q + 1) * a.nkt1 / a.nq1;
-      const int kt = kb + wave;
+      const int s = u / a.nhb, hb = u % a.nhb;
       __syncthreads();  // red[] of the previous unit has been read
-      if (kt < ke) {
-        const uint8_t* W = gu_l + (size_t)sl.id[s] * a.gu_bytes;
-        load_tile(gt, W + ((size_t)j * a.nkt1 + kt) * kTileBytes, lane);
-        load_tile(ut, W + ((size_t)(a.nb1 + j) * a.nkt1 + kt) * kTileBytes, lane);
-      }
-      gu_unit(s, j, kb, ke, q);
+      load_rows(mt0, wave < a.nkt1, wave < a.nkt1 ? gu_row(s, hb, wave) : dummy, dummy);
+      load_rows(mt1, wave + kWaves < a.nkt1, wave + kWaves < a.nkt1 ? gu_row(s, hb, wave + kWaves) : dummy, dummy);
+      gu_unit(s, hb);
     }
 
     // ---- DN units, both of a workgroup at once, and the combine of a band by the last
     // slot to finish it.
     if (n_dn_t > 0) {
-      if (!wait_geq(a, c_slot(dn_d[0][0], g % kSlotCopies), gu_parts, &flag)) return;
-      if (dn_d[1][0] >= 0 && !wait_geq(a, c_slot(dn_d[1][0], g % kSlotCopies), gu_parts, &flag)) return;
+      // h of each of this wave's DN tiles: lane covers columns 128kt + 2*lane (+1), one
+      // tagged word per tile, polled until it carries this launch's tag (columns past I
+      // are zero).  Bounded: past kSpinLimit polls, or when another workgroup gave up,
+      // the stack is abandoned after the whole workgroup has agreed to stop.
+      bool failed = false;
       if (wave > 0) {
-        // h for columns 128kt + 2*lane (+1) of each of this wave's tiles: the GU partials
-        // of both columns for every K part (64-bit loads, all issued before the sums),
-        // summed in part order.
-        uint64_t gq[DNPOS][QM], uq[DNPOS][QM];
+        uint64_t hv[DNPOS];
+        const uint64_t* hp[DNPOS];
+        unsigned need = 0u;
 #pragma unroll
         for (int p = 0; p < DNPOS; ++p) {
           const int t = wave - 1 + (kWaves - 1) * p;
-          const int d = t < n_dn_t ? t / a.nkt2 : 0, kt = t < n_dn_t ? t % a.nkt2 : 0;
-          const int c0 = 128 * kt + 2 * lane;
-          const bool ok = t < n_dn_t && c0 < a.I;
-          const float* gp = gpart + ((size_t)(dn_d[d][0] * a.nb1 + (ok ? c0 >> 6 : 0)) * a.nq1) * 128 + (c0 & 63);
+          const int d = t < n_dn_t ? t / a.nkt2 : 0;
+          const int c0 = 128 * (t < n_dn_t ? t % a.nkt2 : 0) + 2 * lane;
+          hv[p] = 0ull;
+          hp[p] = hbuf + (size_t)(dn_d[d][0] < 0 ? 0 : dn_d[d][0]) * hstride + (c0 >> 1);
+          if (t < n_dn_t && c0 < a.I) need |= 1u << p;
+        }
+        unsigned it = 0;
+        while (__any(need != 0u)) {
 #pragma unroll
-          for (int q = 0; q < QM; ++q)
-            if (ok && q < a.nq1) {
-              gq[p][q] = ld_hand_u64(gp + q * 128);
-              uq[p][q] = ld_hand_u64(gp + q * 128 + 64);
+          for (int p = 0; p < DNPOS; ++p) {
+            if (need & (1u << p)) {
+              hv[p] = ld_dev_u64(hp[p]);
+              if ((uint32_t)(hv[p] >> 32) == tag) need &= ~(1u << p);
             }
+          }
+          if (!__any(need != 0u)) break;
+          ++it;
+          if ((it & 63u) == 0u && ld_dev_u32(abort_flag(a)) != 0u) {
+            failed = true;
+            break;
+          }
+          if (it > kSpinLimit) {
+            if (lane == 0) {
+              st_dev_u32(abort_flag(a), 1u);
+              __hip_atomic_fetch_or(a.err, 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            failed = true;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
         }
 #pragma unroll
         for (int p = 0; p < DNPOS; ++p) {
           const int t = wave - 1 + (kWaves - 1) * p;
           if (t < n_dn_t) {
-            const int c0 = 128 * (t % a.nkt2) + 2 * lane;
-            float h0 = 0.f, h1 = 0.f;
-            if (c0 < a.I) {
-              float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
-#pragma unroll
-              for (int q = 0; q < QM; ++q)
-                if (q < a.nq1) {
-                  g0 += __uint_as_float((uint32_t)gq[p][q]);
-                  g1 += __uint_as_float((uint32_t)(gq[p][q] >> 32));
-                  u0 += __uint_as_float((uint32_t)uq[p][q]);
-                  u1 += __uint_as_float((uint32_t)(uq[p][q] >> 32));
-                }
-              h0 = bf16_round(act_apply(a.act, bf16_round(g0), bf16_round(u0), a.gb, a.vb));
-              h1 = bf16_round(act_apply(a.act, bf16_round(g1), bf16_round(u1), a.gb, a.vb));
-            }
-            hs[wave][p][lane] = f32_to_bf16(h0) | (f32_to_bf16(h1) << 16);
+            const uint32_t hw = (uint32_t)hv[p];  // zero for columns past I
+            const float h0 = bf16_to_f32(hw & 0xffffu), h1 = bf16_to_f32(hw >> 16);
+            hs[wave][p][lane] = hw;
             // Sum over the 16 lanes of a row (32 columns, one group) on DPP: quad swaps,
             // then the half-row and row mirrors.
             float gs = h0 + h1;
@@ -776,6 +777,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
           }
         }
       }
+      if (__syncthreads_or(failed ? 1 : 0)) return;
       // This wave's DN tiles were copied into LDS by its own loads: drain them.
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
@@ -881,17 +883,18 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
   // itself out; the last workgroup out clears every counter for the next launch.
   if (block_arrive(exit_cnt(a), (unsigned)G, &flag)) {
     const int n = a.L * a.cnt_stride;
-    for (int i = tid; i < n; i += kThreads) st_dev_u32(a.cnt + (size_t)i * kCntPad, 0u);
+    for (int i = tid; i < n; i += kThreads) st_dev_u32(a.cnt + (1 + (size_t)i) * kCntPad, 0u);
     if (tid == 0) {
       st_dev_u32(abort_flag(a), 0u);
       st_dev_u32(exit_cnt(a), 0u);
+      st_dev_u32(epoch_cnt(a), (epoch + 1u) & 0x7fffffffu);
     }
   }
 }
 
 struct StackShape {
-  int S, nb1, nb2, nkt1, nkt2, nq1, n_gu, n_dn;
-  size_t off_lpart, off_gpart, off_dout, layer_bytes;
+  int S, nb1, nb2, nkt1, nkt2, nhb, n_gu, n_dn;
+  size_t off_lpart, off_h, off_dout, layer_bytes;
   int cnt_stride;
 };
 
@@ -909,18 +912,18 @@ StackShape stack_shape(const RmoeLayer& L) {
   sh.nb2 = L.H / 64;
   sh.nkt1 = L.H / kTileCols;
   sh.nkt2 = L.Ipad / kTileCols;
-  sh.nq1 = (sh.nkt1 + kWaves - 1) / kWaves;
-  sh.n_gu = sh.S * sh.nb1 * sh.nq1;
+  sh.nhb = L.I / 32;
+  sh.n_gu = sh.S * sh.nhb;
   sh.n_dn = sh.S * sh.nb2;
   size_t off = al256((size_t)L.H * 2);  // x_l (bf16)
   sh.off_lpart = off;
   off += al256((size_t)sh.nb2 * ((L.n_routed + 31) / 32 * 32) * 4);
-  sh.off_gpart = off;
-  off += al256((size_t)sh.S * sh.nb1 * sh.nq1 * 128 * 4);
+  sh.off_h = off;
+  off += al256((size_t)sh.S * (L.Ipad / 2) * 8);
   sh.off_dout = off;
   off += al256((size_t)sh.S * L.H * 4);
   sh.layer_bytes = off;
-  sh.cnt_stride = kReadyCopies + sh.S * kSlotCopies + sh.nb2;
+  sh.cnt_stride = kReadyCopies + sh.nb2;
   return sh;
 }
 
@@ -933,13 +936,13 @@ size_t stack_scratch_bytes(const RmoeLayer& L, int n_layers) {
 }
 
 size_t stack_counter_count(const RmoeLayer& L, int n_layers) {
-  return ((size_t)stack_shape(L).cnt_stride * n_layers + 2) * kCntPad;
+  return (1 + (size_t)stack_shape(L).cnt_stride * n_layers + 2) * kCntPad;
 }
 
 hipError_t stack_check(const RmoeLayer& L, int n_cu) {
   const StackShape sh = stack_shape(L);
   if (L.H > kMaxH || L.n_routed > kMaxE || sh.S > kMaxSlots || kMaxDnUnits * sh.nkt2 > (kWaves - 1) * kMaxDnPos ||
-      sh.nq1 > kMaxQ || dn_lds_bytes(sh.nkt2) + kStaticLds > kLdsLimit)
+      L.I % 64 != 0 || dn_lds_bytes(sh.nkt2) + kStaticLds > kLdsLimit)
     return hipErrorInvalidValue;
 
   if (sh.n_dn > kMaxDnUnits * n_cu || n_cu < sh.nb2) return hipErrorInvalidValue;
@@ -976,7 +979,7 @@ hipError_t launch_decode_stack(const RmoeLayer* const* layers, int n_layers, con
   a.nb2 = sh.nb2;
   a.nkt1 = sh.nkt1;
   a.nkt2 = sh.nkt2;
-  a.nq1 = sh.nq1;
+  a.nhb = sh.nhb;
   a.n_gu = sh.n_gu;
   a.n_dn = sh.n_dn;
   a.Ep = (L0.n_routed + 31) / 32 * 32;
@@ -987,7 +990,7 @@ hipError_t launch_decode_stack(const RmoeLayer* const* layers, int n_layers, con
   a.scratch = s.stack;
   a.layer_bytes = sh.layer_bytes;
   a.off_lpart = sh.off_lpart;
-  a.off_gpart = sh.off_gpart;
+  a.off_h = sh.off_h;
   a.off_dout = sh.off_dout;
   a.cnt = s.stack_cnt;
   a.cnt_stride = sh.cnt_stride;
@@ -1006,14 +1009,12 @@ hipError_t launch_decode_stack(const RmoeLayer* const* layers, int n_layers, con
   const size_t lds = dn_lds_bytes(sh.nkt2);
   const dim3 grid(n_cu), block(kThreads);
   const int pos_need = (kMaxDnUnits * sh.nkt2 + kWaves - 2) / (kWaves - 1);
-  if (pos_need <= 2 && a.E <= 128 && sh.nq1 <= 2)
-    hipLaunchKernelGGL((decode_stack_kernel<2, 1, 2>), grid, block, lds, st, a);
-  else if (pos_need <= 2 && a.E <= 128)
-    hipLaunchKernelGGL((decode_stack_kernel<2, 1, 4>), grid, block, lds, st, a);
+  if (pos_need <= 2 && a.E <= 128)
+    hipLaunchKernelGGL((decode_stack_kernel<2, 1>), grid, block, lds, st, a);
   else if (a.E <= 128)
-    hipLaunchKernelGGL((decode_stack_kernel<4, 1, 4>), grid, block, lds, st, a);
+    hipLaunchKernelGGL((decode_stack_kernel<4, 1>), grid, block, lds, st, a);
   else
-    hipLaunchKernelGGL((decode_stack_kernel<4, 2, 4>), grid, block, lds, st, a);
+    hipLaunchKernelGGL((decode_stack_kernel<4, 2>), grid, block, lds, st, a);
   return hipGetLastError();
 }
 
@@ -1021,8 +1022,8 @@ hipError_t launch_decode_stack(const RmoeLayer* const* layers, int n_layers, con
 // per CU of the most demanding instance at that size.
 hipError_t decode_stack_occupancy(int* blocks_per_cu) {
   const int dyn = (int)(kLdsLimit - kStaticLds);
-  const void* fns[4] = {(const void*)decode_stack_kernel<2, 1, 2>, (const void*)decode_stack_kernel<2, 1, 4>,
-                        (const void*)decode_stack_kernel<4, 1, 4>, (const void*)decode_stack_kernel<4, 2, 4>};
+  const void* fns[3] = {(const void*)decode_stack_kernel<2, 1>, (const void*)decode_stack_kernel<4, 1>,
+                        (const void*)decode_stack_kernel<4, 2>};
   int best = 1 << 30;
   for (const void* f : fns) {
     hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, dyn);

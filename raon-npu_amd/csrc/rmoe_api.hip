@@ -136,8 +136,16 @@ int reserve_layer(rmoe_ctx* ctx, const RmoeLayer& L, int T, int k) {
 // L's geometry.  Counters are zero when (re)allocated and after every complete launch.
 int reserve_stack(rmoe_ctx* ctx, const RmoeLayer& L, int n_layers) {
   RmoeScratch& s = ctx->s;
+  const unsigned* old_cnt = s.stack_cnt;
   TRY(grow(s.stack, s.stack_bytes, rmoe::stack_scratch_bytes(L, n_layers), ctx));
   TRY(grow(s.stack_cnt, s.stack_cnt_n, rmoe::stack_counter_count(L, n_layers), ctx));
+  // The decode stack tags its hand-off words with a launch counter kept beside its
+  // counters; when the counters start again from zero, no older word may carry a tag
+  // that a new launch accepts, so the hand-off area is cleared too.
+  if (s.stack_cnt != old_cnt) {
+    HIP_TRY(hipMemsetAsync(s.stack, 0, s.stack_bytes, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+  }
   return RMOE_OK;
 }
 
@@ -154,8 +162,11 @@ int sync_and_check(rmoe_ctx* ctx, hipStream_t st) {
     if (err & 8) {
       // A wait of the persistent decode kernel timed out: its counters are left
       // mid-way; clear them for the next launch.
+      // Its launch counter restarts with them, so its tagged hand-off words are cleared
+      // as well.
       if (ctx->s.stack_cnt) {
         HIP_TRY(hipMemsetAsync(ctx->s.stack_cnt, 0, ctx->s.stack_cnt_n * sizeof(unsigned), ctx->stream));
+        if (ctx->s.stack) HIP_TRY(hipMemsetAsync(ctx->s.stack, 0, ctx->s.stack_bytes, ctx->stream));
         HIP_TRY(hipStreamSynchronize(ctx->stream));
       }
       return fail(RMOE_EDEVICE, "persistent decode kernel timed out waiting for other workgroups");
