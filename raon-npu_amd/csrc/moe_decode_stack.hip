@@ -655,12 +655,6 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
       }
     };
     if (gu_d[0] < 0) issue_dn();
-    uint4 rwv[kMaxDnUnits][NIT][2];
-#pragma unroll
-    for (int d = 0; d < kMaxDnUnits; ++d)
-      load_router_slice<NIT>(a, a.rw[l + 1 < a.L ? l + 1 : l], dn_d[d][1], dn_d[d][0] >= 0 && l + 1 < a.L, dummy,
-                             rwv[d]);
-
     // ---- slot weights and id order (read by the combine, after later barriers), while
     // the weight loads are in flight.
     if (wave == 0) {
@@ -793,6 +787,14 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
           }
         }
       }
+      // Router weights of the next layer for the band shares of the logits: issued now,
+      // in flight during the band hand-off (holding them from the start of the layer
+      // would cost registers through the GU and DN phases).
+      uint4 rwv[kMaxDnUnits][NIT][2];
+#pragma unroll
+      for (int d = 0; d < kMaxDnUnits; ++d)
+        load_router_slice<NIT>(a, a.rw[l + 1 < a.L ? l + 1 : l], dn_d[d][1], dn_d[d][0] >= 0 && l + 1 < a.L, dummy,
+                               rwv[d]);
       red[wave][0][lane] = acc[0];
       red[wave][1][lane] = acc[1];
       __syncthreads();
@@ -829,13 +831,16 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
         const int b = dn_d[d][1];
         if (wave == 0) {
           const int row = 64 * b + lane;
-          float dv[kMaxSlots];
+          // d of every slot for this band into LDS, up to 9 loads in flight.
+          for (int q0 = 0; q0 < a.S; q0 += 9) {
+            float dv[9];
 #pragma unroll
-          for (int q = 0; q < kMaxSlots; ++q)
-            if (q < a.S) dv[q] = ld_hand_f32(&dout[(size_t)q * a.H + row]);
+            for (int i = 0; i < 9; ++i)
+              if (q0 + i < a.S) dv[i] = ld_hand_f32(&dout[(size_t)(q0 + i) * a.H + row]);
 #pragma unroll
-          for (int q = 0; q < kMaxSlots; ++q)
-            if (q < a.S) cmb[q][lane] = dv[q];
+            for (int i = 0; i < 9; ++i)
+              if (q0 + i < a.S) cmb[q0 + i][lane] = dv[i];
+          }
           // Ascending expert id: the slot order, then each slot's value and weight, read
           // from LDS in batches, then summed in order.
           float acc2 = 0.f;
