@@ -33,7 +33,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 # WRITE_SIZE (calibrated against a 512 MiB copy) over `bench.py --profile-pass`; the
 # summary and commands are in profiles/decode_prefill_hbm_counters.txt.  Re-measure
 # after changing the kernel.
-DECODE_TRAFFIC_BYTES = 1378061940
+DECODE_TRAFFIC_BYTES = 1334592840
 
 
 def log(msg: str) -> None:
