@@ -1,16 +1,20 @@
-// Prefill (many-token) MoE on bf16 MFMA: router GEMM + top-k, tile table over the
-// dispatch, grouped q4nx GEMMs (gate/up with the activation fused, down), ordered
-// combine.  Restates NpuBackend.moe_experts_grouped (npu/backend.py:4845-4979) and the
-// planner's scatter/combine (kernels/moe_grouped/planner.py:184-322) on the device.
+// Prefill (many-token) MoE on MFMA: router GEMM + top-k, tile table over the dispatch,
+// grouped q4nx GEMMs (gate/up with the activation fused, down), ordered combine.
+// Restates NpuBackend.moe_experts_grouped (npu/backend.py:4845-4979) and the planner's
+// scatter/combine (kernels/moe_grouped/planner.py:184-322) on the device.
 //
-// q4nx on MFMA without rounding the weights:  w = min + scale*n  (n = 4-bit code).
-// For one 32-column group g and a tile of tokens m and weight rows r:
-//   sum_k x[m,k] w[r,k] = 16*scale[r]*C'[m,r] + (min[r] - 16*scale[r]) * S[m]
-// where C' = sum_k x[m,k]*(1 + n[r,k]/16) is one v_mfma_f32_16x16x32_bf16 with the
-// codes as exact bf16 values (1 + n/16) and S[m] = sum_k x[m,k].  The first term is
-// added per group with one fp32 FMA per output (scales differ per row and group); the
-// second is a small GEMM over the groups, done on MFMA with S and the coefficient
-// split into bf16 hi + lo parts (relative error ~2^-16).
+// q4nx on fp16 MFMA without rounding the weights:  w = min + scale*n  (n = 4-bit code).
+// For one 32-column group g, activation row m and weight row r:
+//   sum_k x[m,k] w[r,k] = sum_k x[m,k] * (scale[r]*(n[r,k] - 8)) + (min[r] + 8*scale[r]) * S[m]
+// with S[m] = sum_k x[m,k].  scale*(n-8) has at most 11 significant bits (8 of the bf16
+// scale times |n-8| <= 8), so it is exact in fp16, and so is every bf16 activation: the
+// first sum is one v_mfma_f32_16x16x32_f16 per group with no per-group fix-up, and the
+// MFMAs of all groups accumulate in place.  Range: activation rows carry a power-of-two
+// exponent (x rows are normalised to max |x| in [2^14, 2^15); h chunks of 128 units are
+// scaled only when their largest value is outside [2^-6, 2^15)) and each weight row's
+// scales are normalised by a power of two (largest scale in [2^11, 2^12)); the
+// exponents are undone exactly in fp32.  The correction (second sum) is a small GEMM over the groups, done on bf16 MFMA
+// with S and the coefficient split exactly into three bf16 parts (six leading products).
 #include "rmoe_internal.h"
 
 namespace rmoe {
@@ -19,10 +23,50 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ f32x4_t mfma16(const uint4 a, const uint4 b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
                                                  0, 0, 0);
 }
+__device__ __forceinline__ f32x4_t mfma16h(const uint4 a, const uint4 b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0,
+                                                0, 0);
+}
+
+// Power-of-two exponents of the fp16 operands, from the largest magnitude v of a row or
+// chunk (an fp32 value; non-negative).  Zero for a zero or non-finite v (non-finite
+// values then pass through unchanged).
+//   normalise:  v * 2^-e in [2^14, 2^15)  (x rows: values down to 2^-31 v are exact)
+//   chunk:      0 while v is in [2^-6, 2^15), else normalise (h chunks of 128 units, so
+//               that a K step of the down GEMM rarely changes exponent).  With e = 0 the
+//               values from 2^-17 up are exact and smaller ones round to fp16's 2^-24
+//               grid: an absolute error below 2^-25, under 2^-19 v.
+__device__ __forceinline__ int f16_exp_normalise(float v) {
+  const int be = (int)(__float_as_uint(v) >> 23) & 0xff;
+  if (v == 0.f || be == 0xff) return 0;
+  return be == 0 ? -140 : be - 127 - 14;
+}
+__device__ __forceinline__ int f16_exp_chunk(float v) {
+  const int be = (int)(__float_as_uint(v) >> 23) & 0xff;
+  return (be >= 127 - 6 && be < 127 + 15) ? 0 : f16_exp_normalise(v);
+}
+// Two bf16 values (one dword) times 2^-e as an fp16 pair (exact for the ranges above).
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t v, int e) {
+  const float lo = __builtin_amdgcn_ldexpf(bf16_to_f32(v & 0xffffu), -e);
+  const float hi = __builtin_amdgcn_ldexpf(__uint_as_float(v & 0xffff0000u), -e);
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+}
+__device__ __forceinline__ float max_abs_bf16x8(const uint4 v) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m = fmaxf(m, fmaxf(fabsf(bf16_to_f32(w[i] & 0xffffu)), fabsf(__uint_as_float(w[i] & 0xffff0000u))));
+  return m;
+}
+// Row stride (bytes) of an exponent table [rows][K/128]: 16-byte aligned rows.
+__host__ __device__ inline int exp_stride(int K) { return ((K / 128) + 15) & ~15; }
 
 // Exact 3-way bf16 split of an fp32 value: v = hi + mid + lo (8 + 8 + 8 significant
 // bits cover the 24 of fp32), each part the RNE bf16 of the remainder.
@@ -32,6 +76,27 @@ __device__ __forceinline__ void split3_bf16(float v, uint32_t& hi, uint32_t& mid
   mid = f32_to_bf16(r);
   lo = f32_to_bf16(r - bf16_to_f32(mid));
 }
+// The same split by truncation (hi = the top 16 bits of v, then of the remainder): each
+// remainder is exact in fp32 and the last part has at most 8 significant bits, so again
+// v = hi + mid + lo exactly; the parts are returned as fp32 values on the bf16 grid.
+__device__ __forceinline__ void split3_trunc(float v, float& hi, float& mid, float& lo) {
+  hi = __uint_as_float(__float_as_uint(v) & 0xffff0000u);
+  const float r = v - hi;
+  mid = __uint_as_float(__float_as_uint(r) & 0xffff0000u);
+  lo = r - mid;
+}
+// bf16 pair (a | b << 16) of two fp32 values on the bf16 grid (their top halves).
+__device__ __forceinline__ uint32_t pack_bf16_top(float a, float b) {
+  return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+}
+// Two fp32 values -> RNE bf16 pair (a | b << 16) in one instruction; NaNs stay NaNs (the
+// reference's canonical 0x7FC0 is applied where values leave the device path).
+__device__ __forceinline__ uint32_t cvt_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+  const bf16x2v v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ float bf16_round_hw(float a) { return __uint_as_float(cvt_bf16x2(a, 0.f) << 16); }
 // Group sums are stored planar per row: planes hi, mid, lo of Gp = round_up(G, 8) bf16
 // each (G = groups per row; the padding groups hold 0), so that 8 consecutive groups of
 // one plane are one 16-byte MFMA operand.
@@ -185,29 +250,55 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
   }
 }
 
-// ------------------------------------------------------------ row group sums --
-// S[row, g] = sum of the 32 bf16 values of group g of row `row`, as an exact 3-way bf16
-// split in the planar layout of store_split3_planar.  Thread per (row, padded group).
-__global__ void group_sums_kernel(const uint16_t* __restrict__ src, int rows, int K, uint16_t* __restrict__ dst) {
-  const int G = K / 32, Gp = sum_planes_gp(G);
-  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (size_t)rows * Gp) return;
-  const size_t row = idx / Gp;
-  const int g = (int)(idx % Gp);
-  uint16_t* d = dst + row * 3 * Gp + g;
-  if (g >= G) {
-    d[0] = d[Gp] = d[2 * Gp] = 0;
-    return;
-  }
-  const uint32_t* p = reinterpret_cast<const uint32_t*>(src + row * K + 32 * g);
-  float s = 0.f;
+// ------------------------------------------------------ activation prep (x) --
+// For each token row of x [T, K] (bf16): the fp16 operand xh = x * 2^-e (e normalises
+// the row, f16_exp_normalise), the exponent table xe [T][exp_stride(K)] (e in every
+// chunk of 128 columns), and the group sums S[row, g] of the 32 bf16 values of each
+// group as an exact 3-way bf16 split (planar layout of store_split3_planar).
+// One wave per row; lane L holds the 16-byte chunks L + 64i (K <= 8192).
+constexpr int kPrepMaxChunks = 16;
+__global__ __launch_bounds__(256) void prep_x_kernel(const uint16_t* __restrict__ x, int T, int K,
+                                                     uint16_t* __restrict__ xh, int8_t* __restrict__ xe,
+                                                     uint16_t* __restrict__ xsum) {
+  const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int nch = K / 8, G = K / 32, Gp = sum_planes_gp(G);
+  const uint4* src = reinterpret_cast<const uint4*>(x + (size_t)t * K);
+  uint4 v[kPrepMaxChunks];
+  float mx = 0.f;
+  uint16_t* ds = xsum + (size_t)t * 3 * Gp;
 #pragma unroll
-  for (int c = 0; c < 16; ++c) {
-    const uint32_t v = p[c];
-    s += bf16_to_f32(v & 0xffffu);
-    s += bf16_to_f32(v >> 16);
+  for (int i = 0; i < kPrepMaxChunks; ++i) {
+    const int c = lane + 64 * i;
+    if (64 * i >= nch) break;
+    float s = 0.f;
+    if (c < nch) {
+      v[i] = src[c];
+      mx = fmaxf(mx, max_abs_bf16x8(v[i]));
+      const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+      for (int d = 0; d < 4; ++d) s += bf16_to_f32(w[d] & 0xffffu) + __uint_as_float(w[d] & 0xffff0000u);
+    }
+    // A group is the four chunks of lanes 4q..4q+3.
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    if (c < nch && (lane & 3) == 0) store_split3_planar(ds + c / 4, Gp, s);
   }
-  store_split3_planar(d, Gp, s);
+  for (int g = G + lane; g < Gp; g += 64) ds[g] = ds[Gp + g] = ds[2 * Gp + g] = 0;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  const int e = f16_exp_normalise(mx);
+  uint4* dst = reinterpret_cast<uint4*>(xh + (size_t)t * K);
+#pragma unroll
+  for (int i = 0; i < kPrepMaxChunks; ++i) {
+    const int c = lane + 64 * i;
+    if (64 * i >= nch) break;
+    if (c < nch)
+      dst[c] = make_uint4(bf16x2_to_f16x2(v[i].x, e), bf16x2_to_f16x2(v[i].y, e), bf16x2_to_f16x2(v[i].z, e),
+                          bf16x2_to_f16x2(v[i].w, e));
+  }
+  const int es = exp_stride(K);
+  for (int c = lane; c < es; c += 64) xe[(size_t)t * es + c] = (int8_t)e;
 }
 
 // ----------------------------------------------------------------- tile table --
@@ -253,8 +344,9 @@ struct GemmArgs {
   int inter;         // gate/up: I (the up rows start at I)
   int mode;          // 0: gate/up + activation -> h; 1: down -> D
   int n_tiles;       // WG N-tiles (gate/up: ceil(I/128) units of 128; down: N_total/256 rows of 256)
-  // activation rows
-  const uint16_t* src;      // mode 0: x [T, K] gathered by token; mode 1: h [rows, K] in sorted order
+  // activation rows (fp16 operands, see prep_x_kernel and the gate/up epilogue)
+  const uint16_t* src;      // mode 0: xh [T, K] gathered by token; mode 1: h [rows, K] in sorted order
+  const int8_t* aexp;       // exponent table of src rows: [rows][exp_stride(K)], one per 128 columns
   const int32_t* order;     // mode 0: sorted position -> assignment (token*k + route)
   int k_routes;
   int n_routed;             // group id n_routed = shared expert (rows identity tokens / sorted)
@@ -268,6 +360,7 @@ struct GemmArgs {
   uint16_t* out;            // mode 0: h [rows, out_ld]; mode 1: D [rows, out_ld]
   int out_ld;
   uint16_t* out_ssum;       // mode 0: group sums of the h rows (planar, out_ld/32 groups)
+  int8_t* out_exp;          // mode 0: exponent table of the h rows [rows][exp_stride(out_ld)]
   int act;
   float gb, vb;
 };
@@ -362,6 +455,8 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void grouped_gemm_kernel(GemmArgs a, int tile_cap) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kGemmLds];
   __shared__ int rowidx[kBM];
+  __shared__ __attribute__((aligned(16))) int8_t row_e0[kBM];
+  __shared__ __attribute__((aligned(16))) int8_t row_e1[kBM];  // exponent of each tile row in the first / last K step
   // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs; each XCD takes a
   // contiguous eighth of the tiles that exist (the grid is sized for the worst case, the
   // tile count is known only here), so m-tiles sharing a weight tile meet in the same
@@ -384,11 +479,34 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   // Source row of each tile row (token for gate/up, sorted row for down); rows past the
   // tile use the tile's first row (their results are not stored).
+  // The exponents of a row's K steps (chunks of 128 columns) come in 16-byte words;
+  // `chg` tells the workgroup whether any row changes exponent between K steps.
+  const int es = exp_stride(a.K);
+  int chg_row = 0;
   if (tid < kBM) {
     const int p = row0 + (tid < nrows ? tid : 0);
-    rowidx[tid] = a.mode == 1 ? p : (e < a.n_routed ? a.order[p] / a.k_routes : p - a.shared_base);
+    const int src = a.mode == 1 ? p : (e < a.n_routed ? a.order[p] / a.k_routes : p - a.shared_base);
+    rowidx[tid] = src;
+    const uint4* er = reinterpret_cast<const uint4*>(a.aexp + (size_t)src * es);
+    const int8_t first = a.aexp[(size_t)src * es];
+    uint32_t diff = 0u;
+    const uint32_t rep = (uint32_t)(uint8_t)first * 0x01010101u;
+    for (int w = 0; w < es / 16; ++w) {
+      const uint4 q = er[w];
+      const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        // bytes past K/128 are not compared
+        const int b0 = 16 * w + 4 * d, nb = min(4, max(0, nkt - b0));
+        const uint32_t m = nb >= 4 ? 0xffffffffu : ((1u << (8 * nb)) - 1u);
+        diff |= (qw[d] ^ rep) & m;
+      }
+    }
+    chg_row = diff != 0u;
+    row_e0[tid] = first;
+    row_e1[tid] = a.aexp[(size_t)src * es + nkt - 1];
   }
-  __syncthreads();
+  const int chg = __syncthreads_or(chg_row);
 
   // The workgroup's four 64-row weight bands.  Gate/up: gate bands 2nt, 2nt+1, up bands
   // I/64 + 2nt, +1; a band past I (last n-tile when I % 128 != 0) reads band 0 instead
@@ -486,24 +604,30 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
   const uint32_t xrow = (uint32_t)l16 * 256u;  // A row 16m + l16: m*4096 + xrow
 
-  // acc += sum_g (min - 16*scale)[r, g] * S[m, g] over one block of 32 groups, both
-  // factors split exactly into 3 bf16 parts; the 6 leading products are kept.
+  // acc += sum_g (min + 8*scale)[r, g] * S[m, g] over one block of 32 groups, both
+  // factors split exactly into 3 bf16 parts; the 6 leading products are kept.  Also
+  // tracks the largest scale (as bf16 bits; scales are >= 0) of the lane's weight rows.
+  uint32_t smax[2] = {0u, 0u};
   auto corr_block = [&](int blk, const u32x4v (&c)[2][2]) {
     const int gl = 32 * blk + 8 * lq;
     uint4 bc[2][3];
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
       const uint32_t sv[8] = {c[f][0].x, c[f][0].y, c[f][0].z, c[f][0].w, c[f][1].x, c[f][1].y, c[f][1].z, c[f][1].w};
-      uint32_t hv[8], mv[8], lv[8];
+      float hv[8], mv[8], lv[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float coef =
-            gl + i < G ? bf16_to_f32(sv[i] >> 16) - 16.f * bf16_to_f32(sv[i] & 0xffffu) : 0.f;
-        split3_bf16(coef, hv[i], mv[i], lv[i]);
+        const bool live = gl + i < G;
+        const float coef = live ? __uint_as_float(sv[i] & 0xffff0000u) + 8.f * bf16_to_f32(sv[i] & 0xffffu) : 0.f;
+        if (live) smax[f] = max(smax[f], sv[i] & 0x7fffu);
+        split3_trunc(coef, hv[i], mv[i], lv[i]);
       }
-      bc[f][0] = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
-      bc[f][1] = make_uint4(mv[0] | (mv[1] << 16), mv[2] | (mv[3] << 16), mv[4] | (mv[5] << 16), mv[6] | (mv[7] << 16));
-      bc[f][2] = make_uint4(lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16), lv[4] | (lv[5] << 16), lv[6] | (lv[7] << 16));
+      bc[f][0] = make_uint4(pack_bf16_top(hv[0], hv[1]), pack_bf16_top(hv[2], hv[3]), pack_bf16_top(hv[4], hv[5]),
+                            pack_bf16_top(hv[6], hv[7]));
+      bc[f][1] = make_uint4(pack_bf16_top(mv[0], mv[1]), pack_bf16_top(mv[2], mv[3]), pack_bf16_top(mv[4], mv[5]),
+                            pack_bf16_top(mv[6], mv[7]));
+      bc[f][2] = make_uint4(pack_bf16_top(lv[0], lv[1]), pack_bf16_top(lv[2], lv[3]), pack_bf16_top(lv[4], lv[5]),
+                            pack_bf16_top(lv[6], lv[7]));
     }
     const uint8_t* ss = lds + 2 * kStageBytes + (blk & 1) * kSBlock + l16 * kSRow + 16 * lq;
 #pragma unroll
@@ -541,24 +665,67 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     corr_block(blk, cfb);
   }
 
-  // Main K loop:  acc += scale[r, g] * sum_k x[m,k] (16 + n[r,k])  per group g.
-  uint32_t kmask, kone;  // in registers so that v_and_or_b32 can take them
-  asm volatile("v_mov_b32 %0, 0x780078" : "=v"(kmask));
-  asm volatile("v_mov_b32 %0, 0x41804180" : "=v"(kone));
+  // Weight-row exponents: the lane's rows in fragment f have their scales multiplied by
+  // 2^-fx[f] so that the largest lies in [2^11, 2^12) (8 * scale < 2^15 in fp16).
+  int fx[2];
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    uint32_t m = smax[f];
+    m = max(m, (uint32_t)__shfl_xor((int)m, 16, 64));
+    m = max(m, (uint32_t)__shfl_xor((int)m, 32, 64));
+    const int be = (int)(m >> 7) & 0xff;
+    fx[f] = (m == 0u || be == 0xff) ? 0 : (be == 0 ? -138 : be - 127 - 11);
+  }
+  // The correction is in true units; the K loop accumulates in units of
+  // 2^-(row exponent + fx): scale acc over (lane rows 16m + 4lq + i, fragment f).
+  auto scale_rows = [&](const int8_t* rowe, int sign) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const uint32_t e4 = *reinterpret_cast<const uint32_t*>(rowe + 16 * m + 4 * lq);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int er = (int)(int8_t)(e4 >> (8 * i));
+#pragma unroll
+        for (int f = 0; f < 2; ++f) acc[m][f][i] = __builtin_amdgcn_ldexpf(acc[m][f][i], sign * (er + fx[f]));
+      }
+    }
+  };
+  scale_rows(row_e0, -1);
+
+  // Main K loop:  acc += sum_k x[m,k] * (scale[r,g] * 2^-fx) * (n[r,k] - 8), fp16 operands.
+  // Codes -> fp16 pairs 1024 + n by one v_and_or_b32 (nibble q and q+4 of a dword are
+  // columns 8d+2q and 8d+2q+1), then (t - 1032) * s' in packed fp16, exact.
+  uint32_t kmask, kmagic;  // in registers so that v_and_or_b32 can take them
+  asm volatile("v_mov_b32 %0, 0xf000f" : "=v"(kmask));
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(kmagic));
+  const f16x2_t k1032 = {(_Float16)1032.0f, (_Float16)1032.0f};
   const uint32_t wrow0 = (uint32_t)(ft0 * kTileBytes + frow * 16);
   auto kstep = [&](int kt, const int slot) {
     // After this barrier every wave is past step kt-1 (and the correction), so slot
     // (kt+2) % 3 is free.
     ring_wait(kt + 1 < nkt ? per_stage : 0);
     if (kt + 2 < nkt) issue(kt + 2);
+    if (chg && kt > 0) {
+      // Some row of the tile changes exponent at a K step (h chunks outside [2^-6, 2^15)).
+#pragma unroll
+      for (int m = 0; m < 8; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int8_t* er = a.aexp + (size_t)rowidx[16 * m + 4 * lq + i] * es;
+          const int d = (int)er[kt - 1] - (int)er[kt];
+          acc[m][0][i] = __builtin_amdgcn_ldexpf(acc[m][0][i], d);
+          acc[m][1][i] = __builtin_amdgcn_ldexpf(acc[m][1][i], d);
+        }
+    }
     const uint8_t* xs = lds + slot * kStageBytes;
     const uint8_t* ws = xs + kXBytes + wrow0;
     // Operands of group j+1 (8 A fragments, 2 code words) are read while group j's
     // MFMAs run.
     auto read_a = [&](int j, uint4 (&av)[8]) {
       const uint32_t xc = 16u * (uint32_t)((4 * j + lq) ^ l16);  // row % 16 == l16
+      const uint8_t* pa = xs + (xrow + xc);                      // fragments m*4096 apart
 #pragma unroll
-      for (int m = 0; m < 8; ++m) av[m] = *reinterpret_cast<const uint4*>(xs + m * 4096 + xrow + xc);
+      for (int m = 0; m < 8; ++m) av[m] = *reinterpret_cast<const uint4*>(pa + m * 4096);
     };
     auto read_codes = [&](int j, uint32_t (&cv)[2]) {
 #pragma unroll
@@ -567,56 +734,75 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     uint4 smv[2];
 #pragma unroll
     for (int f = 0; f < 2; ++f) smv[f] = *reinterpret_cast<const uint4*>(ws + 2 * f * kTileBytes + kCodeBytes);
-    uint4 av[8];
-    uint32_t cv[2];
-    read_a(0, av);
-    read_codes(0, cv);
-    float sc[2][4];
+    // Two operand buffers in turn: group j reads buffer j & 1 while group j+1's
+    // operands arrive in the other.
+    uint4 av0[8], av1[8];
+    uint32_t cv0[2], cv1[2];
+    read_a(0, av0);
+    read_codes(0, cv0);
+    f16x2_t sc[2][4];
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
-      sc[f][0] = bf16_to_f32(smv[f].x & 0xffffu);
-      sc[f][1] = bf16_to_f32(smv[f].y & 0xffffu);
-      sc[f][2] = bf16_to_f32(smv[f].z & 0xffffu);
-      sc[f][3] = bf16_to_f32(smv[f].w & 0xffffu);
-    }
+      const uint32_t sw[4] = {smv[f].x, smv[f].y, smv[f].z, smv[f].w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint4 avn[8];
-      uint32_t cvn[2];
-      if (j < 3) {
-        read_a(j + 1, avn);
-        read_codes(j + 1, cvn);
+      for (int j = 0; j < 4; ++j) {
+        const float v = __builtin_amdgcn_ldexpf(bf16_to_f32(sw[j] & 0xffffu), -fx[f]);
+        sc[f][j] = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_cvt_pkrtz(v, v));
+      }
+    }
+    // The scheduling barriers keep the order: all LDS reads of group j+1 are issued
+    // before group j's MFMAs (left alone, the compiler reads each A fragment just
+    // before its MFMA and waits on it).
+    auto group = [&](int j, const uint4 (&av)[8], const uint32_t (&cv)[2]) {
+      uint32_t t[2][4];
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        t[f][0] = and_or(cv[f], kmask, kmagic);
+        t[f][1] = and_or(cv[f] >> 4, kmask, kmagic);
+        t[f][2] = and_or(cv[f] >> 8, kmask, kmagic);
+        t[f][3] = and_or(cv[f] >> 12, kmask, kmagic);
       }
       uint4 b[2];
 #pragma unroll
       for (int f = 0; f < 2; ++f) {
-        b[f].x = and_or(cv[f] << 3, kmask, kone);
-        b[f].y = and_or(cv[f] >> 1, kmask, kone);
-        b[f].z = and_or(cv[f] >> 5, kmask, kone);
-        b[f].w = and_or(cv[f] >> 9, kmask, kone);
+        f16x2_t h[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) h[q] = __builtin_bit_cast(f16x2_t, t[f][q]) - k1032;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) h[q] = h[q] * sc[f][j];
+        b[f] = make_uint4(__builtin_bit_cast(uint32_t, h[0]), __builtin_bit_cast(uint32_t, h[1]),
+                          __builtin_bit_cast(uint32_t, h[2]), __builtin_bit_cast(uint32_t, h[3]));
       }
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
 #pragma unroll
-        for (int f = 0; f < 2; ++f) {
-          const f32x4_t c = mfma16(av[m], b[f], f32x4_t{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[m][f][i] = fmaf(sc[f][j], c[i], acc[m][f][i]);
-        }
+        for (int f = 0; f < 2; ++f) acc[m][f] = mfma16h(av[m], b[f], acc[m][f]);
       }
-      if (j < 3) {
-#pragma unroll
-        for (int m = 0; m < 8; ++m) av[m] = avn[m];
-        cv[0] = cvn[0];
-        cv[1] = cvn[1];
-      }
-    }
+    };
+    __builtin_amdgcn_sched_barrier(0);
+    read_a(1, av1);
+    read_codes(1, cv1);
+    __builtin_amdgcn_sched_barrier(0);
+    group(0, av0, cv0);
+    __builtin_amdgcn_sched_barrier(0);
+    read_a(2, av0);
+    read_codes(2, cv0);
+    __builtin_amdgcn_sched_barrier(0);
+    group(1, av1, cv1);
+    __builtin_amdgcn_sched_barrier(0);
+    read_a(3, av1);
+    read_codes(3, cv1);
+    __builtin_amdgcn_sched_barrier(0);
+    group(2, av0, cv0);
+    __builtin_amdgcn_sched_barrier(0);
+    group(3, av1, cv1);
   };
   for (int kt = 0; kt < nkt; kt += kStages) {
     kstep(kt, 0);
     if (kt + 1 < nkt) kstep(kt + 1, 1);
     if (kt + 2 < nkt) kstep(kt + 2, 2);
   }
+  scale_rows(row_e1, 1);
   // Every wave is past its last ring read: the slots become the output staging.
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
@@ -629,10 +815,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int m = 0; m < 8; ++m)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 4; i += 2) {
           const int r = 16 * m + 4 * lq + i;
-          const float g = bf16_round(acc[m][0][i]), u = bf16_round(acc[m][1][i]);
-          stage0[r * kOutStride + 16 * wave + l16] = (uint16_t)f32_to_bf16(swiglu_fast(g, u));
+          const uint32_t gu0 = cvt_bf16x2(acc[m][0][i], acc[m][1][i]);
+          const uint32_t gu1 = cvt_bf16x2(acc[m][0][i + 1], acc[m][1][i + 1]);
+          const float h0 = swiglu_fast(bf16_to_f32(gu0 & 0xffffu), __uint_as_float(gu0 & 0xffff0000u));
+          const float h1 = swiglu_fast(bf16_to_f32(gu1 & 0xffffu), __uint_as_float(gu1 & 0xffff0000u));
+          const uint32_t hp = cvt_bf16x2(h0, h1);
+          stage0[r * kOutStride + 16 * wave + l16] = (uint16_t)(hp & 0xffffu);
+          stage0[(r + 1) * kOutStride + 16 * wave + l16] = (uint16_t)(hp >> 16);
         }
     } else {
       // SiTU-GLU: g and u (bf16) go through slots 1 and 2 and the activation runs in a
@@ -644,13 +835,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = 16 * m + 4 * lq + i;
-          gs[r * kOutStride + 16 * wave + l16] = (uint16_t)f32_to_bf16(acc[m][0][i]);
-          us[r * kOutStride + 16 * wave + l16] = (uint16_t)f32_to_bf16(acc[m][1][i]);
+          const uint32_t gu = cvt_bf16x2(acc[m][0][i], acc[m][1][i]);
+          gs[r * kOutStride + 16 * wave + l16] = (uint16_t)(gu & 0xffffu);
+          us[r * kOutStride + 16 * wave + l16] = (uint16_t)(gu >> 16);
         }
       __syncthreads();
       for (int idx = tid; idx < kBM * 128; idx += 512) {
         const int o = (idx >> 7) * kOutStride + (idx & 127);
-        stage0[o] = (uint16_t)f32_to_bf16(act_situ(bf16_to_f32(gs[o]), bf16_to_f32(us[o]), a.gb, a.vb));
+        stage0[o] = (uint16_t)cvt_bf16x2(act_situ(bf16_to_f32(gs[o]), bf16_to_f32(us[o]), a.gb, a.vb), 0.f);
       }
     }
     __syncthreads();
@@ -670,25 +862,40 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         store_split3_planar(a.out_ssum + (size_t)(row0 + r) * 3 * Gpo + 4 * nt + q, Gpo, hs);
       }
     }
-    // 128 rows x 16 chunks of 8 units.
+    // 128 rows x 16 chunks of 8 units, stored as the fp16 operand of the down GEMM: the
+    // row's 128 units (one K step there) share an exponent (f16_exp_chunk of their
+    // largest magnitude; 16 lanes per row).
+    const int eso = exp_stride(a.out_ld);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int cid = tid + 512 * q, r = cid >> 4, c = cid & 15;
-      if (r < nrows && 128 * nt + 8 * c < a.inter)
+      const bool live = 128 * nt + 8 * c < a.inter;
+      const uint4 v = *reinterpret_cast<const uint4*>(stage0 + r * kOutStride + 8 * c);
+      float mx = live ? max_abs_bf16x8(v) : 0.f;
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      const int ex = f16_exp_chunk(mx);
+      if (r < nrows && live)
         *reinterpret_cast<uint4*>(a.out + (size_t)(row0 + r) * a.out_ld + 128 * nt + 8 * c) =
-            *reinterpret_cast<const uint4*>(stage0 + r * kOutStride + 8 * c);
+            make_uint4(bf16x2_to_f16x2(v.x, ex), bf16x2_to_f16x2(v.y, ex), bf16x2_to_f16x2(v.z, ex),
+                       bf16x2_to_f16x2(v.w, ex));
+      if (r < nrows && c == 0) a.out_exp[(size_t)(row0 + r) * eso + nt] = (int8_t)ex;
     }
   } else {
     // Output columns 0..127 of the 256 in slot 0 (fragment 0), 128..255 in slot 1.
+    // (bf16 by the hardware conversion: a NaN may keep its payload here; the combine
+    // canonicalises what it passes through.)
 #pragma unroll
     for (int m = 0; m < 8; ++m)
 #pragma unroll
       for (int f = 0; f < 2; ++f)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 4; i += 2) {
           const int r = 16 * m + 4 * lq + i;
           uint16_t* st = stage0 + f * (kStageBytes / 2);
-          st[r * kOutStride + 16 * wave + l16] = (uint16_t)f32_to_bf16(acc[m][f][i]);
+          const uint32_t p2 = cvt_bf16x2(acc[m][f][i], acc[m][f][i + 1]);
+          st[r * kOutStride + 16 * wave + l16] = (uint16_t)(p2 & 0xffffu);
+          st[(r + 1) * kOutStride + 16 * wave + l16] = (uint16_t)(p2 >> 16);
         }
     __syncthreads();
 #pragma unroll
@@ -746,7 +953,16 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
           make_uint4(o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16));
     if (has_shared) {
       const uint4 sv = *reinterpret_cast<const uint4*>(D + (size_t)(shared_base + t) * H + c0);
-      if (shared_out) *reinterpret_cast<uint4*>(shared_out + (size_t)t * H + c0) = sv;
+      if (shared_out) {
+        // every NaN leaves as 0x7FC0 (quant/q4nx.py:32-44)
+        uint32_t q[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if ((q[i] & 0x7fffu) > 0x7f80u) q[i] = (q[i] & 0xffff0000u) | 0x7FC0u;
+          if ((q[i] & 0x7fff0000u) > 0x7f800000u) q[i] = (q[i] & 0xffffu) | 0x7FC00000u;
+        }
+        *reinterpret_cast<uint4*>(shared_out + (size_t)t * H + c0) = make_uint4(q[0], q[1], q[2], q[3]);
+      }
       const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -769,8 +985,10 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   }
 }
 
-// Zero h[:, I:Ipad] and the group sums of those columns (thread per row).
-__global__ void zero_pad_cols_kernel(uint16_t* __restrict__ h, uint16_t* __restrict__ hsum, int rows, int I, int Ipad) {
+// Zero h[:, I:Ipad], the group sums of those columns and the exponents of the 128-unit
+// chunks that no gate/up tile writes (thread per row).
+__global__ void zero_pad_cols_kernel(uint16_t* __restrict__ h, uint16_t* __restrict__ hsum, int8_t* __restrict__ hexp,
+                                     int rows, int I, int Ipad) {
   const int r = blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= rows) return;
   for (int c = I; c < Ipad; ++c) h[(size_t)r * Ipad + c] = 0;
@@ -779,33 +997,48 @@ __global__ void zero_pad_cols_kernel(uint16_t* __restrict__ h, uint16_t* __restr
   const int Gp = sum_planes_gp(Ipad / 32);
   uint16_t* d = hsum + (size_t)r * 3 * Gp;
   for (int g = I / 32; g < Gp; ++g) d[g] = d[Gp + g] = d[2 * Gp + g] = 0;
+  const int es = exp_stride(Ipad);
+  for (int c = (I + 127) / 128; c < es; ++c) hexp[(size_t)r * es + c] = 0;
 }
 
-// h[shared_base + t] = RTNE(act(shared_gu[t])) (padded to Ipad) and its group sums.
+// h[shared_base + t] = RTNE(act(shared_gu[t])) (padded to Ipad) as the fp16 operand of
+// the down GEMM, with its group sums and chunk exponents.  Thread per (row, 128-unit
+// chunk): the bf16 values are written first, then rewritten scaled by the chunk's
+// exponent (f16_exp_chunk).  Ipad is a multiple of 256, so no planar padding groups.
 __global__ void shared_act_kernel(const uint16_t* __restrict__ gu, int T, int I, int Ipad, int act, float gb, float vb,
-                                  uint16_t* __restrict__ h, uint16_t* __restrict__ hsum) {
-  const int G = Ipad / 32, Gp = sum_planes_gp(G);
+                                  uint16_t* __restrict__ h, uint16_t* __restrict__ hsum, int8_t* __restrict__ hexp) {
+  const int nch = Ipad / 128, Gp = sum_planes_gp(Ipad / 32), es = exp_stride(Ipad);
   const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (size_t)T * Gp) return;
-  const int t = (int)(idx / Gp), g = (int)(idx % Gp);
-  uint16_t* d = hsum + (size_t)t * 3 * Gp + g;
-  if (g >= G) {
-    d[0] = d[Gp] = d[2 * Gp] = 0;
-    return;
-  }
-  float s = 0.f;
-  for (int c = 0; c < 32; ++c) {
-    const int col = 32 * g + c;
-    uint16_t v = 0;
-    if (col < I) {
-      const float gg = bf16_to_f32(gu[(size_t)t * 2 * I + col]);
-      const float uu = bf16_to_f32(gu[(size_t)t * 2 * I + I + col]);
-      v = (uint16_t)f32_to_bf16(act_apply(act, gg, uu, gb, vb));
+  if (idx >= (size_t)T * nch) return;
+  const int t = (int)(idx / nch), ch = (int)(idx % nch);
+  uint16_t* hr = h + (size_t)t * Ipad + 128 * ch;
+  float mx = 0.f;
+  for (int q = 0; q < 4; ++q) {
+    float s = 0.f;
+    for (int c = 0; c < 32; ++c) {
+      const int col = 128 * ch + 32 * q + c;
+      uint16_t v = 0;
+      if (col < I) {
+        const float gg = bf16_to_f32(gu[(size_t)t * 2 * I + col]);
+        const float uu = bf16_to_f32(gu[(size_t)t * 2 * I + I + col]);
+        v = (uint16_t)f32_to_bf16(act_apply(act, gg, uu, gb, vb));
+      }
+      hr[32 * q + c] = v;
+      s += bf16_to_f32(v);
+      mx = fmaxf(mx, fabsf(bf16_to_f32(v)));
     }
-    h[(size_t)t * Ipad + col] = v;
-    s += bf16_to_f32(v);
+    store_split3_planar(hsum + (size_t)t * 3 * Gp + 4 * ch + q, Gp, s);
   }
-  store_split3_planar(d, Gp, s);
+  const int ex = f16_exp_chunk(mx);
+  for (int c = 0; c < 128; c += 2) {
+    const uint32_t w = (uint32_t)hr[c] | ((uint32_t)hr[c + 1] << 16);
+    const uint32_t o = bf16x2_to_f16x2(w, ex);
+    hr[c] = (uint16_t)(o & 0xffffu);
+    hr[c + 1] = (uint16_t)(o >> 16);
+  }
+  hexp[(size_t)t * es + ch] = (int8_t)ex;
+  if (ch == 0)
+    for (int c = nch; c < es; ++c) hexp[(size_t)t * es + c] = 0;
 }
 
 }  // namespace
@@ -841,12 +1074,15 @@ hipError_t launch_topk(const float* logits, int T, int E, int k, int score, cons
 size_t prefill_scratch_bytes(const RmoeLayer& L, int T) {
   const size_t A = (size_t)T * L.top_k, R = A + T;
   const size_t tiles = A / kBM + L.n_routed + T / kBM + 4;
-  return R * L.Ipad * 2                                  // h
+  return R * L.Ipad * 2                                  // h (fp16 operand)
          + R * 3 * sum_planes_gp(L.Ipad / 32) * 2        // h group sums
+         + R * exp_stride(L.Ipad)                        // h exponents
          + R * L.H * 2                                   // D
+         + (size_t)T * L.H * 2                           // xh (fp16 operand)
+         + (size_t)T * exp_stride(L.H)                   // x exponents
          + (size_t)T * 3 * sum_planes_gp(L.H / 32) * 2   // x group sums
          + (size_t)T * L.n_routed * 4                    // logits
-         + tiles * 4 + 256 * 9;                          // tile table, counts, carve rounding
+         + tiles * 4 + 256 * 12;                         // tile table, counts, carve rounding
 }
 
 hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, const int32_t* ids_in, const float* wts_in,
@@ -856,6 +1092,7 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   const int k = L.top_k, E = L.n_routed;
   const size_t A = (size_t)T * k, R = A + T;
   if (L.n_shared < 1 || prefill_scratch_bytes(L, T) > scratch_bytes) return hipErrorInvalidValue;
+  if (L.H % 128 || L.H > 64 * kPrepMaxChunks * 8 || L.Ipad % 256) return hipErrorInvalidValue;
   if (A > s.order_elems || (size_t)((A + 1023) / 1024) * E > s.chunk_elems) return hipErrorInvalidValue;
   uint8_t* p = scratch;
   auto carve = [&](size_t bytes) {
@@ -866,7 +1103,10 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   uint16_t* h = (uint16_t*)carve(R * L.Ipad * 2);
   const int Gph = sum_planes_gp(L.Ipad / 32), Gpx = sum_planes_gp(L.H / 32);
   uint16_t* hsum = (uint16_t*)carve(R * 3 * Gph * 2);
+  int8_t* hexp = (int8_t*)carve(R * exp_stride(L.Ipad));
   uint16_t* D = (uint16_t*)carve(R * L.H * 2);
+  uint16_t* xh = (uint16_t*)carve((size_t)T * L.H * 2);
+  int8_t* xexp = (int8_t*)carve((size_t)T * exp_stride(L.H));
   uint16_t* xsum = (uint16_t*)carve((size_t)T * 3 * Gpx * 2);
   float* logits = (float*)carve((size_t)T * E * 4);
   const int tile_cap = (int)(A / kBM + E + T / kBM + 4);
@@ -885,15 +1125,13 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   }
   err = launch_dispatch(ids, T, k, E, s.order, s.inv, s.offsets, s, st);
   if (err != hipSuccess) return err;
-  {
-    const size_t n = (size_t)T * Gpx;
-    hipLaunchKernelGGL(group_sums_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, T, L.H, xsum);
-    if ((err = hipGetLastError()) != hipSuccess) return err;
-  }
+  hipLaunchKernelGGL(prep_x_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, x, T, L.H, xh, xexp, xsum);
+  if ((err = hipGetLastError()) != hipSuccess) return err;
   if (L.Ipad > L.I) {
-    // h columns past I (and their group sums) feed the zero-padded down columns.
-    hipLaunchKernelGGL(zero_pad_cols_kernel, dim3((unsigned)((R + 255) / 256)), dim3(256), 0, st, h, hsum, (int)R, L.I,
-                       L.Ipad);
+    // h columns past I (their group sums and chunk exponents) feed the zero-padded down
+    // columns.
+    hipLaunchKernelGGL(zero_pad_cols_kernel, dim3((unsigned)((R + 255) / 256)), dim3(256), 0, st, h, hsum, hexp,
+                       (int)R, L.I, L.Ipad);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
   // Gate/up (+ activation): routed groups, and the shared expert unless its gate/up is given.
@@ -905,7 +1143,8 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   g.inter = L.I;
   g.mode = 0;
   g.n_tiles = (L.I + 127) / 128;
-  g.src = x;
+  g.src = xh;
+  g.aexp = xexp;
   g.order = s.order;
   g.k_routes = k;
   g.n_routed = E;
@@ -918,15 +1157,16 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   g.out = h;
   g.out_ld = L.Ipad;
   g.out_ssum = hsum;
+  g.out_exp = hexp;
   g.act = act;
   g.gb = gb;
   g.vb = vb;
   hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(512), 0, st, s.offsets, E, g.shared_rows, tiles, ntiles, tile_cap);
   if ((err = hipGetLastError()) != hipSuccess) return err;
   if (shared_gu) {
-    const size_t n = (size_t)T * Gph;
+    const size_t n = (size_t)T * (L.Ipad / 128);
     hipLaunchKernelGGL(shared_act_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, shared_gu, T, L.I,
-                       L.Ipad, act, gb, vb, h + A * L.Ipad, hsum + A * 3 * Gph);
+                       L.Ipad, act, gb, vb, h + A * L.Ipad, hsum + A * 3 * Gph, hexp + A * exp_stride(L.Ipad));
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
   {
@@ -947,11 +1187,13 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   d.mode = 1;
   d.n_tiles = L.H / 256;
   d.src = h;
+  d.aexp = hexp;
   d.ssum = hsum;
   d.shared_rows = T;
   d.out = D;
   d.out_ld = L.H;
   d.out_ssum = nullptr;
+  d.out_exp = nullptr;
   {
     const int blocks = (d.n_tiles * tile_cap + 7) / 8 * 8;
     hipLaunchKernelGGL(grouped_gemm_kernel, dim3(blocks), dim3(512), 0, st, d, tile_cap);

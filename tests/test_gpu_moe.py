@@ -335,3 +335,68 @@ def test_residual_stack_matches_oracle(gpu_ctx):
         _check_ulp(h.cpu().numpy().view(np.uint16), ref, "stack")
     for lyr in layers:
         lyr.free()
+
+
+def _check_rows(out, ref, label):
+    """Per token row: rel-L2 <= 1e-3 and every element within two bf16 ulps of the
+    reference or 1e-2 of the row's largest magnitude -- the global bars, applied to each
+    row on its own scale (rows here span magnitudes from 2^-30 to 2^40)."""
+    a = bf16_to_f32(out).astype(np.float64)
+    b = bf16_to_f32(ref).astype(np.float64)
+    worst = 0.0
+    for t in range(b.shape[0]):
+        scale = max(np.abs(b[t]).max(), 1e-300)
+        ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(b[t]), 1e-300))) - 7)
+        bound = np.maximum(TOL_ABS * scale, 2 * ulp)
+        d = np.abs(a[t] - b[t])
+        rel = np.linalg.norm(a[t] - b[t]) / max(np.linalg.norm(b[t]), 1e-300)
+        assert np.all(d <= bound) and rel <= TOL_REL, (label, t, scale, rel, float(np.max(d / bound)))
+        worst = max(worst, rel)
+    print(f"{label}: worst row rel-L2 {worst:.3e}")
+
+
+def test_grouped_operand_ranges(gpu_ctx):
+    """The fp16 operands of the grouped GEMM carry power-of-two exponents (activation rows
+    and h chunks, weight rows).  Experts whose weights are scaled by 2^-24, 2^14 and 2^20,
+    rows whose column halves differ by 2^20 in scale, and token rows scaled by 2^-30 ..
+    2^20 (h chunks then fall outside [2^-6, 2^15) in both directions) must all match the
+    oracle row by row."""
+    geom = G.MoeGeometry(hidden=512, inter=256, n_routed=8, n_shared=1, top_k=2)
+    rng = np.random.default_rng(950)
+    wscale = [1.0, 1.0, 2.0 ** -24, 2.0 ** -24, 2.0 ** 14, 2.0 ** 20, 1.0, 1.0, 1.0]
+    gu, dn = [], []
+    from oracle.q4nx import pack_gemv, quantize
+
+    for e in range(geom.n_experts):
+        w = rng.normal(0.0, 0.02, (2 * geom.inter, geom.hidden)).astype(np.float32) * np.float32(wscale[e])
+        d = rng.normal(0.0, 0.02, (geom.hidden, geom.inter_pad)).astype(np.float32) * np.float32(wscale[e])
+        if e in (6, 7):  # rows whose groups span 2^20 in scale
+            w[:, : geom.hidden // 2] *= np.float32(2.0 ** -20)
+            d[:, : geom.inter_pad // 2] *= np.float32(2.0 ** 20)
+        gu.append(pack_gemv(*quantize(w)))
+        dn.append(pack_gemv(*quantize(d)))
+    lyr = gpu_ctx.create_layer(950, geom)
+    lyr.upload_experts(b"".join(gu), b"".join(dn))
+    lyr.set_router(f32_to_bf16(rng.normal(0.0, 0.02, (geom.n_routed, geom.hidden)).astype(np.float32)),
+                   score="softmax")
+    lyr.reserve(64)
+    bank = om.ExpertBank(b"".join(gu), b"".join(dn), geom.n_experts, geom.hidden, geom.inter, geom.inter_pad,
+                         cache=geom.n_experts)
+    # token classes: (expert pair, token scales); tiny weights never meet tiny tokens
+    classes = [((0, 1), (0, 20, -30, 10)), ((2, 3), (0, 10)), ((4, 5), (0, -10, 5)), ((6, 7), (0, 5, -8))]
+    T = 48
+    xs = random_tokens(T, geom.hidden, 951)
+    ids = np.zeros((T, geom.top_k), np.int64)
+    for t in range(T):
+        pair, scales = classes[t % 4]
+        ids[t] = pair if t % 8 < 4 else pair[::-1]
+        sc = scales[(t // 4) % len(scales)]
+        xs[t] = f32_to_bf16(bf16_to_f32(xs[t]) * np.float32(2.0 ** sc))
+    w = rng.random((T, geom.top_k), dtype=np.float32) + 0.5
+    sgu = np.stack([om.shared_gate_up(bank, geom.shared_id, x) for x in xs])
+    routed, sdown = lyr.moe_experts_grouped(xs, ids, w, sgu, None, None)
+    r_ref, s_ref = om.moe_experts_grouped(bank, xs, ids, w, sgu, geom.shared_id, None, None)
+    assert np.all(np.isfinite(bf16_to_f32(r_ref))) and np.all(np.isfinite(bf16_to_f32(s_ref)))
+    _check_rows(routed, r_ref, "ranges routed")
+    _check_rows(sdown, s_ref, "ranges shared_down")
+    lyr.free()
