@@ -252,8 +252,7 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
 
 // ------------------------------------------------------ activation prep (x) --
 // For each token row of x [T, K] (bf16): the fp16 operand xh = x * 2^-e (e normalises
-// the row, f16_exp_normalise), the exponent table xe [T][exp_stride(K)] (e in every
-// chunk of 128 columns), and the group sums S[row, g] of the 32 bf16 values of each
+// the row, f16_exp_normalise), its exponent xe [T], and the group sums S[row, g] of the 32 bf16 values of each
 // group as an exact 3-way bf16 split (planar layout of store_split3_planar).
 // One wave per row; lane L holds the 16-byte chunks L + 64i (K <= 8192).
 constexpr int kPrepMaxChunks = 16;
@@ -297,8 +296,7 @@ __global__ __launch_bounds__(256) void prep_x_kernel(const uint16_t* __restrict_
       dst[c] = make_uint4(bf16x2_to_f16x2(v[i].x, e), bf16x2_to_f16x2(v[i].y, e), bf16x2_to_f16x2(v[i].z, e),
                           bf16x2_to_f16x2(v[i].w, e));
   }
-  const int es = exp_stride(K);
-  for (int c = lane; c < es; c += 64) xe[(size_t)t * es + c] = (int8_t)e;
+  if (lane == 0) xe[t] = (int8_t)e;
 }
 
 // ----------------------------------------------------------------- tile table --
@@ -346,7 +344,7 @@ struct GemmArgs {
   int n_tiles;       // WG N-tiles (gate/up: ceil(I/128) units of 128; down: N_total/256 rows of 256)
   // activation rows (fp16 operands, see prep_x_kernel and the gate/up epilogue)
   const uint16_t* src;      // mode 0: xh [T, K] gathered by token; mode 1: h [rows, K] in sorted order
-  const int8_t* aexp;       // exponent table of src rows: [rows][exp_stride(K)], one per 128 columns
+  const int8_t* aexp;       // power-of-two exponent of each src row (int8 [rows])
   const int32_t* order;     // mode 0: sorted position -> assignment (token*k + route)
   int k_routes;
   int n_routed;             // group id n_routed = shared expert (rows identity tokens / sorted)
@@ -360,7 +358,7 @@ struct GemmArgs {
   uint16_t* out;            // mode 0: h [rows, out_ld]; mode 1: D [rows, out_ld]
   int out_ld;
   uint16_t* out_ssum;       // mode 0: group sums of the h rows (planar, out_ld/32 groups)
-  int8_t* out_exp;          // mode 0: exponent table of the h rows [rows][exp_stride(out_ld)]
+  int8_t* out_exp;          // mode 0: exponents of the h rows per 128-unit chunk [rows][exp_stride(out_ld)]
   int act;
   float gb, vb;
 };
@@ -455,8 +453,7 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void grouped_gemm_kernel(GemmArgs a, int tile_cap) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kGemmLds];
   __shared__ int rowidx[kBM];
-  __shared__ __attribute__((aligned(16))) int8_t row_e0[kBM];
-  __shared__ __attribute__((aligned(16))) int8_t row_e1[kBM];  // exponent of each tile row in the first / last K step
+  __shared__ __attribute__((aligned(16))) int8_t row_e[kBM];  // power-of-two exponent of each tile row  // exponent of each tile row in the first / last K step
   // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs; each XCD takes a
   // contiguous eighth of the tiles that exist (the grid is sized for the worst case, the
   // tile count is known only here), so m-tiles sharing a weight tile meet in the same
@@ -479,34 +476,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   // Source row of each tile row (token for gate/up, sorted row for down); rows past the
   // tile use the tile's first row (their results are not stored).
-  // The exponents of a row's K steps (chunks of 128 columns) come in 16-byte words;
-  // `chg` tells the workgroup whether any row changes exponent between K steps.
-  const int es = exp_stride(a.K);
-  int chg_row = 0;
   if (tid < kBM) {
     const int p = row0 + (tid < nrows ? tid : 0);
     const int src = a.mode == 1 ? p : (e < a.n_routed ? a.order[p] / a.k_routes : p - a.shared_base);
     rowidx[tid] = src;
-    const uint4* er = reinterpret_cast<const uint4*>(a.aexp + (size_t)src * es);
-    const int8_t first = a.aexp[(size_t)src * es];
-    uint32_t diff = 0u;
-    const uint32_t rep = (uint32_t)(uint8_t)first * 0x01010101u;
-    for (int w = 0; w < es / 16; ++w) {
-      const uint4 q = er[w];
-      const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        // bytes past K/128 are not compared
-        const int b0 = 16 * w + 4 * d, nb = min(4, max(0, nkt - b0));
-        const uint32_t m = nb >= 4 ? 0xffffffffu : ((1u << (8 * nb)) - 1u);
-        diff |= (qw[d] ^ rep) & m;
-      }
-    }
-    chg_row = diff != 0u;
-    row_e0[tid] = first;
-    row_e1[tid] = a.aexp[(size_t)src * es + nkt - 1];
+    row_e[tid] = a.aexp[src];
   }
-  const int chg = __syncthreads_or(chg_row);
+  __syncthreads();
 
   // The workgroup's four 64-row weight bands.  Gate/up: gate bands 2nt, 2nt+1, up bands
   // I/64 + 2nt, +1; a band past I (last n-tile when I % 128 != 0) reads band 0 instead
@@ -525,12 +501,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int ft0 = wave >> 2, frow = 16 * (wave & 3) + l16;
 
   // Copy descriptors.  Activations: copy q = wave + 8i (i < 4) fills LDS rows 4q..4q+3;
-  // lane L brings row 4q + L/16, chunk (L%16) ^ (row%16).
+  // lane L brings row 4q + L/16 into position L%16 of the row: 16-byte chunk
+  // tau((L%16) ^ (row%16)), tau(4a + b) = 4b + a.  A row's chunk c then sits at position
+  // tau(c) ^ (row%16): the K loop's reads of chunks 4lq + j land on positions
+  // (4j + lq) ^ row, a pattern free of LDS bank conflicts.
   const uint8_t* xg[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int q = wave + 8 * i, r = 4 * q + (lane >> 4);
-    const int c = (lane & 15) ^ (r & 15);
+    const int pc = (lane & 15) ^ (r & 15), c = ((pc & 3) << 2) | (pc >> 2);
     xg[i] = reinterpret_cast<const uint8_t*>(a.src + (size_t)rowidx[r] * a.K) + 16 * c;
   }
   // Weights: copy v = wave + 8i (i < 3, v < 20) is 1 KB piece v%5 of tile v/5.
@@ -630,23 +609,30 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                             pack_bf16_top(lv[6], lv[7]));
     }
     const uint8_t* ss = lds + 2 * kStageBytes + (blk & 1) * kSBlock + l16 * kSRow + 16 * lq;
+    // Six products per (m, f), smallest first; consecutive MFMAs go to different
+    // accumulators (16 independent chains).
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
+    for (int half = 0; half < 2; ++half) {
       __builtin_amdgcn_sched_barrier(0);
-      const uint4 ah = *reinterpret_cast<const uint4*>(ss + m * 16 * kSRow);
-      const uint4 am = *reinterpret_cast<const uint4*>(ss + m * 16 * kSRow + 64);
-      const uint4 al = *reinterpret_cast<const uint4*>(ss + m * 16 * kSRow + 128);
+      uint4 ah[4], am[4], al[4];
 #pragma unroll
-      for (int f = 0; f < 2; ++f) {
-        f32x4_t cc = acc[m][f];
-        cc = mfma16(al, bc[f][0], cc);
-        cc = mfma16(am, bc[f][1], cc);
-        cc = mfma16(ah, bc[f][2], cc);
-        cc = mfma16(am, bc[f][0], cc);
-        cc = mfma16(ah, bc[f][1], cc);
-        cc = mfma16(ah, bc[f][0], cc);
-        acc[m][f] = cc;
+      for (int mm = 0; mm < 4; ++mm) {
+        const int m = 4 * half + mm;
+        ah[mm] = *reinterpret_cast<const uint4*>(ss + m * 16 * kSRow);
+        am[mm] = *reinterpret_cast<const uint4*>(ss + m * 16 * kSRow + 64);
+        al[mm] = *reinterpret_cast<const uint4*>(ss + m * 16 * kSRow + 128);
       }
+#pragma unroll
+      for (int p = 0; p < 6; ++p)
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm)
+#pragma unroll
+          for (int f = 0; f < 2; ++f) {
+            const int m = 4 * half + mm;
+            const uint4 av = p == 0 ? al[mm] : (p == 1 || p == 3) ? am[mm] : ah[mm];
+            const uint4 bv = (p == 0 || p == 3 || p == 5) ? bc[f][0] : (p == 1 || p == 4) ? bc[f][1] : bc[f][2];
+            acc[m][f] = mfma16(av, bv, acc[m][f]);
+          }
     }
   };
   // Block 0: past it are in flight group-sum block 1 (3) and K steps 0 and 1.
@@ -690,119 +676,136 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
   };
-  scale_rows(row_e0, -1);
+  scale_rows(row_e, -1);
 
   // Main K loop:  acc += sum_k x[m,k] * (scale[r,g] * 2^-fx) * (n[r,k] - 8), fp16 operands.
-  // Codes -> fp16 pairs 1024 + n by one v_and_or_b32 (nibble q and q+4 of a dword are
-  // columns 8d+2q and 8d+2q+1), then (t - 1032) * s' in packed fp16, exact.
-  uint32_t kmask, kmagic;  // in registers so that v_and_or_b32 can take them
+  // K assignment of the MFMAs: within a K step (4 groups of 32 columns), MFMA j takes
+  // columns 32*lq + 8j .. +7 from lane quarter lq.  A lane's B operands of a step then
+  // all come from one group (lq) of its row -- one 16-byte code word and one scale per
+  // step -- and a group's scale stays inside B, so groups may share an MFMA.
+  // Codes -> fp16 by one v_and_or_b32 per pair: nibbles (q, q+4) of a dword are the
+  // columns (2q, 2q+1); masked in place, nibble pair 0 gives 1024 + n and pair 1 gives
+  // 1024 + 16n, so B = (t - 1032) * s' or (t - 1152) * (s'/16), exact.
+  uint32_t kmask, kmask_hi, kmagic;  // in registers so that v_and_or_b32 can take them
   asm volatile("v_mov_b32 %0, 0xf000f" : "=v"(kmask));
+  asm volatile("v_mov_b32 %0, 0xf000f0" : "=v"(kmask_hi));
   asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(kmagic));
   const f16x2_t k1032 = {(_Float16)1032.0f, (_Float16)1032.0f};
+  const f16x2_t k1152 = {(_Float16)1152.0f, (_Float16)1152.0f};
   const uint32_t wrow0 = (uint32_t)(ft0 * kTileBytes + frow * 16);
-  auto kstep = [&](int kt, const int slot) {
-    // After this barrier every wave is past step kt-1 (and the correction), so slot
-    // (kt+2) % 3 is free.
-    ring_wait(kt + 1 < nkt ? per_stage : 0);
-    if (kt + 2 < nkt) issue(kt + 2);
-    if (chg && kt > 0) {
-      // Some row of the tile changes exponent at a K step (h chunks outside [2^-6, 2^15)).
-#pragma unroll
-      for (int m = 0; m < 8; ++m)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int8_t* er = a.aexp + (size_t)rowidx[16 * m + 4 * lq + i] * es;
-          const int d = (int)er[kt - 1] - (int)er[kt];
-          acc[m][0][i] = __builtin_amdgcn_ldexpf(acc[m][0][i], d);
-          acc[m][1][i] = __builtin_amdgcn_ldexpf(acc[m][1][i], d);
-        }
-    }
-    const uint8_t* xs = lds + slot * kStageBytes;
-    const uint8_t* ws = xs + kXBytes + wrow0;
-    // Operands of group j+1 (8 A fragments, 2 code words) are read while group j's
-    // MFMAs run.
-    auto read_a = [&](int j, uint4 (&av)[8]) {
-      const uint32_t xc = 16u * (uint32_t)((4 * j + lq) ^ l16);  // row % 16 == l16
-      const uint8_t* pa = xs + (xrow + xc);                      // fragments m*4096 apart
-#pragma unroll
-      for (int m = 0; m < 8; ++m) av[m] = *reinterpret_cast<const uint4*>(pa + m * 4096);
-    };
-    auto read_codes = [&](int j, uint32_t (&cv)[2]) {
-#pragma unroll
-      for (int f = 0; f < 2; ++f) cv[f] = *reinterpret_cast<const uint32_t*>(ws + 2 * f * kTileBytes + j * 1024 + 4 * lq);
-    };
-    uint4 smv[2];
-#pragma unroll
-    for (int f = 0; f < 2; ++f) smv[f] = *reinterpret_cast<const uint4*>(ws + 2 * f * kTileBytes + kCodeBytes);
-    // Two operand buffers in turn: group j reads buffer j & 1 while group j+1's
-    // operands arrive in the other.
-    uint4 av0[8], av1[8];
-    uint32_t cv0[2], cv1[2];
-    read_a(0, av0);
-    read_codes(0, cv0);
-    f16x2_t sc[2][4];
+  auto read_w = [&](const int slot, uint4 (&cw)[2], uint32_t (&sw)[2]) {
+    const uint8_t* ws = lds + slot * kStageBytes + kXBytes + wrow0;
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
-      const uint32_t sw[4] = {smv[f].x, smv[f].y, smv[f].z, smv[f].w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float v = __builtin_amdgcn_ldexpf(bf16_to_f32(sw[j] & 0xffffu), -fx[f]);
-        sc[f][j] = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_cvt_pkrtz(v, v));
-      }
+      cw[f] = *reinterpret_cast<const uint4*>(ws + 2 * f * kTileBytes + 1024 * lq);
+      sw[f] = *reinterpret_cast<const uint32_t*>(ws + 2 * f * kTileBytes + kCodeBytes + 4 * lq);
     }
-    // The scheduling barriers keep the order: all LDS reads of group j+1 are issued
-    // before group j's MFMAs (left alone, the compiler reads each A fragment just
-    // before its MFMA and waits on it).
-    auto group = [&](int j, const uint4 (&av)[8], const uint32_t (&cv)[2]) {
-      uint32_t t[2][4];
-#pragma unroll
-      for (int f = 0; f < 2; ++f) {
-        t[f][0] = and_or(cv[f], kmask, kmagic);
-        t[f][1] = and_or(cv[f] >> 4, kmask, kmagic);
-        t[f][2] = and_or(cv[f] >> 8, kmask, kmagic);
-        t[f][3] = and_or(cv[f] >> 12, kmask, kmagic);
-      }
-      uint4 b[2];
-#pragma unroll
-      for (int f = 0; f < 2; ++f) {
-        f16x2_t h[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) h[q] = __builtin_bit_cast(f16x2_t, t[f][q]) - k1032;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) h[q] = h[q] * sc[f][j];
-        b[f] = make_uint4(__builtin_bit_cast(uint32_t, h[0]), __builtin_bit_cast(uint32_t, h[1]),
-                          __builtin_bit_cast(uint32_t, h[2]), __builtin_bit_cast(uint32_t, h[3]));
-      }
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
-#pragma unroll
-        for (int f = 0; f < 2; ++f) acc[m][f] = mfma16h(av[m], b[f], acc[m][f]);
-      }
-    };
-    __builtin_amdgcn_sched_barrier(0);
-    read_a(1, av1);
-    read_codes(1, cv1);
-    __builtin_amdgcn_sched_barrier(0);
-    group(0, av0, cv0);
-    __builtin_amdgcn_sched_barrier(0);
-    read_a(2, av0);
-    read_codes(2, cv0);
-    __builtin_amdgcn_sched_barrier(0);
-    group(1, av1, cv1);
-    __builtin_amdgcn_sched_barrier(0);
-    read_a(3, av1);
-    read_codes(3, cv1);
-    __builtin_amdgcn_sched_barrier(0);
-    group(2, av0, cv0);
-    __builtin_amdgcn_sched_barrier(0);
-    group(3, av1, cv1);
   };
-  for (int kt = 0; kt < nkt; kt += kStages) {
-    kstep(kt, 0);
-    if (kt + 1 < nkt) kstep(kt + 1, 1);
-    if (kt + 2 < nkt) kstep(kt + 2, 2);
+  auto scales = [&](const uint32_t (&sw)[2], f16x2_t (&s1)[2], f16x2_t (&s16)[2]) {
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const float sc = bf16_to_f32(sw[f] & 0xffffu);
+      const float v1 = __builtin_amdgcn_ldexpf(sc, -fx[f]), v16 = __builtin_amdgcn_ldexpf(sc, -fx[f] - 4);
+      s1[f] = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_cvt_pkrtz(v1, v1));
+      s16[f] = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_cvt_pkrtz(v16, v16));
+    }
+  };
+  auto read_a = [&](const int slot, int j, uint4 (&av)[8]) {
+    const uint32_t xc = 16u * (uint32_t)((4 * j + lq) ^ l16);  // chunk 4lq+j of row 16m+l16
+    const uint8_t* pa = lds + slot * kStageBytes + (xrow + xc);  // fragments m*4096 apart
+#pragma unroll
+    for (int m = 0; m < 8; ++m) av[m] = *reinterpret_cast<const uint4*>(pa + m * 4096);
+  };
+  auto build_b = [&](const uint4 (&cw)[2], int j, const f16x2_t (&s1)[2], const f16x2_t (&s16)[2],
+                     uint4 (&b)[2]) {
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const uint32_t cv = j == 0 ? cw[f].x : j == 1 ? cw[f].y : j == 2 ? cw[f].z : cw[f].w;
+      const uint32_t u = cv >> 8;
+      const f16x2_t h0 = (__builtin_bit_cast(f16x2_t, and_or(cv, kmask, kmagic)) - k1032) * s1[f];
+      const f16x2_t h1 = (__builtin_bit_cast(f16x2_t, and_or(cv, kmask_hi, kmagic)) - k1152) * s16[f];
+      const f16x2_t h2 = (__builtin_bit_cast(f16x2_t, and_or(u, kmask, kmagic)) - k1032) * s1[f];
+      const f16x2_t h3 = (__builtin_bit_cast(f16x2_t, and_or(u, kmask_hi, kmagic)) - k1152) * s16[f];
+      b[f] = make_uint4(__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1),
+                        __builtin_bit_cast(uint32_t, h2), __builtin_bit_cast(uint32_t, h3));
+    }
+  };
+  auto mfmas = [&](const uint4 (&av)[8], const uint4 (&b)[2]) {
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+#pragma unroll
+      for (int m = 0; m < 8; ++m) acc[m][f] = mfma16h(av[m], b[f], acc[m][f]);
+    }
+  };
+  // Software pipeline.  Region (kt, j) issues the LDS reads of group j+1, runs the MFMAs
+  // of group j and builds group j+1's B operands between them (one wave's back-to-back
+  // MFMAs leave issue slots that independent VALU fills at little cost); the scheduling
+  // group barriers fix that interleave.  Group 3's MFMAs of a step run after the next
+  // step's barrier, under that step's first LDS reads and B build.
+#define RMOE_INTERLEAVE()                                                   \
+  do {                                                                      \
+    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);                     \
+    _Pragma("unroll") for (int q_ = 0; q_ < 16; ++q_) {                     \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                    \
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);                    \
+    }                                                                       \
+  } while (0)
+  uint4 avA[8], avB[8], bA[2], bB[2], cw[2];
+  uint32_t sw[2];
+  f16x2_t s1[2], s16[2];
+  // Regions 1..3 of the step in `slot` (group 0's operands are in avA / bA).
+  auto step_body = [&](const int slot) {
+    __builtin_amdgcn_sched_barrier(0);
+    read_a(slot, 1, avB);
+    mfmas(avA, bA);
+    build_b(cw, 1, s1, s16, bB);
+    RMOE_INTERLEAVE();
+    __builtin_amdgcn_sched_barrier(0);
+    read_a(slot, 2, avA);
+    mfmas(avB, bB);
+    build_b(cw, 2, s1, s16, bA);
+    RMOE_INTERLEAVE();
+    __builtin_amdgcn_sched_barrier(0);
+    read_a(slot, 3, avB);
+    mfmas(avA, bA);
+    build_b(cw, 3, s1, s16, bB);
+    RMOE_INTERLEAVE();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Step kt >= 1 in ring slot `slot` (= kt % 3): barrier, refill, then region 0 runs
+  // group 3 of step kt-1 while step kt's first operands arrive and its B is built.
+  auto step = [&](int kt, const int slot) {
+    // After this barrier every wave is past its reads of step kt-1, so slot (kt+2) % 3
+    // is free; step kt's copies have landed.
+    ring_wait(kt + 1 < nkt ? per_stage : 0);
+    if (kt + 2 < nkt) issue(kt + 2);
+    read_w(slot, cw, sw);
+    __builtin_amdgcn_sched_barrier(0);
+    read_a(slot, 0, avA);
+    mfmas(avB, bB);  // group 3 of step kt-1
+    scales(sw, s1, s16);
+    build_b(cw, 0, s1, s16, bA);
+    RMOE_INTERLEAVE();
+    __builtin_amdgcn_sched_barrier(0);
+    step_body(slot);
+  };
+  // Step 0: after this barrier every wave is past the correction, so slot 2 is free.
+  ring_wait(nkt > 1 ? per_stage : 0);
+  if (2 < nkt) issue(2);
+  read_w(0, cw, sw);
+  __builtin_amdgcn_sched_barrier(0);
+  read_a(0, 0, avA);
+  scales(sw, s1, s16);
+  build_b(cw, 0, s1, s16, bA);
+  step_body(0);
+  for (int kt = 1; kt < nkt; kt += kStages) {
+    step(kt, 1);
+    if (kt + 1 < nkt) step(kt + 1, 2);
+    if (kt + 2 < nkt) step(kt + 2, 0);
   }
-  scale_rows(row_e1, 1);
+  mfmas(avB, bB);  // group 3 of the last step
+#undef RMOE_INTERLEAVE
+  scale_rows(row_e, 1);
   // Every wave is past its last ring read: the slots become the output staging.
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
@@ -1041,6 +1044,36 @@ __global__ void shared_act_kernel(const uint16_t* __restrict__ gu, int T, int I,
     for (int c = nch; c < es; ++c) hexp[(size_t)t * es + c] = 0;
 }
 
+// One exponent per h row for the down GEMM: the row's chunks (128 units, one exponent
+// each from the gate/up epilogue or shared_act_kernel) are brought to the largest chunk
+// exponent; a chunk below it is rescaled by 2^(e_c - e_row) (values more than 2^38
+// below the row's largest keep their fp16 grid rounding).  Rows whose chunks agree,
+// nearly all, only read their exponents.  Thread per row.
+__global__ void h_unify_kernel(uint16_t* __restrict__ h, const int8_t* __restrict__ hexp, int rows, int Ipad,
+                               int8_t* __restrict__ hrow) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const int nch = Ipad / 128, es = exp_stride(Ipad);
+  const int8_t* er = hexp + (size_t)r * es;
+  int emax = -128, emin = 127;
+  for (int c = 0; c < nch; ++c) {
+    emax = max(emax, (int)er[c]);
+    emin = min(emin, (int)er[c]);
+  }
+  hrow[r] = (int8_t)emax;
+  if (emin == emax) return;
+  for (int c = 0; c < nch; ++c) {
+    const int d = (int)er[c] - emax;
+    if (d == 0) continue;
+    uint32_t* hc = reinterpret_cast<uint32_t*>(h + (size_t)r * Ipad + 128 * c);
+    for (int i = 0; i < 64; ++i) {
+      const f16x2_t v = __builtin_bit_cast(f16x2_t, hc[i]);
+      const float lo = __builtin_amdgcn_ldexpf((float)v[0], d), hi = __builtin_amdgcn_ldexpf((float)v[1], d);
+      hc[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+    }
+  }
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------ launchers --
@@ -1076,10 +1109,10 @@ size_t prefill_scratch_bytes(const RmoeLayer& L, int T) {
   const size_t tiles = A / kBM + L.n_routed + T / kBM + 4;
   return R * L.Ipad * 2                                  // h (fp16 operand)
          + R * 3 * sum_planes_gp(L.Ipad / 32) * 2        // h group sums
-         + R * exp_stride(L.Ipad)                        // h exponents
+         + R * exp_stride(L.Ipad) + R                    // h exponents (per chunk, per row)
          + R * L.H * 2                                   // D
          + (size_t)T * L.H * 2                           // xh (fp16 operand)
-         + (size_t)T * exp_stride(L.H)                   // x exponents
+         + (size_t)T                                     // x exponents
          + (size_t)T * 3 * sum_planes_gp(L.H / 32) * 2   // x group sums
          + (size_t)T * L.n_routed * 4                    // logits
          + tiles * 4 + 256 * 12;                         // tile table, counts, carve rounding
@@ -1104,9 +1137,10 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   const int Gph = sum_planes_gp(L.Ipad / 32), Gpx = sum_planes_gp(L.H / 32);
   uint16_t* hsum = (uint16_t*)carve(R * 3 * Gph * 2);
   int8_t* hexp = (int8_t*)carve(R * exp_stride(L.Ipad));
+  int8_t* hrow = (int8_t*)carve(R);
   uint16_t* D = (uint16_t*)carve(R * L.H * 2);
   uint16_t* xh = (uint16_t*)carve((size_t)T * L.H * 2);
-  int8_t* xexp = (int8_t*)carve((size_t)T * exp_stride(L.H));
+  int8_t* xexp = (int8_t*)carve((size_t)T);
   uint16_t* xsum = (uint16_t*)carve((size_t)T * 3 * Gpx * 2);
   float* logits = (float*)carve((size_t)T * E * 4);
   const int tile_cap = (int)(A / kBM + E + T / kBM + 4);
@@ -1174,6 +1208,9 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
     hipLaunchKernelGGL(grouped_gemm_kernel, dim3(blocks), dim3(512), 0, st, g, tile_cap);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
+  hipLaunchKernelGGL(h_unify_kernel, dim3((unsigned)((R + 255) / 256)), dim3(256), 0, st, h, hexp, (int)R, L.Ipad,
+                     hrow);
+  if ((err = hipGetLastError()) != hipSuccess) return err;
   // Down: every sorted row (routed + shared), rows of h contiguous.
   if (shared_gu) {
     hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(512), 0, st, s.offsets, E, T, tiles, ntiles, tile_cap);
@@ -1187,7 +1224,7 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   d.mode = 1;
   d.n_tiles = L.H / 256;
   d.src = h;
-  d.aexp = hexp;
+  d.aexp = hrow;
   d.ssum = hsum;
   d.shared_rows = T;
   d.out = D;
