@@ -95,6 +95,13 @@ int rmoe_matrix_shape(rmoe_ctx* ctx, int handle, int* M, int* K);
 int rmoe_matrix_upload_bfp16(rmoe_ctx* ctx, const void* gemv_bytes, size_t nbytes, int M, int K, int* handle);
 /* RMOE_FMT_* of a matrix (rmoe_matrix_download returns that format's bytes). */
 int rmoe_matrix_format(rmoe_ctx* ctx, int handle, int* fmt);
+/* Dense q4nx matrix [M, K] straight from a row-major llama.cpp Q4_K tensor (block_q4_K:
+ * 144 bytes per 256 weights of a row; M*K/256*144 bytes; M % 128 == 0, K % 256 == 0),
+ * converted on the device: every 4-bit code is kept and each 32-column group gets
+ * scale = RTNE_bf16(d*sc), min = RTNE_bf16(-dmin*mn).  Replaces GGUFReader.q4nx_components
+ * for a Q4_K tensor (quant/gguf_q4k.py:160-186, 228-233) followed by pack_gemv and the
+ * bundle load; rmoe_matrix_download returns the equivalent pack_gemv bytes. */
+int rmoe_matrix_upload_q4k(rmoe_ctx* ctx, const void* q4k_bytes, size_t nbytes, int M, int K, int* handle);
 
 /* y[T, M] = RTNE_bf16(x[T, K] @ W^T), fp32 accumulation.  Replaces NpuBackend.linear /
  * _execute_gemv for a q4nx or bfp16 bundle (npu/backend.py:3569-3721, 3908-4021) and
@@ -117,6 +124,17 @@ int rmoe_reserve(rmoe_ctx* ctx, int layer, int max_tokens);
  * gate_up: expert_bytes = 2I*H*5/8; down: H*Ipad*5/8.  Replaces moe_b1/moe_b2 uploads. */
 int rmoe_layer_upload_experts(rmoe_ctx* ctx, int layer, const void* gate_up, size_t gu_nbytes,
                               const void* down, size_t dn_nbytes);
+/* One part of expert `expert` from a row-major Q4_K tensor, converted on the device as in
+ * rmoe_matrix_upload_q4k: part RMOE_PART_GATE (rows [0, I) of gate_up) and RMOE_PART_UP
+ * (rows [I, 2I)) take [I, H]; RMOE_PART_DOWN takes [H, I] (I % 256 == 0; the columns up
+ * to Ipad are the zero padding of kernels/moe/pack.py).  Replaces the per-expert
+ * q4nx_components(name, outer_index=e) of quant/gguf_q4k.py:160-186 for the
+ * ffn_{gate,up,down}_exps tensors feeding moe_b1/moe_b2. */
+#define RMOE_PART_GATE 0
+#define RMOE_PART_UP 1
+#define RMOE_PART_DOWN 2
+int rmoe_layer_upload_expert_q4k(rmoe_ctx* ctx, int layer, int expert, int part, const void* q4k_bytes,
+                                 size_t nbytes);
 /* Quantize one expert from fp32 device weights (gate_up [2I, H], down [H, I] row-major;
  * the down input columns past I are zero-padded to Ipad).  Bit-exact quant/q4nx.py:127-200. */
 int rmoe_layer_quantize_expert_dev(rmoe_ctx* ctx, int layer, int expert, const float* gate_up_dev,

@@ -46,12 +46,14 @@ SIGNATURES: dict[str, list] = {
     "rmoe_matrix_shape": [_p, _i, _pi, _pi],
     "rmoe_matrix_upload_bfp16": [_p, _p, _sz, _i, _i, _pi],
     "rmoe_matrix_format": [_p, _i, _pi],
+    "rmoe_matrix_upload_q4k": [_p, _p, _sz, _i, _i, _pi],
     "rmoe_linear": [_p, _i, _p, _i, _i, _p],
     "rmoe_linear_dev": [_p, _i, _p, _i, _p, _p],
     "rmoe_reserve_linear": [_p, _i, _i],
     "rmoe_layer_create": [_p, _i, _i, _i, _i, _i, _i],
     "rmoe_reserve": [_p, _i, _i],
     "rmoe_layer_upload_experts": [_p, _i, _p, _sz, _p, _sz],
+    "rmoe_layer_upload_expert_q4k": [_p, _i, _i, _i, _p, _sz],
     "rmoe_layer_quantize_expert_dev": [_p, _i, _i, _p, _p, _p],
     "rmoe_layer_synthesize_dev": [_p, _i, C.c_uint64, _f, _p],
     "rmoe_layer_download_expert": [_p, _i, _i, _p, _sz, _p, _sz],

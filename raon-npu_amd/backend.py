@@ -98,12 +98,14 @@ class GpuBackend:
         self._cached_inputs.clear()
 
     # ---------------------------------------------------------- registration --
-    _FORMATS = {"q4nx_gemv": "q4nx", "bfp16_gemv": "bfp16"}
+    _FORMATS = {"q4nx_gemv": "q4nx", "bfp16_gemv": "bfp16", "gguf_q4_k": "q4k"}
 
     def register_bundle(self, bundle: str, packed: bytes | np.ndarray, M: int, K: int, fmt: str = "q4nx_gemv") -> None:
-        """Upload one dense bundle: GEMV bytes of an [M, K] matrix in the reference's
-        ``BundleMeta.fmt`` (npu/backend.py:104-117): "q4nx_gemv" (quant/q4nx.py pack_gemv)
-        or "bfp16_gemv" (quant/bfp16.py pack_bfp16_gemv)."""
+        """Upload one dense bundle: an [M, K] matrix in the reference's ``BundleMeta.fmt``
+        (npu/backend.py:104-117): "q4nx_gemv" (quant/q4nx.py pack_gemv) or "bfp16_gemv"
+        (quant/bfp16.py pack_bfp16_gemv); or "gguf_q4_k", a row-major llama.cpp Q4_K tensor
+        that the device converts to q4nx (quant/gguf_q4k.py:160-186, 228-233), for a
+        projection exported straight from the GGUF (e.g. dense_gu or an lm_head)."""
         if fmt not in self._FORMATS:
             raise ValueError(f"Unknown bundle format for {bundle}: {fmt!r}")
         self._bundles[bundle] = self.ctx.upload_matrix(packed, M, K, fmt=self._FORMATS[fmt])
@@ -121,6 +123,31 @@ class GpuBackend:
         """Upload one layer's expert bundles (kernels/moe/pack.py geometry) and optional router."""
         lyr = self.ctx.create_layer(layer, geom)
         lyr.upload_experts(gate_up, down)
+        if router_weight is not None:
+            lyr.set_router(router_weight, router_bias, score, renormalize, scaling)
+        self._layers[int(layer)] = lyr
+        return lyr
+
+    def register_moe_layer_q4k(self, layer: int, geom: MoeGeometry, gate_exps, up_exps, down_exps,
+                               router_weight: np.ndarray | None = None, router_bias: np.ndarray | None = None,
+                               score: str = "softmax", renormalize: bool = True, scaling: float = 1.0) -> MoeLayer:
+        """A layer's experts straight from GGUF Q4_K tensors (``ffn_gate_exps``, ``ffn_up_exps``
+        [E, I, H] and ``ffn_down_exps`` [E, H, I], each the row-major bytes of all E experts
+        back to back, E = n_routed + n_shared); the device converts every expert part to q4nx
+        (quant/gguf_q4k.py:160-186, 228-233).  Requires H % 256 == 0 and I % 256 == 0."""
+        g = geom
+        lyr = self.ctx.create_layer(layer, g)
+        parts = {"gate": (gate_exps, g.inter, g.hidden), "up": (up_exps, g.inter, g.hidden),
+                 "down": (down_exps, g.hidden, g.inter)}
+        for part, (raw, M, K) in parts.items():
+            buf = (np.frombuffer(raw, np.uint8) if isinstance(raw, (bytes, bytearray))
+                   else np.ascontiguousarray(raw, np.uint8).reshape(-1))
+            per = M * (K // 256) * 144
+            if K % 256 or buf.size != per * g.n_experts:
+                raise ValueError(f"{part}_exps: expected {g.n_experts} Q4_K experts of [{M}, {K}] "
+                                 f"({per * g.n_experts} bytes), got {buf.size} bytes")
+            for e in range(g.n_experts):
+                lyr.upload_expert_q4k(e, part, buf[e * per:(e + 1) * per])
         if router_weight is not None:
             lyr.set_router(router_weight, router_bias, score, renormalize, scaling)
         self._layers[int(layer)] = lyr

@@ -100,6 +100,57 @@ __global__ void relayout_out_kernel(const uint8_t* __restrict__ tiles, uint8_t* 
   }
 }
 
+// ------------------------------------------------------------ Q4_K -> tiles --
+// llama.cpp block_q4_K (quant/gguf_q4k.py:189-233): 144 bytes per 256 weights of a row --
+// d (fp16), dmin (fp16), eight 6-bit scales and mins in 12 bytes, 128 code bytes (sub-
+// block 2p = low nibbles of bytes 32p..32p+31, 2p+1 = their high nibbles).  q4nx keeps
+// every code; group j's parameters are RTNE bf16 of d*sc[j] and -dmin*mn[j] (exact fp32
+// products).  Thread = (tile row band, K tile, group j, lane): row row0 + 64*band + lane,
+// group 4*kt + j of a tile matrix Kt wide; groups at or past K are the zero padding
+// (codes 0, scale 0, min 0).
+__global__ void q4k_to_tiles_kernel(const uint8_t* __restrict__ q4k, int M, int K, uint8_t* __restrict__ tiles,
+                                    int Kt, int row0) {
+  const int nkt = Kt / 128;
+  const size_t n = (size_t)M * (Kt / 32);
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n) return;
+  const int lane = (int)(idx & 63);
+  const size_t rest = idx >> 6;
+  const int j = (int)(rest & 3);
+  const size_t rest2 = rest >> 2;
+  const int kt = (int)(rest2 % nkt), band = (int)(rest2 / nkt);
+  const int r = 64 * band + lane, g = 4 * kt + j;
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+  uint32_t sm = 0u;
+  if (32 * g < K) {
+    const uint8_t* b = q4k + ((size_t)r * (K / 256) + g / 8) * 144;
+    const int jj = g % 8;
+    const uint16_t dh = (uint16_t)(b[0] | (b[1] << 8)), mh = (uint16_t)(b[2] | (b[3] << 8));
+    const float d = (float)__builtin_bit_cast(_Float16, dh), dmin = (float)__builtin_bit_cast(_Float16, mh);
+    uint32_t sc, mn;
+    if (jj < 4) {
+      sc = b[4 + jj] & 0x3Fu;
+      mn = b[8 + jj] & 0x3Fu;
+    } else {
+      sc = (b[12 + jj - 4] & 0x0Fu) | ((uint32_t)(b[4 + jj - 4] >> 6) << 4);
+      mn = (uint32_t)(b[12 + jj - 4] >> 4) | ((uint32_t)(b[8 + jj - 4] >> 6) << 4);
+    }
+    sm = f32_to_bf16(__fmul_rn(d, (float)sc)) | (f32_to_bf16(__fmul_rn(-dmin, (float)mn)) << 16);
+    const uint8_t* cb = b + 16 + 32 * (jj / 2);
+    const int shift = (jj & 1) ? 4 : 0;
+#pragma unroll 8
+    for (int c = 0; c < 32; ++c) {
+      const uint32_t code = ((uint32_t)cb[c] >> shift) & 15u;
+      const int ni = tile_nibble_index(c);
+      w[ni >> 3] |= code << (4 * (ni & 7));
+    }
+  }
+  const int R = row0 + r;
+  uint8_t* t = tiles + ((size_t)(R / 64) * nkt + kt) * kTileBytes;
+  *reinterpret_cast<uint4*>(t + j * 1024 + (R % 64) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+  *reinterpret_cast<uint32_t*>(t + kCodeBytes + (R % 64) * 16 + j * 4) = sm;
+}
+
 // ------------------------------------------------------------------ quantizer --
 // Bit-exact restatement of quant/q4nx.py:127-200 per (row, group), in float64 where
 // the reference uses float64.
@@ -235,6 +286,14 @@ hipError_t launch_relayout_in(const uint8_t* packed, uint8_t* tiles, int M, int 
   const size_t n = (size_t)M * (K / 32);
   const unsigned blocks = (unsigned)((n + 255) / 256);
   hipLaunchKernelGGL(relayout_in_kernel, dim3(blocks), dim3(256), 0, st, packed, tiles, M, K);
+  return hipGetLastError();
+}
+
+hipError_t launch_q4k_to_tiles(const uint8_t* q4k, int M, int K, uint8_t* tiles, int Kt, int row0, hipStream_t st) {
+  if (M % 64 || row0 % 64 || K % 256 || Kt % 128 || K > Kt) return hipErrorInvalidValue;
+  const size_t n = (size_t)M * (Kt / 32);
+  const unsigned blocks = (unsigned)((n + 255) / 256);
+  hipLaunchKernelGGL(q4k_to_tiles_kernel, dim3(blocks), dim3(256), 0, st, q4k, M, K, tiles, Kt, row0);
   return hipGetLastError();
 }
 

@@ -285,6 +285,29 @@ int rmoe_matrix_upload(rmoe_ctx* ctx, const void* bytes, size_t nbytes, int M, i
   return RMOE_OK;
 }
 
+int rmoe_matrix_upload_q4k(rmoe_ctx* ctx, const void* bytes, size_t nbytes, int M, int K, int* handle) {
+  if (!ctx || !bytes || !handle) return fail(RMOE_EINVAL, "null argument");
+  TRY(check_mk(M, K));
+  const size_t need = (size_t)M * (K / 256) * 144, tb = rmoe::matrix_bytes(M, K);
+  if (nbytes != need) return fail(RMOE_EINVAL, "Q4_K tensor has %zu bytes, expected %zu for [%d, %d]", nbytes, need, M, K);
+  HIP_TRY(hipSetDevice(ctx->device));
+  RmoeMatrix m;
+  m.M = M;
+  m.K = K;
+  if (hipMalloc((void**)&m.tiles, tb) != hipSuccess) return fail(RMOE_ENOMEM, "hipMalloc of %zu bytes failed", tb);
+  int r = grow(ctx->s.staging, ctx->s.staging_bytes, need, ctx);
+  if (r != RMOE_OK) {
+    hipFree(m.tiles);
+    return r;
+  }
+  HIP_TRY(hipMemcpyAsync(ctx->s.staging, bytes, need, hipMemcpyHostToDevice, ctx->stream));
+  HIP_TRY(rmoe::launch_q4k_to_tiles(ctx->s.staging, M, K, m.tiles, K, 0, ctx->stream));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  *handle = ctx->next_handle++;
+  ctx->mats[*handle] = m;
+  return RMOE_OK;
+}
+
 int rmoe_matrix_upload_bfp16(rmoe_ctx* ctx, const void* bytes, size_t nbytes, int M, int K, int* handle) {
   if (!ctx || !bytes || !handle) return fail(RMOE_EINVAL, "null argument");
   TRY(check_mk(M, K));
@@ -514,6 +537,33 @@ int rmoe_layer_upload_experts(rmoe_ctx* ctx, int layer, const void* gate_up, siz
     // The staging buffer is reused by the next expert: wait for the re-layout.
     HIP_TRY(hipStreamSynchronize(ctx->stream));
   }
+  return RMOE_OK;
+}
+
+int rmoe_layer_upload_expert_q4k(rmoe_ctx* ctx, int layer, int expert, int part, const void* bytes, size_t nbytes) {
+  RmoeLayer* L;
+  TRY(check_layer(ctx, layer, &L));
+  if (expert < 0 || expert >= L->n_routed + L->n_shared) return fail(RMOE_EINVAL, "expert %d out of range", expert);
+  if (!bytes) return fail(RMOE_EINVAL, "null Q4_K tensor");
+  int M, K, Kt, row0;
+  uint8_t* dst;
+  if (part == RMOE_PART_GATE || part == RMOE_PART_UP) {
+    M = L->I, K = L->H, Kt = L->H, row0 = part == RMOE_PART_UP ? L->I : 0;
+    dst = L->gu + (size_t)expert * L->gu_bytes;
+  } else if (part == RMOE_PART_DOWN) {
+    M = L->H, K = L->I, Kt = L->Ipad, row0 = 0;
+    dst = L->dn + (size_t)expert * L->dn_bytes;
+  } else {
+    return fail(RMOE_EINVAL, "part %d is not RMOE_PART_GATE, _UP or _DOWN", part);
+  }
+  if (K % 256) return fail(RMOE_EINVAL, "Q4_K rows must be a multiple of 256 wide, got %d", K);
+  const size_t need = (size_t)M * (K / 256) * 144;
+  if (nbytes != need) return fail(RMOE_EINVAL, "Q4_K tensor has %zu bytes, expected %zu for [%d, %d]", nbytes, need, M, K);
+  HIP_TRY(hipSetDevice(ctx->device));
+  TRY(grow(ctx->s.staging, ctx->s.staging_bytes, need, ctx));
+  HIP_TRY(hipMemcpyAsync(ctx->s.staging, bytes, need, hipMemcpyHostToDevice, ctx->stream));
+  HIP_TRY(rmoe::launch_q4k_to_tiles(ctx->s.staging, M, K, dst, Kt, row0, ctx->stream));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
   return RMOE_OK;
 }
 

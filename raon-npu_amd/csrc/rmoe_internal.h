@@ -246,6 +246,8 @@ namespace rmoe {
 
 hipError_t launch_relayout_in(const uint8_t* packed, uint8_t* tiles, int M, int K, hipStream_t st);
 hipError_t launch_relayout_out(const uint8_t* tiles, uint8_t* packed, int M, int K, hipStream_t st);
+// Rows [row0, row0 + M) of a tile matrix Kt wide from a row-major Q4_K tensor [M, K].
+hipError_t launch_q4k_to_tiles(const uint8_t* q4k, int M, int K, uint8_t* tiles, int Kt, int row0, hipStream_t st);
 hipError_t launch_quantize(const float* w, int M, int K, int ld, int k_valid, uint8_t* tiles, int* err,
                            hipStream_t st);
 hipError_t launch_synth_quantize(uint64_t seed, float std, int M, int K, int k_valid, uint8_t* tiles, int* err,

@@ -86,16 +86,21 @@ class Context:
 
     # ------------------------------------------------------------ matrices --
     def upload_matrix(self, packed: bytes | np.ndarray, M: int, K: int, fmt: str = "q4nx") -> "Matrix":
-        """Upload GEMV bytes of an [M, K] matrix: ``fmt`` "q4nx" (quant/q4nx.py pack_gemv)
-        or "bfp16" (quant/bfp16.py pack_bfp16_gemv, 9 bits per weight)."""
-        buf = np.frombuffer(packed, dtype=np.uint8) if isinstance(packed, (bytes, bytearray)) else np.ascontiguousarray(packed, dtype=np.uint8)
+        """Upload an [M, K] matrix: ``fmt`` "q4nx" (quant/q4nx.py pack_gemv bytes), "bfp16"
+        (quant/bfp16.py pack_bfp16_gemv, 9 bits per weight) or "q4k" (a row-major llama.cpp
+        Q4_K tensor, converted to q4nx on the device as quant/gguf_q4k.py:228-233 does)."""
+        buf = (np.frombuffer(packed, dtype=np.uint8) if isinstance(packed, (bytes, bytearray))
+               else np.ascontiguousarray(packed, dtype=np.uint8).reshape(-1))
         h = C.c_int()
         if fmt == "q4nx":
             call("rmoe_matrix_upload", self._h, ptr(buf), buf.size, int(M), int(K), C.byref(h))
         elif fmt == "bfp16":
             call("rmoe_matrix_upload_bfp16", self._h, ptr(buf), buf.size, int(M), int(K), C.byref(h))
+        elif fmt == "q4k":
+            call("rmoe_matrix_upload_q4k", self._h, ptr(buf), buf.size, int(M), int(K), C.byref(h))
+            fmt = "q4nx"
         else:
-            raise ValueError(f"unknown matrix format {fmt!r} (expected 'q4nx' or 'bfp16')")
+            raise ValueError(f"unknown matrix format {fmt!r} (expected 'q4nx', 'bfp16' or 'q4k')")
         return Matrix(self, h.value, M, K, fmt)
 
     def quantize_matrix(self, w_dev, M: int, K: int, stream=None) -> "Matrix":
@@ -209,6 +214,19 @@ class MoeLayer:
         gu = np.frombuffer(gate_up, np.uint8) if isinstance(gate_up, (bytes, bytearray)) else np.ascontiguousarray(gate_up, np.uint8)
         dn = np.frombuffer(down, np.uint8) if isinstance(down, (bytes, bytearray)) else np.ascontiguousarray(down, np.uint8)
         call("rmoe_layer_upload_experts", self.ctx.handle, self.layer, ptr(gu), gu.size, ptr(dn), dn.size)
+
+    _Q4K_PARTS = {"gate": 0, "up": 1, "down": 2}
+
+    def upload_expert_q4k(self, expert: int, part: str, q4k: bytes | np.ndarray):
+        """One part ("gate" [I, H], "up" [I, H] or "down" [H, I]) of an expert from a row-major
+        llama.cpp Q4_K tensor, converted to q4nx on the device (quant/gguf_q4k.py:160-186,
+        228-233: ``q4nx_components(name, outer_index=expert)`` of ffn_{gate,up,down}_exps)."""
+        if part not in self._Q4K_PARTS:
+            raise ValueError(f"part must be one of {sorted(self._Q4K_PARTS)}, got {part!r}")
+        buf = (np.frombuffer(q4k, np.uint8) if isinstance(q4k, (bytes, bytearray))
+               else np.ascontiguousarray(q4k, np.uint8).reshape(-1))
+        call("rmoe_layer_upload_expert_q4k", self.ctx.handle, self.layer, int(expert), self._Q4K_PARTS[part], ptr(buf),
+             buf.size)
 
     def quantize_expert(self, expert: int, gate_up_dev, down_dev, stream=None):
         g = self.geom
