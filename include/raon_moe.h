@@ -144,7 +144,30 @@ int rmoe_layer_quantize_expert_dev(rmoe_ctx* ctx, int layer, int expert, const f
  * same bit-exact q4nx quantizer.  For benchmarks at full depth; synchronous.  No
  * reference counterpart (the reference quantizes host arrays, quant/q4nx.py:127-200). */
 int rmoe_layer_synthesize_dev(rmoe_ctx* ctx, int layer, uint64_t seed, float std, void* stream);
-/* Read one expert back as pack_gemv bytes (round trips, oracle cross-checks). */
+/* A MoE layer in the reference's weights-d layout (npu/backend.py:624-700), the format the
+ * released model ships in:
+ *   moe_b1  "q4nx_gemv_bundle": n_routed experts of [2I, H] (gate rows, then up rows),
+ *           expert_bytes = 2I*H*5/8 (3,481,600 B for H=2560, I=1088);
+ *   moe_b2  "bfp16_gemv_bundle": n_routed + 1 experts of [H, Ipad] bfp16ebs8, the last one
+ *           the shared expert's down projection (component fmt "shared_down", expert_id
+ *           128), expert_bytes = H*Ipad*9/8 (3,686,400 B).
+ * The shared expert's gate/up (shared_gu, a dense "bfp16_gemv" matrix) stays outside the
+ * layer, as in the reference: serve it with rmoe_matrix_upload_bfp16 + rmoe_linear.
+ * Such a layer serves rmoe_route, rmoe_moe_experts (routed experts: q4nx gate/up, bfp16
+ * down, ordered combine) and rmoe_moe_experts_grouped (routed sums + shared down from
+ * shared_gu); the entry points that compute the shared gate/up inside the layer (decode,
+ * decode stack, prefill_dev) reject it with RMOE_EINVAL. */
+int rmoe_layer_create_d(rmoe_ctx* ctx, int layer, int hidden, int inter, int n_routed, int top_k);
+/* Experts [expert0, expert0 + n) of one bundle of a weights-d layer: bytes are n
+ * consecutive expert slices of moe_b1.bin (RMOE_BUNDLE_B1, offset expert*expert_bytes) or
+ * moe_b2.bin (RMOE_BUNDLE_B2), as DWeights._read_expert_slice (npu/backend.py:1006-1034)
+ * reads them; re-laid out on the device.  Lets a loader stream a bundle file in pieces. */
+#define RMOE_BUNDLE_B1 1
+#define RMOE_BUNDLE_B2 2
+int rmoe_layer_upload_d(rmoe_ctx* ctx, int layer, int bundle, int expert0, int n, const void* bytes, size_t nbytes);
+/* Read one expert back in its bundle's GEMV bytes (round trips, oracle cross-checks).
+ * For a weights-d layer down is bfp16 (H*Ipad*9/8 bytes) and the shared expert
+ * (expert n_routed) has no gate/up: pass gate_up = NULL, gu_nbytes = 0. */
 int rmoe_layer_download_expert(rmoe_ctx* ctx, int layer, int expert, void* gate_up, size_t gu_nbytes,
                                void* down, size_t dn_nbytes);
 /* Router of the layer (host/raon.py:1224-1247): weight bf16 [n_routed, H]; bias fp32

@@ -179,6 +179,62 @@ class ExpertBank:
             self._cache.popitem(last=False)
         return out
 
+    def down_proj(self, e: int) -> np.ndarray:
+        """``[H, I]`` fp32 down projection of expert ``e``."""
+        return self.expert(e)[2]
+
+
+class DExpertBank:
+    """Experts of one layer in the weights-d bundles, served as fp32 the way ``DWeights``
+    does (``npu/backend.py:1246-1273``, ``:1228-1239``).
+
+    ``moe_b1`` holds ``n_routed`` q4nx experts ``[2I, H]`` back to back; ``moe_b2`` holds
+    ``n_routed + 1`` bfp16 experts ``[H, Ipad]`` whose last one is the shared expert's down
+    projection (``npu/backend.py:624-700``); ``shared_gu`` is the shared expert's bfp16
+    ``[2I, H]`` gate/up matrix (or None).  bfp16 weights decode as ``m * 2**(e - 133)``
+    (``parse_bfp16_gemv``, quant/bfp16.py:412-440).  Duck-types ``ExpertBank`` for the
+    functions below, the shared expert being expert ``n_routed``.
+    """
+
+    def __init__(self, moe_b1, moe_b2, n_routed: int, hidden: int, inter: int, shared_gu=None, cache: int = 32):
+        from . import bfp16 as _b16
+
+        self._b16 = _b16
+        self.moe_b1 = np.frombuffer(moe_b1, np.uint8) if isinstance(moe_b1, (bytes, bytearray)) else np.asarray(moe_b1, np.uint8).reshape(-1)
+        self.moe_b2 = np.frombuffer(moe_b2, np.uint8) if isinstance(moe_b2, (bytes, bytearray)) else np.asarray(moe_b2, np.uint8).reshape(-1)
+        self.n_routed, self.hidden, self.inter = n_routed, hidden, inter
+        self.inter_pad = -(-inter // 256) * 256
+        self.gu_bytes = 2 * inter * hidden * 5 // 8
+        self.dn_bytes = hidden * self.inter_pad * 9 // 8
+        if self.moe_b1.size != n_routed * self.gu_bytes or self.moe_b2.size != (n_routed + 1) * self.dn_bytes:
+            raise ValueError("bundle sizes do not match the weights-d expert geometry")
+        self.shared_gu = None if shared_gu is None else _b16.parse_gemv(shared_gu, K=hidden, M=2 * inter)
+        self._cache: OrderedDict[int, tuple[np.ndarray, np.ndarray, np.ndarray]] = OrderedDict()
+        self._cap = max(1, cache)
+
+    def down_proj(self, e: int) -> np.ndarray:
+        """``[H, I]`` fp32 down projection of expert ``e`` (``n_routed`` = shared)."""
+        dn = self.moe_b2[e * self.dn_bytes : (e + 1) * self.dn_bytes]
+        return np.ascontiguousarray(self._b16.parse_gemv(dn, K=self.inter_pad, M=self.hidden)[:, : self.inter])
+
+    def expert(self, e: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+        hit = self._cache.get(e)
+        if hit is not None:
+            self._cache.move_to_end(e)
+            return hit
+        if e == self.n_routed:
+            if self.shared_gu is None:
+                raise ValueError("the shared expert's gate/up (shared_gu) was not given")
+            w = self.shared_gu
+        else:
+            gu = self.moe_b1[e * self.gu_bytes : (e + 1) * self.gu_bytes]
+            w = dequantize_simple(*parse_gemv(gu, K=self.hidden, M=2 * self.inter))
+        out = (np.ascontiguousarray(w[: self.inter]), np.ascontiguousarray(w[self.inter :]), self.down_proj(e))
+        self._cache[e] = out
+        while len(self._cache) > self._cap:
+            self._cache.popitem(last=False)
+        return out
+
 
 def expert_chain(bank: ExpertBank, e: int, x_u16: np.ndarray, gate_beta, value_beta) -> np.ndarray:
     """gate, up, activation -> RTNE, down for one expert: bf16 ``[H]`` out."""
@@ -243,7 +299,7 @@ def moe_experts_grouped(bank: ExpertBank, x_u16, top_ids, top_weights, shared_gu
     shared down rows are ``down(RTNE(act(shared_gu)))`` of the shared expert.
     """
     inter = bank.inter
-    _, _, d = bank.expert(shared_id)
+    d = bank.down_proj(shared_id)
     routed = np.stack([moe_experts(bank, x_u16[t], top_ids[t], top_weights[t], gate_beta, value_beta)
                        for t in range(x_u16.shape[0])])
     act = f32_to_bf16(glu(shared_gu[:, :inter], shared_gu[:, inter:], gate_beta, value_beta))
@@ -276,7 +332,7 @@ def moe_experts_grouped_batched(bank: ExpertBank, x_u16, top_ids, top_weights, s
         for r in np.argsort(top_ids[t], kind="stable"):
             acc += bf16_to_f32(down_rows[t, r]) * float(top_weights[t, r])
         routed[t] = f32_to_bf16(acc)
-    _, _, d = bank.expert(shared_id)
+    d = bank.down_proj(shared_id)
     act = f32_to_bf16(glu(shared_gu[:, :inter], shared_gu[:, inter:], gate_beta, value_beta))
     shared_down = f32_to_bf16(bf16_to_f32(act) @ d.T)
     return routed, shared_down

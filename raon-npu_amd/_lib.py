@@ -24,6 +24,8 @@ SCORE_SIGMOID = 0
 SCORE_SOFTMAX = 1
 FMT_Q4NX = 0
 FMT_BFP16 = 1
+BUNDLE_B1 = 1
+BUNDLE_B2 = 2
 
 _p = C.c_void_p
 _i = C.c_int
@@ -54,6 +56,8 @@ SIGNATURES: dict[str, list] = {
     "rmoe_reserve": [_p, _i, _i],
     "rmoe_layer_upload_experts": [_p, _i, _p, _sz, _p, _sz],
     "rmoe_layer_upload_expert_q4k": [_p, _i, _i, _i, _p, _sz],
+    "rmoe_layer_create_d": [_p, _i, _i, _i, _i, _i],
+    "rmoe_layer_upload_d": [_p, _i, _i, _i, _i, _p, _sz],
     "rmoe_layer_quantize_expert_dev": [_p, _i, _i, _p, _p, _p],
     "rmoe_layer_synthesize_dev": [_p, _i, C.c_uint64, _f, _p],
     "rmoe_layer_download_expert": [_p, _i, _i, _p, _sz, _p, _sz],

@@ -60,8 +60,12 @@ class GpuBackend:
 
     _TIMING_KEYS = ("linear_gpu", "moe_gpu", "moe_grouped_gpu", "moe_host", "route_gpu")
 
-    def __init__(self, device: int = 0, *, activation: str | None = None):
-        self.ctx = Context(device)
+    def __init__(self, device: int = 0, *, activation: str | None = None, weights_dir=None, manifest_path=None,
+                 layers=None, top_k: int = 6, context: Context | None = None):
+        """``weights_dir``/``manifest_path`` load a weights-d directory as the NpuBackend
+        constructor does (npu/backend.py:2404-2412); ``context`` shares an existing device
+        context instead of creating one on ``device``."""
+        self.ctx = context if context is not None else Context(device)
         self.activation = activation  # "swiglu" forces SwiGLU; None follows the betas
         self._bundles: dict[str, Matrix] = {}
         self._components: dict[str, _Component] = {}
@@ -74,6 +78,8 @@ class GpuBackend:
         self.timings: dict[str, float] = {}
         self.call_counts: dict[str, int] = defaultdict(int)
         self.reset_timings()
+        if weights_dir is not None:
+            self.load_weights_d(weights_dir, manifest_path, layers=layers, top_k=top_k)
 
     # ----------------------------------------------------------- bookkeeping --
     def reset_timings(self) -> None:
@@ -152,6 +158,50 @@ class GpuBackend:
             lyr.set_router(router_weight, router_bias, score, renormalize, scaling)
         self._layers[int(layer)] = lyr
         return lyr
+
+    def register_moe_layer_d(self, layer: int, geom: MoeGeometry, moe_b1: bytes | np.ndarray, moe_b2: bytes | np.ndarray,
+                             shared_gu: bytes | np.ndarray | None = None, router_weight: np.ndarray | None = None,
+                             router_bias: np.ndarray | None = None, score: str = "sigmoid", renormalize: bool = True,
+                             scaling: float = 1.0) -> MoeLayer:
+        """A layer from in-memory weights-d bundles (npu/backend.py:624-700): ``moe_b1``
+        (q4nx_gemv_bundle, ``n_routed`` experts ``[2I, H]``), ``moe_b2`` (bfp16_gemv_bundle,
+        ``n_routed + 1`` experts ``[H, Ipad]``, the last the shared down) and optionally
+        ``shared_gu`` (bfp16 ``[2I, H]``).  The shared expert's gate/up/down are registered as
+        the components ``model.layers.{layer}.moe.shared_experts.{gate,up,down}_proj.weight``,
+        served by ``linear`` as ``RaonModel._moe_token`` calls them (host/raon.py:1314-1324)."""
+        g = geom
+        lyr = self.ctx.create_layer_d(layer, g)
+        try:
+            b1 = np.frombuffer(moe_b1, np.uint8) if isinstance(moe_b1, (bytes, bytearray)) else np.ascontiguousarray(moe_b1, np.uint8).reshape(-1)
+            b2 = np.frombuffer(moe_b2, np.uint8) if isinstance(moe_b2, (bytes, bytearray)) else np.ascontiguousarray(moe_b2, np.uint8).reshape(-1)
+            if b1.size != g.n_routed * lyr.gu_expert_bytes:
+                raise ValueError(f"moe_b1 has {b1.size} bytes, expected {g.n_routed} x {lyr.gu_expert_bytes}")
+            if b2.size != (g.n_routed + 1) * lyr.dn_expert_bytes:
+                raise ValueError(f"moe_b2 has {b2.size} bytes, expected {g.n_routed + 1} x {lyr.dn_expert_bytes}")
+            lyr.upload_d(1, 0, b1)
+            lyr.upload_d(2, 0, b2)
+        except BaseException:
+            lyr.free()
+            raise
+        if router_weight is not None:
+            lyr.set_router(router_weight, router_bias, score, renormalize, scaling)
+        self._layers[int(layer)] = lyr
+        pfx, d = f"model.layers.{int(layer)}.moe.shared_experts", f"L{int(layer):02d}"
+        if shared_gu is not None:
+            self.register_bundle(f"{d}/shared_gu", shared_gu, 2 * g.inter, g.hidden, fmt="bfp16_gemv")
+            self.register_component(f"{pfx}.gate_proj.weight", f"{d}/shared_gu", 0, g.inter)
+            self.register_component(f"{pfx}.up_proj.weight", f"{d}/shared_gu", g.inter, 2 * g.inter)
+        per = lyr.dn_expert_bytes
+        self.register_bundle(f"{d}/shared_down", b2[g.n_routed * per:], g.hidden, g.inter_pad, fmt="bfp16_gemv")
+        self.register_component(f"{pfx}.down_proj.weight", f"{d}/shared_down", 0, g.hidden, orig_k=g.inter)
+        return lyr
+
+    def load_weights_d(self, weights_dir, manifest_path=None, **kw) -> dict:
+        """Validate a weights-d directory's manifest (npu/backend.py:729-929) and load its MoE
+        path bundles; see ``weights_d.load_weights_d``."""
+        from .weights_d import load_weights_d
+
+        return load_weights_d(self, weights_dir, manifest_path, **kw)
 
     def layer(self, layer: int) -> MoeLayer:
         try:

@@ -28,7 +28,6 @@
 namespace rmoe {
 namespace {
 
-constexpr int kMantBytes = 8192;
 constexpr int kRefHalfBytes = 4608;
 constexpr int kRefGroupBytes = 144;
 
@@ -70,7 +69,7 @@ __global__ __launch_bounds__(256) void b16_relayout_in_kernel(const uint8_t* __r
     const uint32_t b = src[ref_group(R, kt * kTileCols + 8 * g, kb_n) + r16];
     e[g >> 2] |= b << (8 * (g & 3));
   }
-  *reinterpret_cast<uint4*>(dst + kMantBytes) = make_uint4(e[0], e[1], e[2], e[3]);
+  *reinterpret_cast<uint4*>(dst + kB16MantBytes) = make_uint4(e[0], e[1], e[2], e[3]);
 }
 
 // The inverse: every reference byte is written exactly once.
@@ -94,7 +93,7 @@ __global__ __launch_bounds__(256) void b16_relayout_out_kernel(const uint8_t* __
       dst[ref_group(R, C, kb_n) + 16 + (C & 7) * 16 + r16] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
     }
   }
-  const uint4 v = *reinterpret_cast<const uint4*>(src + kMantBytes);
+  const uint4 v = *reinterpret_cast<const uint4*>(src + kB16MantBytes);
   const uint32_t e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
   for (int g = 0; g < 16; ++g)
@@ -116,21 +115,6 @@ struct B16Args {
   unsigned* counters;
   int ksplit;
 };
-
-// bf16 pair (lo, hi) of two fp32 values whose low 16 bits are zero.
-__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
-  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
-}
-
-// The 4 mantissas of a dword -> two exact bf16 pairs (columns (4d, 4d+1), (4d+2, 4d+3)).
-// (float)(int8_t) compiles to one sign-extending SDWA convert per byte.
-__device__ __forceinline__ void mant_pairs(uint32_t w, uint32_t& p0, uint32_t& p1) {
-  p0 = bf16_pair((float)(int8_t)w, (float)(int8_t)(w >> 8));
-  p1 = bf16_pair((float)(int8_t)(w >> 16), (float)((int32_t)w >> 24));
-}
-
-// Kernel scale of an exponent byte: 2^(max(e, 7) - 133), built as fp32 bits.
-__device__ __forceinline__ float exp_scale(uint32_t e) { return __uint_as_float((max(e, 7u) - 6u) << 23); }
 
 __global__ __launch_bounds__(256) void linear_bfp16_kernel(B16Args a) {
   // Dynamic LDS: x of the K range as bf16 pairs [kNT][per * 64] (128 columns per tile),
@@ -167,7 +151,7 @@ __global__ __launch_bounds__(256) void linear_bfp16_kernel(B16Args a) {
     uint4 mc[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) mc[c] = load_stream16(tile + c * 1024);
-    const uint4 eq = load_stream16(tile + kMantBytes);
+    const uint4 eq = load_stream16(tile + kB16MantBytes);
     const uint32_t ew[4] = {eq.x, eq.y, eq.z, eq.w};
 #pragma unroll
     for (int c = 0; c < 8; ++c) {

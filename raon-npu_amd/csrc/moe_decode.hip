@@ -13,6 +13,7 @@
 // Kernel A streams gate+up of all slots (one launch) and applies the activation in the
 // last workgroup of each (slot, 64-unit) band; kernel B streams down of all slots and
 // the last workgroup of each 64-row output band performs the ordered combine.
+#include "../../include/raon_moe.h"
 #include "rmoe_internal.h"
 
 namespace rmoe {
@@ -265,10 +266,16 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeArgs a) {
   if (wave == 0) {
     const float gb = bf16_round(g), ub = bf16_round(u);
     a.h[(size_t)s * a.Ipad + j * 64 + lane] = (uint16_t)f32_to_bf16(act_apply(a.act, gb, ub, a.gb, a.vb));
+    // The down input's padding columns [I, Ipad) are zero: the scratch is shared with
+    // other layers and launches, and padded weights need not be zero (bfp16 moe_b2).
+    if (j == nj - 1)
+      for (int c = a.I + lane; c < a.Ipad; c += 64) a.h[(size_t)s * a.Ipad + c] = 0;
   }
 }
 
-// grid slots*(H/64)*ks2, block 64*waves.
+// grid slots*(H/64)*ks2, block 64*waves.  kFmt: format of the down weights (q4nx, or
+// bfp16 for a weights-d layer whose moe_b2 holds bfp16ebs8 experts).
+template <int kFmt>
 __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
   __shared__ uint32_t xs[kMaxRange * 64];
   __shared__ float ssum[kMaxRange * 4];
@@ -290,8 +297,13 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
 
   float acc = 0.f;
   for (int it = wave; it < nrange; it += nwaves) {
-    const uint8_t* tile = W + ((size_t)rt * nkt + kt0 + it) * kTileBytes;
-    acc = tile_accumulate(tile, lane, xs + it * 64, ssum + it * 4, acc);
+    if constexpr (kFmt == RMOE_FMT_BFP16) {
+      const uint8_t* tile = W + ((size_t)rt * nkt + kt0 + it) * kB16TileBytes;
+      acc = b16_tile_accumulate(tile, lane, xs + it * 64, acc);
+    } else {
+      const uint8_t* tile = W + ((size_t)rt * nkt + kt0 + it) * kTileBytes;
+      acc = tile_accumulate(tile, lane, xs + it * 64, ssum + it * 4, acc);
+    }
   }
   red[wave][lane] = acc;
   __syncthreads();
@@ -341,7 +353,29 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
   }
 }
 
+// One thread per element of h[T, Ipad].
+__global__ __launch_bounds__(256) void act_rows_kernel(const uint16_t* __restrict__ gu, int T, int I, int Ipad, int act,
+                                                       float gb, float vb, uint16_t* __restrict__ h) {
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (size_t)T * Ipad) return;
+  const int t = (int)(idx / Ipad), c = (int)(idx % Ipad);
+  uint32_t v = 0u;
+  if (c < I) {
+    const uint16_t* row = gu + (size_t)t * 2 * I;
+    v = f32_to_bf16(act_apply(act, bf16_to_f32(row[c]), bf16_to_f32(row[I + c]), gb, vb));
+  }
+  h[idx] = (uint16_t)v;
+}
+
 }  // namespace
+
+hipError_t launch_act_rows(const uint16_t* gu, int T, int I, int Ipad, int act, float gb, float vb, uint16_t* h,
+                           hipStream_t st) {
+  const size_t n = (size_t)T * Ipad;
+  hipLaunchKernelGGL(act_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gu, T, I, Ipad, act, gb,
+                     vb, h);
+  return hipGetLastError();
+}
 
 hipError_t launch_route(const RmoeLayer& L, const uint16_t* x, int T, int32_t* ids, float* wts, float* logits,
                         RmoeScratch& s, hipStream_t st) {
@@ -382,7 +416,8 @@ hipError_t launch_moe_decode(const RmoeLayer& L, const uint16_t* x, const int32_
   int ks1, ks2;
   decode_splits(L, ks1, ks2);
   const int slots = k + (with_shared ? 1 : 0);
-  if (with_shared && L.n_shared < 1) return hipErrorInvalidValue;
+  // A weights-d layer keeps the shared gate/up outside the layer: routed slots only.
+  if (with_shared && (L.n_shared < 1 || L.d_layout)) return hipErrorInvalidValue;
   const size_t nf = (size_t)slots * (L.I / 64) * ks1 * 128 + (size_t)slots * (L.H / 64) * ks2 * 64;
   const size_t nc = (size_t)slots * (L.I / 64) + (size_t)slots * (L.H / 64) + (L.H / 64);
   if (nf > s.part_floats || nc > s.n_counters || (size_t)slots * L.Ipad > s.h_elems ||
@@ -426,7 +461,10 @@ hipError_t launch_moe_decode(const RmoeLayer& L, const uint16_t* x, const int32_
     if (e != hipSuccess) return e;
   }
   if (stages & 2) {
-    hipLaunchKernelGGL(decode_down_kernel, dim3(slots * (L.H / 64) * ks2), dim3(64 * w2), 0, st, a);
+    if (L.dn_fmt == RMOE_FMT_BFP16)
+      hipLaunchKernelGGL(decode_down_kernel<RMOE_FMT_BFP16>, dim3(slots * (L.H / 64) * ks2), dim3(64 * w2), 0, st, a);
+    else
+      hipLaunchKernelGGL(decode_down_kernel<RMOE_FMT_Q4NX>, dim3(slots * (L.H / 64) * ks2), dim3(64 * w2), 0, st, a);
     return hipGetLastError();
   }
   return hipSuccess;

@@ -126,8 +126,8 @@ int reserve_layer(rmoe_ctx* ctx, const RmoeLayer& L, int T, int k) {
   TRY(grow(s.inv, oe, (size_t)T * kk, ctx));
   s.order_elems = oe;
   TRY(grow(s.offsets, s.offset_elems, 257, ctx));
-  if (L.n_shared > 0) TRY(grow(s.pf, s.pf_bytes, rmoe::prefill_scratch_bytes(Lk, T), ctx));
-  if (L.n_shared > 0) TRY(reserve_stack(ctx, L, 1));
+  if (L.n_shared > 0 && !L.d_layout) TRY(grow(s.pf, s.pf_bytes, rmoe::prefill_scratch_bytes(Lk, T), ctx));
+  if (L.n_shared > 0 && !L.d_layout) TRY(reserve_stack(ctx, L, 1));
   s.max_tokens = std::max(s.max_tokens, T);
   return RMOE_OK;
 }
@@ -173,6 +173,28 @@ int sync_and_check(rmoe_ctx* ctx, hipStream_t st) {
     }
     return fail(RMOE_EDEVICE, "device error flag 0x%x", err);
   }
+  return RMOE_OK;
+}
+
+// Allocate the expert storage of L and register it as `layer` (replacing nothing:
+// the caller freed any previous layer of that id).
+int place_layer(rmoe_ctx* ctx, int layer, RmoeLayer& L) {
+  if (hipMalloc((void**)&L.gu, (size_t)L.gu_experts * L.gu_bytes) != hipSuccess)
+    return fail(RMOE_ENOMEM, "hipMalloc of expert gate_up failed");
+  if (hipMalloc((void**)&L.dn, (size_t)L.dn_experts * L.dn_bytes) != hipSuccess) {
+    hipFree(L.gu);
+    return fail(RMOE_ENOMEM, "hipMalloc of expert down failed");
+  }
+  ctx->layers[layer] = L;
+  return reserve_layer(ctx, L, 1, L.top_k);
+}
+
+// Entry points that need every expert's gate/up inside the layer (the shared expert
+// included) serve q4nx layers only.
+int require_q4nx_layer(const RmoeLayer& L, int layer, const char* what) {
+  if (L.d_layout)
+    return fail(RMOE_EINVAL, "layer %d holds weights-d bundles (bfp16 down, shared gate/up outside the layer): %s "
+                "serves q4nx layers only", layer, what);
   return RMOE_OK;
 }
 
@@ -486,14 +508,64 @@ int rmoe_layer_create(rmoe_ctx* ctx, int layer, int hidden, int inter, int n_rou
   L.top_k = top_k;
   L.gu_bytes = rmoe::matrix_bytes(2 * inter, hidden);
   L.dn_bytes = rmoe::matrix_bytes(hidden, L.Ipad);
-  const size_t ne = (size_t)n_routed + n_shared;
-  if (hipMalloc((void**)&L.gu, ne * L.gu_bytes) != hipSuccess) return fail(RMOE_ENOMEM, "hipMalloc of expert gate_up failed");
-  if (hipMalloc((void**)&L.dn, ne * L.dn_bytes) != hipSuccess) {
-    hipFree(L.gu);
-    return fail(RMOE_ENOMEM, "hipMalloc of expert down failed");
+  L.gu_experts = L.dn_experts = n_routed + n_shared;
+  return place_layer(ctx, layer, L);
+}
+
+int rmoe_layer_create_d(rmoe_ctx* ctx, int layer, int hidden, int inter, int n_routed, int top_k) {
+  if (!ctx) return fail(RMOE_EINVAL, "null context");
+  if (hidden <= 0 || hidden % 256) return fail(RMOE_EINVAL, "hidden (%d) must be a positive multiple of 256", hidden);
+  if (inter <= 0 || inter % 64) return fail(RMOE_EINVAL, "intermediate size (%d) must be a positive multiple of 64", inter);
+  if (n_routed < 1 || n_routed > 256) return fail(RMOE_EINVAL, "n_routed (%d) must be in 1..256", n_routed);
+  if (top_k < 1 || top_k > 16 || top_k > n_routed) return fail(RMOE_EINVAL, "top_k (%d) must be in 1..min(16, n_routed)", top_k);
+  HIP_TRY(hipSetDevice(ctx->device));
+  rmoe_layer_free(ctx, layer);
+  g_err.clear();
+  RmoeLayer L;
+  L.H = hidden;
+  L.I = inter;
+  L.Ipad = (inter + 255) / 256 * 256;
+  L.n_routed = n_routed;
+  L.n_shared = 1;
+  L.top_k = top_k;
+  L.d_layout = true;
+  L.dn_fmt = RMOE_FMT_BFP16;
+  L.gu_bytes = rmoe::matrix_bytes(2 * inter, hidden);
+  L.dn_bytes = rmoe::matrix_bytes_bfp16(hidden, L.Ipad);
+  L.gu_experts = n_routed;
+  L.dn_experts = n_routed + 1;
+  return place_layer(ctx, layer, L);
+}
+
+int rmoe_layer_upload_d(rmoe_ctx* ctx, int layer, int bundle, int expert0, int n, const void* bytes, size_t nbytes) {
+  RmoeLayer* L;
+  TRY(check_layer(ctx, layer, &L));
+  if (!L->d_layout) return fail(RMOE_EINVAL, "layer %d is not a weights-d layer (rmoe_layer_create_d)", layer);
+  if (bundle != RMOE_BUNDLE_B1 && bundle != RMOE_BUNDLE_B2)
+    return fail(RMOE_EINVAL, "bundle %d is not RMOE_BUNDLE_B1 or RMOE_BUNDLE_B2", bundle);
+  const bool b1 = bundle == RMOE_BUNDLE_B1;
+  const int count = b1 ? L->gu_experts : L->dn_experts;
+  const size_t per = b1 ? L->gu_bytes : L->dn_bytes;
+  if (!bytes || n < 1 || expert0 < 0 || expert0 + n > count)
+    return fail(RMOE_EINVAL, "experts [%d, %d) outside moe_b%d's %d experts", expert0, expert0 + n, bundle, count);
+  if (nbytes != (size_t)n * per)
+    return fail(RMOE_EINVAL, "moe_b%d slice has %zu bytes, expected %zu (%d experts x %zu)", bundle, nbytes,
+                (size_t)n * per, n, per);
+  HIP_TRY(hipSetDevice(ctx->device));
+  TRY(grow(ctx->s.staging, ctx->s.staging_bytes, per, ctx));
+  uint8_t* base = b1 ? L->gu : L->dn;
+  for (int i = 0; i < n; ++i) {
+    const size_t e = (size_t)expert0 + i;
+    HIP_TRY(hipMemcpyAsync(ctx->s.staging, (const uint8_t*)bytes + (size_t)i * per, per, hipMemcpyHostToDevice,
+                           ctx->stream));
+    if (b1)
+      HIP_TRY(rmoe::launch_relayout_in(ctx->s.staging, base + e * per, 2 * L->I, L->H, ctx->stream));
+    else
+      HIP_TRY(rmoe::launch_b16_relayout_in(ctx->s.staging, base + e * per, L->H, L->Ipad, ctx->stream));
+    // The staging buffer is reused by the next expert: wait for the re-layout.
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
   }
-  ctx->layers[layer] = L;
-  return reserve_layer(ctx, L, 1, top_k);
+  return RMOE_OK;
 }
 
 int rmoe_layer_free(rmoe_ctx* ctx, int layer) {
@@ -521,6 +593,7 @@ int rmoe_layer_upload_experts(rmoe_ctx* ctx, int layer, const void* gate_up, siz
                               size_t dn_nbytes) {
   RmoeLayer* L;
   TRY(check_layer(ctx, layer, &L));
+  TRY(require_q4nx_layer(*L, layer, "rmoe_layer_upload_experts"));
   const size_t ne = (size_t)L->n_routed + L->n_shared;
   if (!gate_up || gu_nbytes != ne * L->gu_bytes)
     return fail(RMOE_EINVAL, "gate_up bundle has %zu bytes, expected %zu (%zu experts x %zu)", gu_nbytes, ne * L->gu_bytes, ne, L->gu_bytes);
@@ -543,6 +616,7 @@ int rmoe_layer_upload_experts(rmoe_ctx* ctx, int layer, const void* gate_up, siz
 int rmoe_layer_upload_expert_q4k(rmoe_ctx* ctx, int layer, int expert, int part, const void* bytes, size_t nbytes) {
   RmoeLayer* L;
   TRY(check_layer(ctx, layer, &L));
+  TRY(require_q4nx_layer(*L, layer, "rmoe_layer_upload_expert_q4k"));
   if (expert < 0 || expert >= L->n_routed + L->n_shared) return fail(RMOE_EINVAL, "expert %d out of range", expert);
   if (!bytes) return fail(RMOE_EINVAL, "null Q4_K tensor");
   int M, K, Kt, row0;
@@ -571,6 +645,7 @@ int rmoe_layer_quantize_expert_dev(rmoe_ctx* ctx, int layer, int expert, const f
                                    const float* down_dev, void* stream) {
   RmoeLayer* L;
   TRY(check_layer(ctx, layer, &L));
+  TRY(require_q4nx_layer(*L, layer, "rmoe_layer_quantize_expert_dev"));
   if (expert < 0 || expert >= L->n_routed + L->n_shared) return fail(RMOE_EINVAL, "expert %d out of range", expert);
   if (!gate_up_dev || !down_dev) return fail(RMOE_EINVAL, "null weights");
   HIP_TRY(hipSetDevice(ctx->device));
@@ -585,6 +660,7 @@ int rmoe_layer_quantize_expert_dev(rmoe_ctx* ctx, int layer, int expert, const f
 int rmoe_layer_synthesize_dev(rmoe_ctx* ctx, int layer, uint64_t seed, float std, void* stream) {
   RmoeLayer* L;
   TRY(check_layer(ctx, layer, &L));
+  TRY(require_q4nx_layer(*L, layer, "rmoe_layer_synthesize_dev"));
   if (!(std > 0.f) || !(std < 1e30f)) return fail(RMOE_EINVAL, "std must be positive and finite");
   HIP_TRY(hipSetDevice(ctx->device));
   hipStream_t st = pick_stream(ctx, stream);
@@ -602,15 +678,22 @@ int rmoe_layer_download_expert(rmoe_ctx* ctx, int layer, int expert, void* gate_
                                size_t dn_nbytes) {
   RmoeLayer* L;
   TRY(check_layer(ctx, layer, &L));
-  if (expert < 0 || expert >= L->n_routed + L->n_shared) return fail(RMOE_EINVAL, "expert %d out of range", expert);
-  if (!gate_up || gu_nbytes != L->gu_bytes || !down || dn_nbytes != L->dn_bytes)
-    return fail(RMOE_EINVAL, "download buffers must hold %zu and %zu bytes", L->gu_bytes, L->dn_bytes);
+  if (expert < 0 || expert >= L->dn_experts) return fail(RMOE_EINVAL, "expert %d out of range", expert);
+  // A weights-d layer has no gate/up for its last (shared) expert: gate_up must be null.
+  const bool has_gu = expert < L->gu_experts;
+  if ((has_gu ? (!gate_up || gu_nbytes != L->gu_bytes) : (gate_up != nullptr)) || !down || dn_nbytes != L->dn_bytes)
+    return fail(RMOE_EINVAL, "download buffers must hold %zu and %zu bytes", has_gu ? L->gu_bytes : 0, L->dn_bytes);
   HIP_TRY(hipSetDevice(ctx->device));
   TRY(grow(ctx->s.staging, ctx->s.staging_bytes, std::max(L->gu_bytes, L->dn_bytes), ctx));
-  HIP_TRY(rmoe::launch_relayout_out(L->gu + (size_t)expert * L->gu_bytes, ctx->s.staging, 2 * L->I, L->H, ctx->stream));
-  HIP_TRY(hipMemcpyAsync(gate_up, ctx->s.staging, L->gu_bytes, hipMemcpyDeviceToHost, ctx->stream));
-  HIP_TRY(hipStreamSynchronize(ctx->stream));
-  HIP_TRY(rmoe::launch_relayout_out(L->dn + (size_t)expert * L->dn_bytes, ctx->s.staging, L->H, L->Ipad, ctx->stream));
+  if (has_gu) {
+    HIP_TRY(rmoe::launch_relayout_out(L->gu + (size_t)expert * L->gu_bytes, ctx->s.staging, 2 * L->I, L->H, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(gate_up, ctx->s.staging, L->gu_bytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+  }
+  if (L->dn_fmt == RMOE_FMT_BFP16)
+    HIP_TRY(rmoe::launch_b16_relayout_out(L->dn + (size_t)expert * L->dn_bytes, ctx->s.staging, L->H, L->Ipad, ctx->stream));
+  else
+    HIP_TRY(rmoe::launch_relayout_out(L->dn + (size_t)expert * L->dn_bytes, ctx->s.staging, L->H, L->Ipad, ctx->stream));
   HIP_TRY(hipMemcpyAsync(down, ctx->s.staging, L->dn_bytes, hipMemcpyDeviceToHost, ctx->stream));
   HIP_TRY(hipStreamSynchronize(ctx->stream));
   return RMOE_OK;
@@ -712,6 +795,7 @@ static int stack_layers(rmoe_ctx* ctx, const int* layers, int n_layers, std::vec
     TRY(check_layer(ctx, layers[i], &L));
     if (!L->has_router) return fail(RMOE_EINVAL, "layer %d has no router", layers[i]);
     if (L->n_shared < 1) return fail(RMOE_EINVAL, "layer %d has no shared expert", layers[i]);
+    TRY(require_q4nx_layer(*L, layers[i], "the persistent decode kernel"));
     if (!ptrs.empty()) {
       const RmoeLayer& F = *ptrs[0];
       if (L->H != F.H || L->I != F.I || L->n_routed != F.n_routed || L->top_k != F.top_k || L->score != F.score ||
@@ -785,6 +869,7 @@ int rmoe_moe_decode_stage_dev(rmoe_ctx* ctx, int layer, int stage, const void* x
   TRY(check_layer(ctx, layer, &L));
   if (stage < 0 || stage > 2) return fail(RMOE_EINVAL, "stage must be 0 (router), 1 (gate/up) or 2 (down)");
   if (!L->has_router || L->n_shared < 1) return fail(RMOE_EINVAL, "layer %d needs a router and a shared expert", layer);
+  TRY(require_q4nx_layer(*L, layer, "rmoe_moe_decode_stage_dev"));
   if (!x_dev || (stage == 2 && !out_dev)) return fail(RMOE_EINVAL, "null argument");
   if (act != RMOE_ACT_SITU && act != RMOE_ACT_SWIGLU) return fail(RMOE_EINVAL, "unknown activation %d", act);
   if ((size_t)L->top_k > ctx->s.route_elems || (size_t)L->n_routed > ctx->s.logit_elems)
@@ -843,9 +928,9 @@ int rmoe_moe_experts_grouped(rmoe_ctx* ctx, int layer, const uint16_t* x, int T,
   TRY(reserve_layer(ctx, *L, T, L->top_k));
   const int k = L->top_k;
   const size_t xb = align_up((size_t)T * L->H * 2, 256), ib = align_up((size_t)T * k * 4, 256),
-               gb = align_up((size_t)T * 2 * L->I * 2, 256);
+               gb = align_up((size_t)T * 2 * L->I * 2, 256), hb = align_up((size_t)T * L->Ipad * 2, 256);
   uint8_t* io;
-  TRY(io_area(ctx, 3 * xb + 2 * ib + gb, &io));
+  TRY(io_area(ctx, 3 * xb + 2 * ib + gb + (L->d_layout ? hb : 0), &io));
   uint16_t* xd = (uint16_t*)io;
   uint16_t* rd = (uint16_t*)(io + xb);
   uint16_t* sd = (uint16_t*)(io + 2 * xb);
@@ -856,8 +941,22 @@ int rmoe_moe_experts_grouped(rmoe_ctx* ctx, int layer, const uint16_t* x, int T,
   HIP_TRY(hipMemcpyAsync(idd, top_ids, (size_t)T * k * 4, hipMemcpyHostToDevice, ctx->stream));
   HIP_TRY(hipMemcpyAsync(wd, top_weights, (size_t)T * k * 4, hipMemcpyHostToDevice, ctx->stream));
   HIP_TRY(hipMemcpyAsync(gd, shared_gu, (size_t)T * 2 * L->I * 2, hipMemcpyHostToDevice, ctx->stream));
-  HIP_TRY(rmoe::launch_moe_prefill(*L, xd, T, idd, wd, nullptr, nullptr, gd, act, gate_beta, value_beta, false, nullptr,
-                                   rd, sd, ctx->s.pf, ctx->s.pf_bytes, ctx->s, ctx->stream));
+  if (L->d_layout) {
+    // Weights-d layer: the routed experts of each token run through the decode kernels
+    // (q4nx gate/up, bfp16 down, ordered combine), queued back to back; the shared down
+    // is the bfp16 GEMV of moe_b2's last expert over RTNE(act(shared_gu)).
+    uint16_t* hd = (uint16_t*)(io + 3 * xb + 2 * ib + gb);
+    for (int t = 0; t < T; ++t)
+      HIP_TRY(rmoe::launch_moe_decode(*L, xd + (size_t)t * L->H, idd + (size_t)t * k, wd + (size_t)t * k, k, false, act,
+                                      gate_beta, value_beta, false, nullptr, rd + (size_t)t * L->H, ctx->s,
+                                      ctx->stream));
+    HIP_TRY(rmoe::launch_act_rows(gd, T, L->I, L->Ipad, act, gate_beta, value_beta, hd, ctx->stream));
+    HIP_TRY(rmoe::launch_linear_bfp16(L->dn + (size_t)L->n_routed * L->dn_bytes, L->H, L->Ipad, hd, T, sd, ctx->s,
+                                      ctx->stream));
+  } else {
+    HIP_TRY(rmoe::launch_moe_prefill(*L, xd, T, idd, wd, nullptr, nullptr, gd, act, gate_beta, value_beta, false,
+                                     nullptr, rd, sd, ctx->s.pf, ctx->s.pf_bytes, ctx->s, ctx->stream));
+  }
   HIP_TRY(hipMemcpyAsync(routed, rd, (size_t)T * L->H * 2, hipMemcpyDeviceToHost, ctx->stream));
   HIP_TRY(hipMemcpyAsync(shared_down, sd, (size_t)T * L->H * 2, hipMemcpyDeviceToHost, ctx->stream));
   return sync_and_check(ctx, ctx->stream);
@@ -869,6 +968,7 @@ int rmoe_moe_prefill_dev(rmoe_ctx* ctx, int layer, const void* x_dev, int T, voi
   TRY(check_layer(ctx, layer, &L));
   if (!L->has_router) return fail(RMOE_EINVAL, "layer %d has no router", layer);
   if (L->n_shared < 1) return fail(RMOE_EINVAL, "layer %d has no shared expert", layer);
+  TRY(require_q4nx_layer(*L, layer, "rmoe_moe_prefill_dev"));
   if (!x_dev || !out_dev || T < 1) return fail(RMOE_EINVAL, "bad argument");
   if (act != RMOE_ACT_SITU && act != RMOE_ACT_SWIGLU) return fail(RMOE_EINVAL, "unknown activation %d", act);
   if (T > ctx->s.max_tokens) return fail(RMOE_EINVAL, "T=%d exceeds the reserved %d tokens: call rmoe_reserve", T, ctx->s.max_tokens);

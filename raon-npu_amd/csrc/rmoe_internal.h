@@ -35,6 +35,7 @@ inline size_t matrix_bytes(int M, int K) { return (size_t)M * (size_t)K * 5 / 8;
 // bfp16ebs8 matrices (bfp16_gemv.hip): 9 bits per weight in tiles of 64 rows x 128
 // columns, 9,216 bytes each (8,192 B of int8 mantissas, then 1,024 B of exponents).
 constexpr int kB16TileBytes = 9216;
+constexpr int kB16MantBytes = 8192;
 inline size_t matrix_bytes_bfp16(int M, int K) { return (size_t)M * (size_t)K * 9 / 8; }
 
 // ------------------------------------------------------------- device helpers --
@@ -102,6 +103,54 @@ __device__ __forceinline__ float group_apply(uint32_t sm, float dprime, float s_
   const float a = 16.f * scale;
   const float b = mn - a;
   return fmaf(a, dprime, fmaf(b, s_sum, y));
+}
+
+// ---- bfp16ebs8 helpers (quant/bfp16.py:71-140, kernels/gemv_bfp16/bfp16_gemv.cc:8-22) ----
+// bf16 pair (lo, hi) of two fp32 values whose low 16 bits are zero.
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// The 4 mantissas of a dword -> two exact bf16 pairs (columns (4d, 4d+1), (4d+2, 4d+3)).
+// (float)(int8_t) compiles to one sign-extending SDWA convert per byte.
+__device__ __forceinline__ void mant_pairs(uint32_t w, uint32_t& p0, uint32_t& p1) {
+  p0 = bf16_pair((float)(int8_t)w, (float)(int8_t)(w >> 8));
+  p1 = bf16_pair((float)(int8_t)(w >> 16), (float)((int32_t)w >> 24));
+}
+
+// Kernel scale of an exponent byte: 2^(max(e, 7) - 133), built as fp32 bits.
+__device__ __forceinline__ float exp_scale(uint32_t e) { return __uint_as_float((max(e, 7u) - 6u) << 23); }
+
+// One lane's row of a bfp16 tile (64 rows x 128 columns) against x of those 128 columns
+// (64 bf16-pair dwords): per 8-column group d = dot(mantissas, x) from 0, then
+// acc = fma(2^(e-133), d, acc), in column order -- the order of the dense bfp16 GEMV.
+__device__ __forceinline__ float b16_tile_accumulate(const uint8_t* tile, int lane, const uint32_t* __restrict__ xs,
+                                                     float acc) {
+  const uint8_t* p = tile + lane * 16;
+  uint4 mc[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) mc[c] = load_stream16(p + c * 1024);
+  const uint4 eq = load_stream16(p + kB16MantBytes);
+  const uint32_t ew[4] = {eq.x, eq.y, eq.z, eq.w};
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const uint32_t w[4] = {mc[c].x, mc[c].y, mc[c].z, mc[c].w};
+    uint32_t q[8];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) mant_pairs(w[d], q[2 * d], q[2 * d + 1]);
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg) {
+      const int g = 2 * c + gg;
+      const float s = exp_scale((ew[g >> 2] >> (8 * (g & 3))) & 0xffu);
+      const uint4 xv = *reinterpret_cast<const uint4*>(xs + g * 4);
+      float d = dot2_bf16(q[4 * gg], xv.x, 0.f);
+      d = dot2_bf16(q[4 * gg + 1], xv.y, d);
+      d = dot2_bf16(q[4 * gg + 2], xv.z, d);
+      d = dot2_bf16(q[4 * gg + 3], xv.w, d);
+      acc = fmaf(s, d, acc);
+    }
+  }
+  return acc;
 }
 
 // Activations, in the operation order of the oracle (fp32).
@@ -184,8 +233,16 @@ struct RmoeMatrix {
 struct RmoeLayer {
   int H = 0, I = 0, Ipad = 0, n_routed = 0, n_shared = 0, top_k = 0;
   size_t gu_bytes = 0, dn_bytes = 0;  // per expert
-  uint8_t* gu = nullptr;              // (n_routed + n_shared) experts, tile layout
-  uint8_t* dn = nullptr;
+  // Layout of the expert weights.  A q4nx layer holds gate/up and down of every expert
+  // (n_routed + n_shared) in q4nx.  A weights-d layer (rmoe_layer_create_d) holds the
+  // reference's moe_b1 (q4nx gate/up of the n_routed routed experts) and moe_b2 (bfp16
+  // down of n_routed + 1 experts, the last one the shared expert's); the shared gate/up
+  // is a separate dense matrix.
+  bool d_layout = false;
+  int gu_experts = 0, dn_experts = 0;
+  int dn_fmt = 0;                     // RMOE_FMT_Q4NX or RMOE_FMT_BFP16
+  uint8_t* gu = nullptr;              // gu_experts experts, tile layout
+  uint8_t* dn = nullptr;              // dn_experts experts, tile layout of dn_fmt
   uint16_t* router_w = nullptr;  // [n_routed, H] bf16
   float* router_bias = nullptr;  // [n_routed] or null
   bool has_router = false;
@@ -273,6 +330,10 @@ hipError_t launch_route(const RmoeLayer& L, const uint16_t* x, int T, int32_t* i
 hipError_t launch_moe_decode(const RmoeLayer& L, const uint16_t* x, const int32_t* ids, const float* wts, int k,
                              bool with_shared, int act, float gb, float vb, bool residual, uint16_t* out,
                              uint16_t* out_routed, RmoeScratch& s, hipStream_t st, int stages = 3);
+
+// h[T, Ipad] = RTNE(act(gu[t, :I], gu[t, I:2I])) with zero columns [I, Ipad).
+hipError_t launch_act_rows(const uint16_t* gu, int T, int I, int Ipad, int act, float gb, float vb, uint16_t* h,
+                           hipStream_t st);
 
 hipError_t launch_dispatch(const int32_t* ids, int T, int k, int n_experts, int32_t* order, int32_t* inv,
                            int32_t* offsets, RmoeScratch& s, hipStream_t st);

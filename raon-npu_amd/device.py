@@ -12,7 +12,7 @@ import ctypes as C
 import numpy as np
 
 from . import _lib
-from ._lib import ACT_SITU, ACT_SWIGLU, SCORE_SIGMOID, SCORE_SOFTMAX, call, ptr
+from ._lib import ACT_SITU, ACT_SWIGLU, BUNDLE_B1, BUNDLE_B2, SCORE_SIGMOID, SCORE_SOFTMAX, call, ptr
 from .geometry import MoeGeometry
 
 
@@ -115,6 +115,14 @@ class Context:
         call("rmoe_layer_create", self._h, int(layer), geom.hidden, geom.inter, geom.n_routed, geom.n_shared, geom.top_k)
         return MoeLayer(self, int(layer), geom)
 
+    def create_layer_d(self, layer: int, geom: MoeGeometry) -> "MoeLayer":
+        """A layer in the reference's weights-d layout (npu/backend.py:624-700): moe_b1 q4nx
+        gate/up of the routed experts, moe_b2 bfp16 down of routed + shared experts."""
+        if geom.n_shared != 1:
+            raise ValueError("a weights-d layer has exactly one shared expert (moe_b2's last expert)")
+        call("rmoe_layer_create_d", self._h, int(layer), geom.hidden, geom.inter, geom.n_routed, geom.top_k)
+        return MoeLayer(self, int(layer), geom, d_layout=True)
+
     # ------------------------------------------------------- decode stack --
     @staticmethod
     def _layer_ids(layers) -> np.ndarray:
@@ -206,9 +214,34 @@ class Matrix:
 class MoeLayer:
     """One MoE layer (experts + router) resident on the device."""
 
-    def __init__(self, ctx: Context, layer: int, geom: MoeGeometry):
+    def __init__(self, ctx: Context, layer: int, geom: MoeGeometry, d_layout: bool = False):
         self.ctx, self.layer, self.geom = ctx, layer, geom
+        self.d_layout = bool(d_layout)
         self.has_router = False
+
+    @property
+    def gu_expert_bytes(self) -> int:
+        """GEMV bytes of one expert's gate/up (q4nx [2I, H])."""
+        return self.geom.gu_bytes
+
+    @property
+    def dn_expert_bytes(self) -> int:
+        """GEMV bytes of one expert's down: q4nx [H, Ipad], or bfp16 [H, Ipad] in a weights-d layer."""
+        g = self.geom
+        return g.hidden * g.inter_pad * 9 // 8 if self.d_layout else g.dn_bytes
+
+    def upload_d(self, bundle: int, expert0: int, data: bytes | np.ndarray):
+        """Experts ``[expert0, expert0 + n)`` of moe_b1 (``bundle`` 1) or moe_b2 (2) of a
+        weights-d layer from ``n`` consecutive expert slices of the bundle file."""
+        if bundle not in (BUNDLE_B1, BUNDLE_B2):
+            raise ValueError(f"bundle must be {BUNDLE_B1} (moe_b1) or {BUNDLE_B2} (moe_b2), got {bundle!r}")
+        buf = (np.frombuffer(data, np.uint8) if isinstance(data, (bytes, bytearray, memoryview))
+               else np.ascontiguousarray(data, np.uint8).reshape(-1))
+        per = self.gu_expert_bytes if bundle == BUNDLE_B1 else self.dn_expert_bytes
+        if buf.size % per:
+            raise ValueError(f"moe_b{bundle} slice of {buf.size} bytes is not a whole number of {per}-byte experts")
+        call("rmoe_layer_upload_d", self.ctx.handle, self.layer, int(bundle), int(expert0), buf.size // per, ptr(buf),
+             buf.size)
 
     def upload_experts(self, gate_up: bytes | np.ndarray, down: bytes | np.ndarray):
         gu = np.frombuffer(gate_up, np.uint8) if isinstance(gate_up, (bytes, bytearray)) else np.ascontiguousarray(gate_up, np.uint8)
@@ -241,10 +274,14 @@ class MoeLayer:
              _stream_ptr(stream))
 
     def download_expert(self, expert: int) -> tuple[bytes, bytes]:
-        gu = np.empty(self.geom.gu_bytes, np.uint8)
-        dn = np.empty(self.geom.dn_bytes, np.uint8)
-        call("rmoe_layer_download_expert", self.ctx.handle, self.layer, int(expert), ptr(gu), gu.size, ptr(dn), dn.size)
-        return gu.tobytes(), dn.tobytes()
+        """(gate_up, down) GEMV bytes of one expert; gate_up is b"" for the shared expert
+        of a weights-d layer, whose gate/up lives outside the layer."""
+        no_gu = self.d_layout and int(expert) == self.geom.n_routed
+        gu = None if no_gu else np.empty(self.gu_expert_bytes, np.uint8)
+        dn = np.empty(self.dn_expert_bytes, np.uint8)
+        call("rmoe_layer_download_expert", self.ctx.handle, self.layer, int(expert), ptr(gu), 0 if no_gu else gu.size,
+             ptr(dn), dn.size)
+        return (b"" if no_gu else gu.tobytes()), dn.tobytes()
 
     def set_router(self, weight_bf16, bias=None, score: str = "softmax", renormalize: bool = True, scaling: float = 1.0):
         code = {"sigmoid": SCORE_SIGMOID, "softmax": SCORE_SOFTMAX}[score]

@@ -90,8 +90,7 @@ def test_moe_layer_from_q4k_experts(gpu_ctx):
     down = _q4k_tensor(ne * geom.hidden, geom.inter, 23)
     rng = np.random.default_rng(24)
     router = f32_to_bf16(rng.normal(0.0, 0.05, (geom.n_routed, geom.hidden)).astype(np.float32))
-    be = GpuBackend.__new__(GpuBackend)  # share the session context
-    be.ctx, be._layers = gpu_ctx, {}
+    be = GpuBackend(context=gpu_ctx)
     lyr = be.register_moe_layer_q4k(960, geom, gate, up, down, router_weight=router, score="softmax")
     lyr.reserve(4)
     gu_parts, dn_parts = [], []
