@@ -33,7 +33,10 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 # WRITE_SIZE (calibrated against a 512 MiB copy) over `bench.py --profile-pass`; the
 # summary and commands are in profiles/decode_prefill_hbm_counters.txt.  Re-measure
 # after changing the kernel.
-DECODE_TRAFFIC_BYTES = 1334592840
+DECODE_TRAFFIC_BYTES = 1334635261
+# HBM bytes per lm_head GEMV launch from the same counter passes (1.001x its 749,076,480
+# algorithmic bytes).
+LM_HEAD_TRAFFIC_BYTES = 749777961
 
 
 def log(msg: str) -> None:
@@ -53,6 +56,7 @@ def parse_args():
     ap.add_argument("--prefill-reps", type=int, default=10)
     ap.add_argument("--zipf-tau", type=float, default=0.02)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-lm-head", action="store_true", help="skip the lm_head bfp16 GEMV measurement")
     ap.add_argument("--profile-pass", action="store_true",
                     help="short run for hardware counters: 2 decode launches, 1 prefill layer and a "
                          "512 MiB device copy (the calibration kernel of known size); prints no JSON")
@@ -147,6 +151,39 @@ def prefill_bench(ctx, geom, T: int, seed: int, reps: int, tau: float, stream):
     return secs, flops, hist
 
 
+def lm_head_bench(ctx, stream, seed: int, n: int = 50):
+    """The released model's lm_head GEMV (npu/backend.py:703-719): bfp16ebs8 [260096, 2560],
+    749 MB, one token.  Synthetic GEMV bytes (uniform int8 mantissas, exponent 118) uploaded
+    through rmoe_matrix_upload_bfp16; n launches captured in one graph."""
+    import numpy as np
+    import torch
+
+    M, K = 260096, 2560
+    nbytes = M * K * 9 // 8
+    rng = np.random.default_rng(seed + 11)
+    buf = rng.integers(0, 256, nbytes, dtype=np.uint8)
+    buf.reshape(-1, 144)[:, :16] = 118
+    mat = ctx.upload_matrix(buf, M, K, fmt="bfp16")
+    del buf
+    mat.reserve(1)
+    x = torch.randn(1, K, device="cuda").to(torch.bfloat16).view(torch.int16)
+    y = torch.empty(1, M, dtype=torch.int16, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        mat.linear_dev(x, 1, y, stream=stream)
+        with torch.cuda.graph(g, stream=stream):
+            for _ in range(n):
+                mat.linear_dev(x, 1, y, stream=stream)
+        g.replay()
+    torch.cuda.synchronize()
+    secs = time_graph(g, 1, stream) / n
+    mat.free()
+    gbs = nbytes / secs / 1e9
+    return {"workload": "lm_head bfp16ebs8 GEMV [260096, 2560], 1 token (linear_bfp16_kernel)",
+            "us_per_launch": round(secs * 1e6, 2), "bytes_per_launch": nbytes, "GBps": round(gbs, 1),
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "traffic": LM_HEAD_TRAFFIC_BYTES}
+
+
 def cpu_baseline(lyr, geom, budget_s: float, seed: int):
     """The NumPy oracle (reference CPU path, DWeights-style per-call dequant with an LRU of
     32 experts) on this host: seconds per token-layer, extrapolated to the 48-layer stack."""
@@ -185,8 +222,8 @@ def cpu_baseline(lyr, geom, budget_s: float, seed: int):
 def profile_pass(ctx, layers, geom, args, stream, gen) -> int:
     """A short, fixed sequence of kernels for per-dispatch hardware counters: a plain
     device copy of 512 MiB (twice; its FETCH_SIZE / WRITE_SIZE per dispatch calibrate the
-    counters against a known byte count), two decode launches of the 48-layer stack and
-    one prefill layer of config 5."""
+    counters against a known byte count), two decode launches of the 48-layer stack, one
+    prefill layer of config 5 and the lm_head GEMV."""
     import torch
 
     n = 512 * 1024 * 1024
@@ -204,8 +241,10 @@ def profile_pass(ctx, layers, geom, args, stream, gen) -> int:
     torch.cuda.synchronize()
     if not args.no_prefill:
         prefill_bench(ctx, geom, args.prefill_tokens, args.seed, 1, args.zipf_tau, stream)
+    if not args.no_lm_head:
+        lm_head_bench(ctx, stream, args.seed, n=2)
     torch.cuda.synchronize()
-    log("profile pass done: copy 512 MiB x2, decode stack x2, prefill x1")
+    log("profile pass done: copy 512 MiB x2, decode stack x2, prefill x1, lm_head GEMV")
     ctx.close()
     return 0
 
@@ -279,6 +318,11 @@ def main() -> int:
         log(f"prefill {args.prefill_tokens} tokens: {psec * 1e3:.3f} ms/layer, {tflops:.1f} TFLOP/s "
             f"(hist max {hist.max()} min {hist.min()})")
 
+    lm_head = None
+    if not args.no_lm_head:
+        lm_head = lm_head_bench(ctx, stream, args.seed)
+        log(f"lm_head bfp16 GEMV: {lm_head['us_per_launch']} us, {lm_head['GBps']} GB/s")
+
     cpu = None
     if not args.no_cpu:
         per_layer, n, threads = cpu_baseline(layers[0], geom, args.cpu_seconds, args.seed)
@@ -331,6 +375,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "lm_head": lm_head,
     }
     print(json.dumps(line), flush=True)
     ctx.close()
