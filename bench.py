@@ -57,6 +57,7 @@ def parse_args():
     ap.add_argument("--zipf-tau", type=float, default=0.02)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-lm-head", action="store_true", help="skip the lm_head bfp16 GEMV measurement")
+    ap.add_argument("--no-configs", action="store_true", help="skip configs 1-3 and the weights-d layer")
     ap.add_argument("--profile-pass", action="store_true",
                     help="short run for hardware counters: 2 decode launches, 1 prefill layer and a "
                          "512 MiB device copy (the calibration kernel of known size); prints no JSON")
@@ -182,6 +183,97 @@ def lm_head_bench(ctx, stream, seed: int, n: int = 50):
     return {"workload": "lm_head bfp16ebs8 GEMV [260096, 2560], 1 token (linear_bfp16_kernel)",
             "us_per_launch": round(secs * 1e6, 2), "bytes_per_launch": nbytes, "GBps": round(gbs, 1),
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "traffic": LM_HEAD_TRAFFIC_BYTES}
+
+
+def graph_us(fn, n: int, stream) -> float:
+    """Microseconds per call of fn() (a device-side launch sequence), n calls in one graph."""
+    import torch
+
+    with torch.cuda.stream(stream):
+        fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g, stream=stream):
+            for _ in range(n):
+                fn()
+        g.replay()
+    torch.cuda.synchronize()
+    return time_graph(g, 1, stream) / n * 1e6
+
+
+def configs_bench(ctx, layers, geom, seed: int, stream) -> dict:
+    """SURVEY configs 1-3 (the other rows of the measurement table) and one weights-d MoE
+    layer at the released model's shapes; each timed as back-to-back launches in a graph."""
+    import numpy as np
+    import torch
+
+    from raon_npu_amd.geometry import RAON_1_MINI
+
+    out = {}
+    gen = torch.Generator(device="cuda").manual_seed(seed + 21)
+    # config 1: one q4nx GEMV, W [768, 2048] (the down width of a BASELINE expert), x 1 x 2048
+    w = torch.randn(768, 2048, device="cuda", generator=gen) * 0.02
+    mat = ctx.quantize_matrix(w, 768, 2048)
+    del w
+    mat.reserve(1)
+    x = torch.randn(1, 2048, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
+    y = torch.empty(1, 768, dtype=torch.int16, device="cuda")
+    us = graph_us(lambda: mat.linear_dev(x, 1, y, stream=stream), 1000, stream)
+    b = 990208  # weights 983,040 + x 4,096 + y 3,072 (SURVEY 8(d))
+    out["config1_gemv"] = {"workload": "q4nx GEMV [768, 2048] x 1 token, 1000 launches in a graph",
+                           "us_per_launch": round(us, 3), "GBps": round(b / us / 1e3, 1)}
+    mat.free()
+    # config 2: one decode layer (router + 8 routed + shared + combine), one persistent launch
+    x1 = torch.randn(geom.hidden, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
+    o1 = torch.empty_like(x1)
+    us = graph_us(lambda: ctx.decode_stack_dev([layers[0]], x1, o1, residual=True, stream=stream), 200, stream)
+    b = geom.decode_bytes()
+    out["config2_decode_layer"] = {"workload": "one BASELINE decode layer, batch 1 (1-layer persistent launch)",
+                                   "us_per_layer": round(us, 3), "GBps": round(b / us / 1e3, 1),
+                                   "frac_hbm_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+    ctx.reserve_decode_stack(layers)
+    # config 3: prefill of 445 tokens, router without selection bias (near-uniform routing)
+    lyr = layers[0]
+    T = 445
+    lyr.reserve(T)
+    xp = torch.randn(T, geom.hidden, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
+    op = torch.empty_like(xp)
+    us = graph_us(lambda: lyr.moe_prefill_dev(xp, T, op, stream=stream), 20, stream)
+    fl = T * (geom.top_k + 1) * geom.flops_per_assignment + 2 * T * geom.hidden * geom.n_routed
+    wb = geom.n_experts * geom.expert_bytes
+    out["config3_prefill_445"] = {"workload": "one BASELINE prefill layer, 445 tokens, softmax top-8 routing",
+                                  "ms_per_layer": round(us / 1e3, 4), "tflops": round(fl / us / 1e6, 2),
+                                  "weight_GBps": round(wb / us / 1e3, 1)}
+    # weights-d layer: moe_b1 (q4nx) + moe_b2 (bfp16) at H=2560, I=1088, 128+1 experts, top-6
+    g = RAON_1_MINI
+    rng = np.random.default_rng(seed + 23)
+    dl = ctx.create_layer_d(1001, g)
+    b1 = rng.integers(0, 256, g.n_routed * g.gu_bytes, dtype=np.uint8)
+    blk = b1.reshape(-1, 5120)
+    sc = rng.uniform(5e-4, 2e-3, (blk.shape[0], 256)).astype(np.float32)
+    blk[:, :512] = (sc.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).reshape(-1, 512)
+    blk[:, 512:1024] = ((-7.5 * sc).view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).reshape(-1, 512)
+    dl.upload_d(1, 0, b1)
+    del b1, blk
+    b2 = rng.integers(0, 256, (g.n_routed + 1) * dl.dn_expert_bytes, dtype=np.uint8)
+    b2.reshape(-1, 144)[:, :16] = 118
+    dl.upload_d(2, 0, b2)
+    del b2
+    dl.reserve(1)
+    xd = torch.randn(g.hidden, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
+    od = torch.empty_like(xd)
+    ids = torch.tensor(rng.choice(g.n_routed, g.top_k, replace=False), dtype=torch.int32, device="cuda")
+    wts = torch.full((g.top_k,), 1.0 / g.top_k, dtype=torch.float32, device="cuda")
+    us = graph_us(lambda: dl.moe_experts_dev(xd, ids, wts, od, stream=stream), 200, stream)
+    b = g.top_k * (dl.gu_expert_bytes + dl.dn_expert_bytes)
+    out["weights_d_moe_experts"] = {
+        "workload": "released-model MoE layer from weights-d bundles (q4nx moe_b1 + bfp16 moe_b2, H=2560, "
+                    "I=1088), 6 routed experts of one token (decode_gate_up_kernel + decode_down_kernel)",
+        "us_per_layer": round(us, 3), "bytes": b, "GBps": round(b / us / 1e3, 1),
+        "frac_hbm_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+    dl.free()
+    return out
 
 
 def cpu_baseline(lyr, geom, budget_s: float, seed: int):
@@ -318,6 +410,12 @@ def main() -> int:
         log(f"prefill {args.prefill_tokens} tokens: {psec * 1e3:.3f} ms/layer, {tflops:.1f} TFLOP/s "
             f"(hist max {hist.max()} min {hist.min()})")
 
+    configs = None
+    if not args.no_configs:
+        configs = configs_bench(ctx, layers, geom, args.seed, stream)
+        for k, v in configs.items():
+            log(f"{k}: {v}")
+
     lm_head = None
     if not args.no_lm_head:
         lm_head = lm_head_bench(ctx, stream, args.seed)
@@ -376,6 +474,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "prefill": prefill,
         "lm_head": lm_head,
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
     ctx.close()

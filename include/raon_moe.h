@@ -190,6 +190,15 @@ int rmoe_route(rmoe_ctx* ctx, int layer, const uint16_t* x, int T, int32_t* top_
 int rmoe_moe_experts(rmoe_ctx* ctx, int layer, const uint16_t* x, const int32_t* top_ids,
                      const float* top_weights, int k, int act, float gate_beta, float value_beta,
                      uint16_t* out);
+/* Device-pointer form of rmoe_moe_experts for any layer (q4nx or weights-d): x_dev bf16
+ * [H], top_ids_dev int32 [k] (distinct, in 0..n_routed-1: not checked on the device beyond
+ * clamping into range), top_weights_dev fp32 [k], out_dev bf16 [H].  Queued on `stream`
+ * (NULL: the context stream); never allocates, so it can be captured in a HIP graph after
+ * rmoe_reserve(layer, 1) with k <= top_k.  Replaces NpuBackend.moe_experts' direct decode
+ * runner (npu/backend.py:5098-5229) for an engine that keeps activations on the device. */
+int rmoe_moe_experts_dev(rmoe_ctx* ctx, int layer, const void* x_dev, const void* top_ids_dev,
+                         const void* top_weights_dev, int k, int act, float gate_beta, float value_beta,
+                         void* out_dev, void* stream);
 
 /* Router + routed + shared expert + combine for one decode token, all on the device:
  * RaonModel._moe_token (host/raon.py:1288-1330) with the router moved onto the GPU.

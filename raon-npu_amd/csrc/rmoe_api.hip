@@ -783,6 +783,23 @@ int rmoe_moe_experts(rmoe_ctx* ctx, int layer, const uint16_t* x, const int32_t*
   return RMOE_OK;
 }
 
+int rmoe_moe_experts_dev(rmoe_ctx* ctx, int layer, const void* x_dev, const void* top_ids_dev,
+                         const void* top_weights_dev, int k, int act, float gate_beta, float value_beta,
+                         void* out_dev, void* stream) {
+  RmoeLayer* L;
+  TRY(check_layer(ctx, layer, &L));
+  if (!x_dev || !top_ids_dev || !top_weights_dev || !out_dev) return fail(RMOE_EINVAL, "null argument");
+  if (k < 1 || k > 16 || k > L->n_routed) return fail(RMOE_EINVAL, "k (%d) must be in 1..min(16, n_routed)", k);
+  if (act != RMOE_ACT_SITU && act != RMOE_ACT_SWIGLU) return fail(RMOE_EINVAL, "unknown activation %d", act);
+  hipError_t e = rmoe::launch_moe_decode(*L, (const uint16_t*)x_dev, (const int32_t*)top_ids_dev,
+                                         (const float*)top_weights_dev, k, false, act, gate_beta, value_beta, false,
+                                         nullptr, (uint16_t*)out_dev, ctx->s, pick_stream(ctx, stream));
+  if (e == hipErrorInvalidValue)
+    return fail(RMOE_EINVAL, "scratch too small for layer %d with k=%d: call rmoe_reserve", layer, k);
+  HIP_TRY(e);
+  return RMOE_OK;
+}
+
 // Validate a list of decode layers for the persistent kernel; fills ptrs.
 static int stack_layers(rmoe_ctx* ctx, const int* layers, int n_layers, std::vector<const RmoeLayer*>& ptrs) {
   if (!ctx) return fail(RMOE_EINVAL, "null context");

@@ -202,3 +202,41 @@ def test_load_weights_d_real_shapes(gpu_ctx, tmp_path, small_d):
     assert 1 not in be._layers
     with pytest.raises(KeyError):  # the device layer was freed too
         lyr.free()
+
+
+def test_moe_experts_dev_matches_host_and_replays(small_d):
+    """rmoe_moe_experts_dev: the host entry point's result from device pointers, eagerly
+    and from a captured graph replayed with eager work in between (every replay checked)."""
+    import torch
+
+    be, lyr, geom, bank, _ = small_d
+    rng = np.random.default_rng(51)
+    xs = random_tokens(3, geom.hidden, 52)
+    ids = np.stack([rng.choice(geom.n_routed, geom.top_k, replace=False) for _ in range(3)]).astype(np.int32)
+    w = rng.uniform(0.1, 1.0, (3, geom.top_k)).astype(np.float32)
+    want = np.stack([be.moe_experts(970, xs[t], ids[t], w[t]) for t in range(3)])
+    xd = torch.from_numpy(xs.view(np.int16)).cuda()
+    idd = torch.from_numpy(ids).cuda()
+    wd = torch.from_numpy(w).cuda()
+    od = torch.zeros_like(xd)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for t in range(3):
+            lyr.moe_experts_dev(xd[t], idd[t], wd[t], od[t], stream=stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(od.cpu().numpy().view(np.uint16), want)
+    od.zero_()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g, stream=stream):
+            for t in range(3):
+                lyr.moe_experts_dev(xd[t], idd[t], wd[t], od[t], stream=stream)
+    for rep in range(3):
+        od.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(od.cpu().numpy().view(np.uint16), want), rep
+        be.moe_experts(970, xs[rep], ids[(rep + 1) % 3], w[rep])  # eager work between replays
+    with pytest.raises(ValueError):
+        lyr.moe_experts_dev(xd[0], idd[0][:2].contiguous(), wd[0], od[0])
