@@ -300,36 +300,51 @@ __global__ __launch_bounds__(256) void prep_x_kernel(const uint16_t* __restrict_
 }
 
 // ----------------------------------------------------------------- tile table --
-// tiles[i] = expert | (row_start << 9) for the m-tiles of every group; group e covers
-// sorted rows [offsets[e], offsets[e+1]); the extra group n_routed (shared expert)
-// covers rows [offsets[n_routed], offsets[n_routed] + shared_rows).  tiles[-1]... the
-// count is written to *ntiles.
+// The m-tiles of every group, 128 sorted rows each; group e covers sorted rows
+// [offsets[e], offsets[e+1]) and the extra group n_routed (shared expert) rows
+// [offsets[n_routed], offsets[n_routed] + shared_rows).  A tile is
+// expert | (row_start << 9).  Tiles are listed by class, the number of 16-row fragments
+// that hold rows: class 0 (up to 32 rows: 2 fragments), 1 (up to 64: 4), 2 (8); the
+// grouped GEMM runs each class with that many fragments, so a group's short last tile
+// does no MFMA work on absent rows.  Class c's tiles sit at tiles[c * cap ...] in group
+// order, their count in ntiles[c].
 constexpr int kBM = 128;
+constexpr int kTileClasses = 3;
+__host__ __device__ constexpr int class_fragments(int c) { return c == 0 ? 2 : c == 1 ? 4 : 8; }
 
 // One workgroup of 512 threads; thread e owns group e (routed 0..n_routed-1, shared n_routed).
 __global__ __launch_bounds__(512) void tile_table_kernel(const int32_t* __restrict__ offsets, int n_routed,
                                                          int shared_rows, uint32_t* __restrict__ tiles,
                                                          int* __restrict__ ntiles, int cap) {
-  __shared__ int base[513];
+  __shared__ int base[kTileClasses][513];
   const int e = threadIdx.x;
   const int ng = n_routed + (shared_rows > 0 ? 1 : 0);
-  int b = 0, end = 0, nt = 0;
+  int b = 0, full = 0, cnt[kTileClasses] = {0, 0, 0};
   if (e < ng) {
     b = offsets[min(e, n_routed)];
-    end = e < n_routed ? offsets[e + 1] : b + shared_rows;
-    nt = (end - b + kBM - 1) / kBM;
+    const int end = e < n_routed ? offsets[e + 1] : b + shared_rows;
+    full = (end - b) / kBM;
+    const int rem = (end - b) % kBM;
+    cnt[2] = full + (rem > 64 ? 1 : 0);
+    cnt[1] = (rem > 32 && rem <= 64) ? 1 : 0;
+    cnt[0] = (rem > 0 && rem <= 32) ? 1 : 0;
   }
-  base[e + 1] = nt;
-  if (e == 0) base[0] = 0;
-  __syncthreads();
-  if (e == 0)
-    for (int q = 1; q <= ng; ++q) base[q] += base[q - 1];
-  __syncthreads();
-  for (int i = 0; i < nt; ++i) {
-    const int slot = base[e] + i;
-    if (slot < cap) tiles[slot] = (uint32_t)e | ((uint32_t)(b + i * kBM) << 9);
+#pragma unroll
+  for (int c = 0; c < kTileClasses; ++c) {
+    base[c][e + 1] = cnt[c];
+    if (e == 0) base[c][0] = 0;
   }
-  if (e == 0) *ntiles = min(base[ng], cap);
+  __syncthreads();
+  if (e < kTileClasses)
+    for (int q = 1; q <= ng; ++q) base[e][q] += base[e][q - 1];
+  __syncthreads();
+  for (int i = 0; i < cnt[2]; ++i) {
+    const int slot = base[2][e] + i;
+    if (slot < cap) tiles[2 * cap + slot] = (uint32_t)e | ((uint32_t)(b + i * kBM) << 9);
+  }
+  for (int c = 0; c < 2; ++c)
+    if (cnt[c] && base[c][e] < cap) tiles[c * cap + base[c][e]] = (uint32_t)e | ((uint32_t)(b + full * kBM) << 9);
+  if (e < kTileClasses) ntiles[e] = min(base[e][ng], cap);
 }
 
 // ------------------------------------------------------------- grouped GEMM --
@@ -450,6 +465,7 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
 // while the first two K steps' copies are in flight.  K loop: a three-deep LDS ring
 // filled by global->LDS copies; per K step one barrier, then the copy for step kt+2
 // into the slot step kt-1 used.
+template <int MF>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void grouped_gemm_kernel(GemmArgs a, int tile_cap) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kGemmLds];
   __shared__ int rowidx[kBM];
@@ -575,9 +591,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   issue(0);
   issue_to(nkt > 1 ? 1 : 0, 1);
 
-  f32x4_t acc[8][2];
+  f32x4_t acc[MF][2];
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
+  for (int m = 0; m < MF; ++m) {
     acc[m][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     acc[m][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
@@ -612,12 +628,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // Six products per (m, f), smallest first; consecutive MFMAs go to different
     // accumulators (16 independent chains).
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
+    for (int half = 0; half < (MF + 3) / 4; ++half) {
       __builtin_amdgcn_sched_barrier(0);
       uint4 ah[4], am[4], al[4];
 #pragma unroll
       for (int mm = 0; mm < 4; ++mm) {
         const int m = 4 * half + mm;
+        if (m >= MF) continue;
         ah[mm] = *reinterpret_cast<const uint4*>(ss + m * 16 * kSRow);
         am[mm] = *reinterpret_cast<const uint4*>(ss + m * 16 * kSRow + 64);
         al[mm] = *reinterpret_cast<const uint4*>(ss + m * 16 * kSRow + 128);
@@ -629,6 +646,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
           for (int f = 0; f < 2; ++f) {
             const int m = 4 * half + mm;
+            if (m >= MF) continue;
             const uint4 av = p == 0 ? al[mm] : (p == 1 || p == 3) ? am[mm] : ah[mm];
             const uint4 bv = (p == 0 || p == 3 || p == 5) ? bc[f][0] : (p == 1 || p == 4) ? bc[f][1] : bc[f][2];
             acc[m][f] = mfma16(av, bv, acc[m][f]);
@@ -666,7 +684,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // 2^-(row exponent + fx): scale acc over (lane rows 16m + 4lq + i, fragment f).
   auto scale_rows = [&](const int8_t* rowe, int sign) {
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
+    for (int m = 0; m < MF; ++m) {
       const uint32_t e4 = *reinterpret_cast<const uint32_t*>(rowe + 16 * m + 4 * lq);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -710,11 +728,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       s16[f] = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_cvt_pkrtz(v16, v16));
     }
   };
-  auto read_a = [&](const int slot, int j, uint4 (&av)[8]) {
+  auto read_a = [&](const int slot, int j, uint4 (&av)[MF]) {
     const uint32_t xc = 16u * (uint32_t)((4 * j + lq) ^ l16);  // chunk 4lq+j of row 16m+l16
     const uint8_t* pa = lds + slot * kStageBytes + (xrow + xc);  // fragments m*4096 apart
 #pragma unroll
-    for (int m = 0; m < 8; ++m) av[m] = *reinterpret_cast<const uint4*>(pa + m * 4096);
+    for (int m = 0; m < MF; ++m) av[m] = *reinterpret_cast<const uint4*>(pa + m * 4096);
   };
   auto build_b = [&](const uint4 (&cw)[2], int j, const f16x2_t (&s1)[2], const f16x2_t (&s16)[2],
                      uint4 (&b)[2]) {
@@ -730,11 +748,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                         __builtin_bit_cast(uint32_t, h2), __builtin_bit_cast(uint32_t, h3));
     }
   };
-  auto mfmas = [&](const uint4 (&av)[8], const uint4 (&b)[2]) {
+  auto mfmas = [&](const uint4 (&av)[MF], const uint4 (&b)[2]) {
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
 #pragma unroll
-      for (int m = 0; m < 8; ++m) acc[m][f] = mfma16h(av[m], b[f], acc[m][f]);
+      for (int m = 0; m < MF; ++m) acc[m][f] = mfma16h(av[m], b[f], acc[m][f]);
     }
   };
   // Software pipeline.  Region (kt, j) issues the LDS reads of group j+1, runs the MFMAs
@@ -750,7 +768,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);                    \
     }                                                                       \
   } while (0)
-  uint4 avA[8], avB[8], bA[2], bB[2], cw[2];
+  uint4 avA[MF], avB[MF], bA[2], bB[2], cw[2];
   uint32_t sw[2];
   f16x2_t s1[2], s16[2];
   // Regions 1..3 of the step in `slot` (group 0's operands are in avA / bA).
@@ -816,7 +834,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // h tile [128 rows][128 units] in slot 0.
     if (a.act == 1) {
 #pragma unroll
-      for (int m = 0; m < 8; ++m)
+      for (int m = 0; m < MF; ++m)
 #pragma unroll
         for (int i = 0; i < 4; i += 2) {
           const int r = 16 * m + 4 * lq + i;
@@ -834,7 +852,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       uint16_t* gs = reinterpret_cast<uint16_t*>(lds + kStageBytes);
       uint16_t* us = reinterpret_cast<uint16_t*>(lds + 2 * kStageBytes);
 #pragma unroll
-      for (int m = 0; m < 8; ++m)
+      for (int m = 0; m < MF; ++m)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = 16 * m + 4 * lq + i;
@@ -889,7 +907,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // (bf16 by the hardware conversion: a NaN may keep its payload here; the combine
     // canonicalises what it passes through.)
 #pragma unroll
-    for (int m = 0; m < 8; ++m)
+    for (int m = 0; m < MF; ++m)
 #pragma unroll
       for (int f = 0; f < 2; ++f)
 #pragma unroll
@@ -1104,6 +1122,23 @@ hipError_t launch_topk(const float* logits, int T, int E, int k, int score, cons
   return hipGetLastError();
 }
 
+// The grouped GEMM over the three tile classes, largest first: one launch per class,
+// each grid sized for the class's worst case (a class-0/1 tile is a group's last).
+static hipError_t launch_grouped(GemmArgs a, uint32_t* tiles, int* ntiles, int cap, int n_routed, hipStream_t st) {
+  for (int c = kTileClasses - 1; c >= 0; --c) {
+    a.tiles = tiles + (size_t)c * cap;
+    a.ntiles = ntiles + c;
+    const int ccap = c == kTileClasses - 1 ? cap : min(cap, n_routed + 1);
+    const int blocks = (a.n_tiles * ccap + 7) / 8 * 8;  // the XCD mapping needs a multiple of 8
+    if (c == 2) hipLaunchKernelGGL(grouped_gemm_kernel<class_fragments(2)>, dim3(blocks), dim3(512), 0, st, a, ccap);
+    if (c == 1) hipLaunchKernelGGL(grouped_gemm_kernel<class_fragments(1)>, dim3(blocks), dim3(512), 0, st, a, ccap);
+    if (c == 0) hipLaunchKernelGGL(grouped_gemm_kernel<class_fragments(0)>, dim3(blocks), dim3(512), 0, st, a, ccap);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
+}
+
 size_t prefill_scratch_bytes(const RmoeLayer& L, int T) {
   const size_t A = (size_t)T * L.top_k, R = A + T;
   const size_t tiles = A / kBM + L.n_routed + T / kBM + 4;
@@ -1115,7 +1150,7 @@ size_t prefill_scratch_bytes(const RmoeLayer& L, int T) {
          + (size_t)T                                     // x exponents
          + (size_t)T * 3 * sum_planes_gp(L.H / 32) * 2   // x group sums
          + (size_t)T * L.n_routed * 4                    // logits
-         + tiles * 4 + 256 * 12;                         // tile table, counts, carve rounding
+         + kTileClasses * tiles * 4 + 256 * 12;          // tile table, counts, carve rounding
 }
 
 hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, const int32_t* ids_in, const float* wts_in,
@@ -1144,7 +1179,7 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   uint16_t* xsum = (uint16_t*)carve((size_t)T * 3 * Gpx * 2);
   float* logits = (float*)carve((size_t)T * E * 4);
   const int tile_cap = (int)(A / kBM + E + T / kBM + 4);
-  uint32_t* tiles = (uint32_t*)carve((size_t)tile_cap * 4);
+  uint32_t* tiles = (uint32_t*)carve((size_t)kTileClasses * tile_cap * 4);
   int* ntiles = (int*)carve(256);
   hipError_t err;
   const int32_t* ids = ids_in;
@@ -1203,11 +1238,7 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
                        L.Ipad, act, gb, vb, h + A * L.Ipad, hsum + A * 3 * Gph, hexp + A * exp_stride(L.Ipad));
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
-  {
-    const int blocks = (g.n_tiles * tile_cap + 7) / 8 * 8;  // the XCD mapping needs a multiple of 8
-    hipLaunchKernelGGL(grouped_gemm_kernel, dim3(blocks), dim3(512), 0, st, g, tile_cap);
-    if ((err = hipGetLastError()) != hipSuccess) return err;
-  }
+  if ((err = launch_grouped(g, tiles, ntiles, tile_cap, E, st)) != hipSuccess) return err;
   hipLaunchKernelGGL(h_unify_kernel, dim3((unsigned)((R + 255) / 256)), dim3(256), 0, st, h, hexp, (int)R, L.Ipad,
                      hrow);
   if ((err = hipGetLastError()) != hipSuccess) return err;
@@ -1231,11 +1262,7 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   d.out_ld = L.H;
   d.out_ssum = nullptr;
   d.out_exp = nullptr;
-  {
-    const int blocks = (d.n_tiles * tile_cap + 7) / 8 * 8;
-    hipLaunchKernelGGL(grouped_gemm_kernel, dim3(blocks), dim3(512), 0, st, d, tile_cap);
-    if ((err = hipGetLastError()) != hipSuccess) return err;
-  }
+  if ((err = launch_grouped(d, tiles, ntiles, tile_cap, E, st)) != hipSuccess) return err;
   hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, st, D, L.H, ids, wts, s.inv, k, (int)A,
                      residual ? x : nullptr, out, routed, shared_down, 1);
   return hipGetLastError();
