@@ -400,3 +400,53 @@ def test_grouped_operand_ranges(gpu_ctx):
     _check_rows(routed, r_ref, "ranges routed")
     _check_rows(sdown, s_ref, "ranges shared_down")
     lyr.free()
+
+
+def test_prefill_config5_full_size_properties(baseline):
+    """BASELINE config 5 at its full size: 6,700 tokens under Zipf(1.1) expert popularity
+    (a hot expert takes every token, cold ones a handful).  Size-independent properties:
+    a token's output does not depend on the rest of the batch -- a 445-token subset,
+    whose groups fall into other tile classes, reproduces the full run's rows bit for bit
+    (routing included) -- and sampled tokens (hot- and cold-expert ones) match the oracle."""
+    import torch
+
+    import bench
+
+    geom, lyr, bank, spec = baseline
+    T = 6700
+    bias = bench.zipf_bias(geom.n_routed, 0.02, 0)
+    xs = random_tokens(T, geom.hidden, 630)
+    lyr.set_router(spec.weight_bf16, bias=bias, score="softmax")
+    try:
+        lyr.reserve(T)
+        stream = torch.cuda.current_stream()
+
+        def run(x):
+            xd = torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).cuda()
+            out = torch.empty_like(xd)
+            ids = torch.empty((x.shape[0], geom.top_k), dtype=torch.int32, device="cuda")
+            wts = torch.empty((x.shape[0], geom.top_k), dtype=torch.float32, device="cuda")
+            lyr.moe_prefill_dev(xd, x.shape[0], out, ids_dev=ids, wts_dev=wts, stream=stream)
+            torch.cuda.synchronize()
+            return out.cpu().numpy().view(np.uint16), ids.cpu().numpy(), wts.cpu().numpy()
+
+        out, ids, wts = run(xs)
+        hist = np.bincount(ids.reshape(-1), minlength=geom.n_routed)
+        print(f"config 5 histogram: max {hist.max()} min {hist.min()} (>1000: {(hist > 1000).sum()}, <10: {(hist < 10).sum()})")
+        assert hist.max() > 1000
+        sub = np.sort(np.random.default_rng(631).choice(T, 445, replace=False))
+        o2, i2, w2 = run(xs[sub])
+        np.testing.assert_array_equal(i2, ids[sub])
+        np.testing.assert_array_equal(w2, wts[sub])
+        np.testing.assert_array_equal(o2, out[sub])
+        zspec = om.RouterSpec(spec.weight_bf16, geom.top_k, score="softmax", bias=bias)
+        rarest = np.argsort(hist[ids].min(axis=1), kind="stable")[:3]  # tokens of the coldest experts
+        cold = [int(t) for t in rarest]
+        for t in cold + [0, 1, 2]:
+            if routing_margin(xs[t], zspec) <= MARGIN:
+                continue
+            ref, top, _, _ = om.moe_token(bank, zspec, xs[t], None, None, shared_id=geom.shared_id)
+            assert sorted(ids[t].tolist()) == sorted(top.tolist()), t
+            _check(out[t:t + 1], ref[None], f"config 5 token {t}")
+    finally:
+        lyr.set_router(spec.weight_bf16, score="softmax")
