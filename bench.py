@@ -267,6 +267,24 @@ def configs_bench(ctx, layers, geom, seed: int, stream) -> dict:
     wts = torch.full((g.top_k,), 1.0 / g.top_k, dtype=torch.float32, device="cuda")
     us = graph_us(lambda: dl.moe_experts_dev(xd, ids, wts, od, stream=stream), 200, stream)
     b = g.top_k * (dl.gu_expert_bytes + dl.dn_expert_bytes)
+    # the same layer's grouped prefill contract for a chunk of 256 tokens (host entry point,
+    # uploads and read-back included, as moe_experts_grouped serves RaonModel.prefill)
+    Tg = 256
+    xg = np.asarray(rng.standard_normal((Tg, g.hidden)), np.float32)
+    xg = ((xg.view(np.uint32) + 0x8000) >> 16).astype(np.uint16)
+    idg = np.stack([rng.choice(g.n_routed, g.top_k, replace=False) for _ in range(Tg)]).astype(np.int32)
+    wg = np.full((Tg, g.top_k), 1.0 / g.top_k, np.float32)
+    sg = ((np.asarray(rng.standard_normal((Tg, 2 * g.inter)), np.float32).view(np.uint32) + 0x8000) >> 16).astype(np.uint16)
+    dl.reserve(Tg)
+    dl.moe_experts_grouped(xg, idg, wg, sg)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        dl.moe_experts_grouped(xg, idg, wg, sg)
+    gsec = (time.perf_counter() - t0) / 3
+    out["weights_d_grouped_256"] = {
+        "workload": "released-model MoE layer from weights-d bundles, moe_experts_grouped of 256 tokens "
+                    "(routed sums + shared down; host call incl. copies)",
+        "ms_per_layer": round(gsec * 1e3, 3), "tokens_per_s": round(Tg / gsec, 1)}
     out["weights_d_moe_experts"] = {
         "workload": "released-model MoE layer from weights-d bundles (q4nx moe_b1 + bfp16 moe_b2, H=2560, "
                     "I=1088), 6 routed experts of one token (decode_gate_up_kernel + decode_down_kernel)",

@@ -167,7 +167,30 @@ struct DecodeArgs {
   unsigned* cnt_dn;     // [slots, H/64]
   unsigned* cnt_rt;     // [H/64]
   int ks1, ks2;
+  // Tokens: blockIdx.y selects the token; every per-token buffer above is the first
+  // token's and the next token's starts the given number of elements later.
+  size_t tok_part_gu, tok_part_dn, tok_cnt_gu, tok_cnt_dn, tok_h, tok_dout;
 };
+
+// The arguments of token blockIdx.y (a copy with every per-token pointer advanced).
+__device__ __forceinline__ DecodeArgs token_args(const DecodeArgs& a0) {
+  DecodeArgs a = a0;
+  const size_t t = blockIdx.y;
+  if (t == 0) return a;
+  a.x += t * a.H;
+  a.ids += t * a.k;
+  a.wts += t * a.k;
+  a.h += t * a.tok_h;
+  a.dout += t * a.tok_dout;
+  if (a.out) a.out += t * a.H;
+  if (a.out_routed) a.out_routed += t * a.H;
+  a.part_gu += t * a.tok_part_gu;
+  a.part_dn += t * a.tok_part_dn;
+  a.cnt_gu += t * a.tok_cnt_gu;
+  a.cnt_dn += t * a.tok_cnt_dn;
+  a.cnt_rt += t * a.tok_cnt_dn;
+  return a;
+}
 
 __device__ __forceinline__ int slot_expert(const DecodeArgs& a, int s) {
   if (s >= a.k) return a.n_routed;  // shared expert
@@ -208,8 +231,9 @@ __device__ __forceinline__ float tile_accumulate(const uint8_t* tile, int lane, 
   return acc;
 }
 
-// grid slots*(I/64)*ks1, block 256.
-__global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeArgs a) {
+// grid (slots*(I/64)*ks1, tokens), block 256.
+__global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeArgs a0) {
+  const DecodeArgs a = token_args(a0);
   __shared__ uint32_t xs[kMaxRange * 64];
   __shared__ float ssum[kMaxRange * 4];
   __shared__ float red[4][2][64];
@@ -276,7 +300,8 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeArgs a) {
 // grid slots*(H/64)*ks2, block 64*waves.  kFmt: format of the down weights (q4nx, or
 // bfp16 for a weights-d layer whose moe_b2 holds bfp16ebs8 experts).
 template <int kFmt>
-__global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a0) {
+  const DecodeArgs a = token_args(a0);
   __shared__ uint32_t xs[kMaxRange * 64];
   __shared__ float ssum[kMaxRange * 4];
   __shared__ float red[4][64];
@@ -412,16 +437,17 @@ size_t decode_scratch_counters(const RmoeLayer& L) {
 
 hipError_t launch_moe_decode(const RmoeLayer& L, const uint16_t* x, const int32_t* ids, const float* wts, int k,
                              bool with_shared, int act, float gb, float vb, bool residual, uint16_t* out,
-                             uint16_t* out_routed, RmoeScratch& s, hipStream_t st, int stages) {
+                             uint16_t* out_routed, RmoeScratch& s, hipStream_t st, int stages, int ntok) {
   int ks1, ks2;
   decode_splits(L, ks1, ks2);
   const int slots = k + (with_shared ? 1 : 0);
   // A weights-d layer keeps the shared gate/up outside the layer: routed slots only.
   if (with_shared && (L.n_shared < 1 || L.d_layout)) return hipErrorInvalidValue;
+  if (ntok < 1) return hipErrorInvalidValue;
   const size_t nf = (size_t)slots * (L.I / 64) * ks1 * 128 + (size_t)slots * (L.H / 64) * ks2 * 64;
   const size_t nc = (size_t)slots * (L.I / 64) + (size_t)slots * (L.H / 64) + (L.H / 64);
-  if (nf > s.part_floats || nc > s.n_counters || (size_t)slots * L.Ipad > s.h_elems ||
-      (size_t)slots * L.H > s.dout_elems)
+  if (nf * ntok > s.part_floats || nc * ntok > s.n_counters || (size_t)slots * L.Ipad * ntok > s.h_elems ||
+      (size_t)slots * L.H * ntok > s.dout_elems)
     return hipErrorInvalidValue;
   DecodeArgs a{};
   a.gu = L.gu;
@@ -452,19 +478,29 @@ hipError_t launch_moe_decode(const RmoeLayer& L, const uint16_t* x, const int32_
   a.cnt_rt = a.cnt_dn + (size_t)slots * (L.H / 64);
   a.ks1 = ks1;
   a.ks2 = ks2;
+  // Token t's scratch: its partials and counters follow token t-1's (the layout of one
+  // token repeated), its h and expert outputs likewise.
+  a.tok_part_gu = nf;
+  a.tok_part_dn = nf;
+  a.tok_cnt_gu = nc;
+  a.tok_cnt_dn = nc;
+  a.tok_h = (size_t)slots * L.Ipad;
+  a.tok_dout = (size_t)slots * L.H;
   const int nkt1 = L.H / kTileCols, nkt2 = L.Ipad / kTileCols;
   const int per1 = (nkt1 + ks1 - 1) / ks1, per2 = (nkt2 + ks2 - 1) / ks2;
   const int w1 = min(4, 2 * per1), w2 = min(4, per2);
   if (stages & 1) {
-    hipLaunchKernelGGL(decode_gate_up_kernel, dim3(slots * (L.I / 64) * ks1), dim3(64 * w1), 0, st, a);
+    hipLaunchKernelGGL(decode_gate_up_kernel, dim3(slots * (L.I / 64) * ks1, ntok), dim3(64 * w1), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (stages & 2) {
     if (L.dn_fmt == RMOE_FMT_BFP16)
-      hipLaunchKernelGGL(decode_down_kernel<RMOE_FMT_BFP16>, dim3(slots * (L.H / 64) * ks2), dim3(64 * w2), 0, st, a);
+      hipLaunchKernelGGL(decode_down_kernel<RMOE_FMT_BFP16>, dim3(slots * (L.H / 64) * ks2, ntok), dim3(64 * w2), 0,
+                         st, a);
     else
-      hipLaunchKernelGGL(decode_down_kernel<RMOE_FMT_Q4NX>, dim3(slots * (L.H / 64) * ks2), dim3(64 * w2), 0, st, a);
+      hipLaunchKernelGGL(decode_down_kernel<RMOE_FMT_Q4NX>, dim3(slots * (L.H / 64) * ks2, ntok), dim3(64 * w2), 0,
+                         st, a);
     return hipGetLastError();
   }
   return hipSuccess;

@@ -106,12 +106,15 @@ int reserve_layer(rmoe_ctx* ctx, const RmoeLayer& L, int T, int k) {
   linear_needs(2 * L.I, L.H, T, f1, c1);
   linear_needs(L.H, L.Ipad, T, f2, c2);
   Lk.n_shared = 1;
-  const size_t floats = std::max({rmoe::decode_scratch_floats(Lk), f1, f2});
-  const size_t counters = std::max({rmoe::decode_scratch_counters(Lk), c1, c2, (size_t)T});
+  // A weights-d layer's grouped path runs the decode kernels over all T tokens in one
+  // launch: one copy of the decode scratch per token.
+  const size_t dtok = L.d_layout ? (size_t)T : 1;
+  const size_t floats = std::max({rmoe::decode_scratch_floats(Lk) * dtok, f1, f2});
+  const size_t counters = std::max({rmoe::decode_scratch_counters(Lk) * dtok, c1, c2, (size_t)T});
   TRY(grow(s.part, s.part_floats, floats, ctx));
   TRY(grow(s.counters, s.n_counters, counters, ctx));
-  TRY(grow(s.h, s.h_elems, (size_t)(kk + 1) * L.Ipad, ctx));
-  TRY(grow(s.dout, s.dout_elems, (size_t)(kk + 1) * L.H, ctx));
+  TRY(grow(s.h, s.h_elems, (size_t)(kk + 1) * L.Ipad * dtok, ctx));
+  TRY(grow(s.dout, s.dout_elems, (size_t)(kk + 1) * L.H * dtok, ctx));
   size_t re = s.route_elems;
   TRY(grow(s.ids, re, (size_t)T * kk, ctx));
   re = s.route_elems;
@@ -940,6 +943,7 @@ int rmoe_moe_experts_grouped(rmoe_ctx* ctx, int layer, const uint16_t* x, int T,
   if (T < 1) return fail(RMOE_EINVAL, "T must be >= 1");
   if (L->n_shared < 1) return fail(RMOE_EINVAL, "layer %d has no shared expert", layer);
   if (act != RMOE_ACT_SITU && act != RMOE_ACT_SWIGLU) return fail(RMOE_EINVAL, "unknown activation %d", act);
+  if (L->d_layout && T > 65535) return fail(RMOE_EINVAL, "a weights-d layer takes at most 65535 tokens per call");
   TRY(check_ids(top_ids, T, L->top_k, L->n_routed));
   HIP_TRY(hipSetDevice(ctx->device));
   TRY(reserve_layer(ctx, *L, T, L->top_k));
@@ -959,14 +963,12 @@ int rmoe_moe_experts_grouped(rmoe_ctx* ctx, int layer, const uint16_t* x, int T,
   HIP_TRY(hipMemcpyAsync(wd, top_weights, (size_t)T * k * 4, hipMemcpyHostToDevice, ctx->stream));
   HIP_TRY(hipMemcpyAsync(gd, shared_gu, (size_t)T * 2 * L->I * 2, hipMemcpyHostToDevice, ctx->stream));
   if (L->d_layout) {
-    // Weights-d layer: the routed experts of each token run through the decode kernels
-    // (q4nx gate/up, bfp16 down, ordered combine), queued back to back; the shared down
-    // is the bfp16 GEMV of moe_b2's last expert over RTNE(act(shared_gu)).
+    // Weights-d layer: the routed experts of all T tokens run through the decode kernels
+    // (q4nx gate/up, bfp16 down, ordered combine per token) in one launch each; the
+    // shared down is the bfp16 GEMV of moe_b2's last expert over RTNE(act(shared_gu)).
     uint16_t* hd = (uint16_t*)(io + 3 * xb + 2 * ib + gb);
-    for (int t = 0; t < T; ++t)
-      HIP_TRY(rmoe::launch_moe_decode(*L, xd + (size_t)t * L->H, idd + (size_t)t * k, wd + (size_t)t * k, k, false, act,
-                                      gate_beta, value_beta, false, nullptr, rd + (size_t)t * L->H, ctx->s,
-                                      ctx->stream));
+    HIP_TRY(rmoe::launch_moe_decode(*L, xd, idd, wd, k, false, act, gate_beta, value_beta, false, nullptr, rd, ctx->s,
+                                    ctx->stream, 3, T));
     HIP_TRY(rmoe::launch_act_rows(gd, T, L->I, L->Ipad, act, gate_beta, value_beta, hd, ctx->stream));
     HIP_TRY(rmoe::launch_linear_bfp16(L->dn + (size_t)L->n_routed * L->dn_bytes, L->H, L->Ipad, hd, T, sd, ctx->s,
                                       ctx->stream));

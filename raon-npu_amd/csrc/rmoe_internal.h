@@ -324,12 +324,14 @@ hipError_t launch_linear_bfp16(const uint8_t* tiles, int M, int K, const uint16_
 hipError_t launch_route(const RmoeLayer& L, const uint16_t* x, int T, int32_t* ids, float* wts, float* logits,
                         RmoeScratch& s, hipStream_t st);
 
-// Decode MoE: slots = k routed (+ shared); ids/wts on device ([k]); x [H].
+// Decode MoE: slots = k routed (+ shared); ids/wts on device ([k]); x [H].  With ntok > 1
+// the launch covers ntok tokens (x [ntok, H], ids/wts [ntok, k], outputs [ntok, H]), each
+// with its own copy of the one-token scratch.
 // out_routed (may be null) gets RTNE of the routed sum; out gets the full combine
 // (routed + shared, + x when residual).
 hipError_t launch_moe_decode(const RmoeLayer& L, const uint16_t* x, const int32_t* ids, const float* wts, int k,
                              bool with_shared, int act, float gb, float vb, bool residual, uint16_t* out,
-                             uint16_t* out_routed, RmoeScratch& s, hipStream_t st, int stages = 3);
+                             uint16_t* out_routed, RmoeScratch& s, hipStream_t st, int stages = 3, int ntok = 1);
 
 // h[T, Ipad] = RTNE(act(gu[t, :I], gu[t, I:2I])) with zero columns [I, Ipad).
 hipError_t launch_act_rows(const uint16_t* gu, int T, int I, int Ipad, int act, float gb, float vb, uint16_t* h,
