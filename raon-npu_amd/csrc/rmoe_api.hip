@@ -77,6 +77,9 @@ int io_area(rmoe_ctx* ctx, size_t bytes, uint8_t** out) {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// Tokens per launch of a weights-d layer's grouped path (bounds its decode scratch).
+constexpr int kDChunk = 1024;
+
 int check_layer(rmoe_ctx* ctx, int layer, RmoeLayer** out) {
   if (!ctx) return fail(RMOE_EINVAL, "null context");
   auto it = ctx->layers.find(layer);
@@ -106,9 +109,9 @@ int reserve_layer(rmoe_ctx* ctx, const RmoeLayer& L, int T, int k) {
   linear_needs(2 * L.I, L.H, T, f1, c1);
   linear_needs(L.H, L.Ipad, T, f2, c2);
   Lk.n_shared = 1;
-  // A weights-d layer's grouped path runs the decode kernels over all T tokens in one
-  // launch: one copy of the decode scratch per token.
-  const size_t dtok = L.d_layout ? (size_t)T : 1;
+  // A weights-d layer's grouped path runs the decode kernels over up to kDChunk tokens per
+  // launch: one copy of the decode scratch per token of a chunk.
+  const size_t dtok = L.d_layout ? (size_t)std::min(T, kDChunk) : 1;
   const size_t floats = std::max({rmoe::decode_scratch_floats(Lk) * dtok, f1, f2});
   const size_t counters = std::max({rmoe::decode_scratch_counters(Lk) * dtok, c1, c2, (size_t)T});
   TRY(grow(s.part, s.part_floats, floats, ctx));
@@ -943,7 +946,6 @@ int rmoe_moe_experts_grouped(rmoe_ctx* ctx, int layer, const uint16_t* x, int T,
   if (T < 1) return fail(RMOE_EINVAL, "T must be >= 1");
   if (L->n_shared < 1) return fail(RMOE_EINVAL, "layer %d has no shared expert", layer);
   if (act != RMOE_ACT_SITU && act != RMOE_ACT_SWIGLU) return fail(RMOE_EINVAL, "unknown activation %d", act);
-  if (L->d_layout && T > 65535) return fail(RMOE_EINVAL, "a weights-d layer takes at most 65535 tokens per call");
   TRY(check_ids(top_ids, T, L->top_k, L->n_routed));
   HIP_TRY(hipSetDevice(ctx->device));
   TRY(reserve_layer(ctx, *L, T, L->top_k));
@@ -967,8 +969,10 @@ int rmoe_moe_experts_grouped(rmoe_ctx* ctx, int layer, const uint16_t* x, int T,
     // (q4nx gate/up, bfp16 down, ordered combine per token) in one launch each; the
     // shared down is the bfp16 GEMV of moe_b2's last expert over RTNE(act(shared_gu)).
     uint16_t* hd = (uint16_t*)(io + 3 * xb + 2 * ib + gb);
-    HIP_TRY(rmoe::launch_moe_decode(*L, xd, idd, wd, k, false, act, gate_beta, value_beta, false, nullptr, rd, ctx->s,
-                                    ctx->stream, 3, T));
+    for (int t0 = 0; t0 < T; t0 += kDChunk)
+      HIP_TRY(rmoe::launch_moe_decode(*L, xd + (size_t)t0 * L->H, idd + (size_t)t0 * k, wd + (size_t)t0 * k, k, false,
+                                      act, gate_beta, value_beta, false, nullptr, rd + (size_t)t0 * L->H, ctx->s,
+                                      ctx->stream, 3, std::min(kDChunk, T - t0)));
     HIP_TRY(rmoe::launch_act_rows(gd, T, L->I, L->Ipad, act, gate_beta, value_beta, hd, ctx->stream));
     HIP_TRY(rmoe::launch_linear_bfp16(L->dn + (size_t)L->n_routed * L->dn_bytes, L->H, L->Ipad, hd, T, sd, ctx->s,
                                       ctx->stream));

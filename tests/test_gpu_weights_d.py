@@ -240,3 +240,24 @@ def test_moe_experts_dev_matches_host_and_replays(small_d):
         be.moe_experts(970, xs[rep], ids[(rep + 1) % 3], w[rep])  # eager work between replays
     with pytest.raises(ValueError):
         lyr.moe_experts_dev(xd[0], idd[0][:2].contiguous(), wd[0], od[0])
+
+
+def test_d_layer_grouped_across_launch_chunks(small_d):
+    """More tokens than one launch of the weights-d grouped path takes (1,024): rows on both
+    sides of the chunk boundary equal the one-token path bit for bit, and the whole call
+    matches the batched oracle."""
+    be, lyr, geom, bank, _ = small_d
+    T = 1100
+    rng = np.random.default_rng(53)
+    x = random_tokens(T, geom.hidden, 54)
+    ids = np.stack([rng.choice(geom.n_routed, geom.top_k, replace=False) for _ in range(T)]).astype(np.int64)
+    w = rng.uniform(0.1, 1.0, (T, geom.top_k)).astype(np.float32)
+    sgu = random_tokens(T, 2 * geom.inter, 55)
+    routed, sdown = be.moe_experts_grouped(970, x, ids, w, sgu)
+    for t in (0, 1023, 1024, 1099):
+        assert np.array_equal(routed[t], be.moe_experts(970, x[t], ids[t], w[t])), t
+    r_ref, s_ref = om.moe_experts_grouped_batched(bank, x, ids, w, sgu, geom.n_routed)
+    for got, ref, what in ((routed, r_ref, "routed"), (sdown, s_ref, "shared_down")):
+        err, rel, same = compare_bf16(got, ref)
+        print(f"d-layer grouped T={T} {what}: max-abs {err:.3e} rel-L2 {rel:.3e} identical {same:.4f}")
+        assert err <= 1e-2 and rel <= 1e-3
