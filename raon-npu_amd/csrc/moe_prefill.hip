@@ -465,22 +465,12 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
 // while the first two K steps' copies are in flight.  K loop: a three-deep LDS ring
 // filled by global->LDS copies; per K step one barrier, then the copy for step kt+2
 // into the slot step kt-1 used.
+// One (m-tile, n-tile) with MF live 16-row fragments; tl is the tile list of its class.
+// lds / rowidx / row_e are the kernel's shared arrays.
 template <int MF>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void grouped_gemm_kernel(GemmArgs a, int tile_cap) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kGemmLds];
-  __shared__ int rowidx[kBM];
-  __shared__ __attribute__((aligned(16))) int8_t row_e[kBM];  // power-of-two exponent of each tile row  // exponent of each tile row in the first / last K step
-  // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs; each XCD takes a
-  // contiguous eighth of the tiles that exist (the grid is sized for the worst case, the
-  // tile count is known only here), so m-tiles sharing a weight tile meet in the same
-  // L2 and every XCD gets the same share.
-  const int n_act = a.n_tiles * *a.ntiles, per = (n_act + 7) / 8;
-  const int slot8 = blockIdx.x / 8, lid = (blockIdx.x % 8) * per + slot8;
-  if (slot8 >= per || lid >= n_act) return;
-  // m-tile major: the n-tiles of one m-tile (sharing the gathered rows) and consecutive
-  // m-tiles of one expert (sharing its weights) run back to back on one XCD.
-  const int mt = lid / a.n_tiles, nt = lid % a.n_tiles;
-  const uint32_t te = a.tiles[mt];
+__device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint32_t* __restrict__ tl, int mt, int nt,
+                                          uint8_t* lds, int* rowidx, int8_t* row_e) {
+  const uint32_t te = tl[mt];
   const int e = (int)(te & 511u), row0 = (int)(te >> 9);
   const int rend = group_end(a, e);
   const int nrows = min(kBM, rend - row0);
@@ -930,6 +920,52 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
+// Grid: per class in kMask (bit c: class c), 8 x ceil(n_tiles * tiles / 8) workgroups;
+// 512 threads.  Class c's tile count sits in ntiles[c], its tiles at tiles + c * cap.
+// All three classes share one launch (kMask = 7): separate launches leave the chip
+// idle in each launch's tail, which costs a mid-size prefill (445 tokens) ~20 %.
+template <int kMask>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void grouped_gemm_kernel(GemmArgs a, int cap) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kGemmLds];
+  __shared__ int rowidx[kBM];
+  __shared__ __attribute__((aligned(16))) int8_t row_e[kBM];  // power-of-two exponent of each tile row
+  // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs; each XCD takes a
+  // contiguous eighth of every class's tiles (the grid is sized for the worst case, the
+  // tile counts are known only here), so m-tiles sharing a weight tile meet in the same
+  // L2 and every XCD gets the same share of each class.  Within an XCD the workgroups
+  // take the 8-fragment tiles first, then the 4- and 2-fragment ones.
+  // m-tile major: the n-tiles of one m-tile (sharing the gathered rows) and consecutive
+  // m-tiles of one expert (sharing its weights) run back to back on one XCD.
+  const int xcd = blockIdx.x % 8;
+  const int n2 = (kMask & 4) ? a.n_tiles * a.ntiles[2] : 0;
+  const int n1 = (kMask & 2) ? a.n_tiles * a.ntiles[1] : 0;
+  const int n0 = (kMask & 1) ? a.n_tiles * a.ntiles[0] : 0;
+  const int p2 = (n2 + 7) / 8, p1 = (n1 + 7) / 8, p0 = (n0 + 7) / 8;
+  int j = blockIdx.x / 8, c, per, n;
+  if (j < p2) {
+    c = 2, per = p2, n = n2;
+  } else if ((j -= p2) < p1) {
+    c = 1, per = p1, n = n1;
+  } else if ((j -= p1) < p0) {
+    c = 0, per = p0, n = n0;
+  } else {
+    return;
+  }
+  const int lid = xcd * per + j;
+  if (lid >= n) return;
+  const int mt = lid / a.n_tiles, nt = lid % a.n_tiles;
+  const uint32_t* tl = a.tiles + (size_t)c * cap;
+  if constexpr ((kMask & 4) != 0) {
+    if (c == 2) gemm_tile<class_fragments(2)>(a, tl, mt, nt, lds, rowidx, row_e);
+  }
+  if constexpr ((kMask & 3) != 0) {
+    if (c == 1)
+      gemm_tile<class_fragments(1)>(a, tl, mt, nt, lds, rowidx, row_e);
+    else if (c == 0)
+      gemm_tile<class_fragments(0)>(a, tl, mt, nt, lds, rowidx, row_e);
+  }
+}
+
 // ---------------------------------------------------------------- combine --
 // out[t] = RTNE(RTNE(sum_{routes by ascending expert} f32(D[inv[t,r]]) * w[t,r]) + D_shared[t])
 // (+ x[t] with residual); optionally also the routed and shared rows separately.
@@ -1122,21 +1158,16 @@ hipError_t launch_topk(const float* logits, int T, int E, int k, int score, cons
   return hipGetLastError();
 }
 
-// The grouped GEMM over the three tile classes, largest first: one launch per class,
-// each grid sized for the class's worst case (a class-0/1 tile is a group's last).
+// The grouped GEMM over the tiles of all three classes in one launch; the grid is sized
+// for the worst case (a class-0/1 tile is a group's last, so at most one per group),
+// 8 x ceil(tiles / 8) workgroups per class (the XCD mapping deals each class in eighths).
 static hipError_t launch_grouped(GemmArgs a, uint32_t* tiles, int* ntiles, int cap, int n_routed, hipStream_t st) {
-  for (int c = kTileClasses - 1; c >= 0; --c) {
-    a.tiles = tiles + (size_t)c * cap;
-    a.ntiles = ntiles + c;
-    const int ccap = c == kTileClasses - 1 ? cap : min(cap, n_routed + 1);
-    const int blocks = (a.n_tiles * ccap + 7) / 8 * 8;  // the XCD mapping needs a multiple of 8
-    if (c == 2) hipLaunchKernelGGL(grouped_gemm_kernel<class_fragments(2)>, dim3(blocks), dim3(512), 0, st, a, ccap);
-    if (c == 1) hipLaunchKernelGGL(grouped_gemm_kernel<class_fragments(1)>, dim3(blocks), dim3(512), 0, st, a, ccap);
-    if (c == 0) hipLaunchKernelGGL(grouped_gemm_kernel<class_fragments(0)>, dim3(blocks), dim3(512), 0, st, a, ccap);
-    const hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
-  }
-  return hipSuccess;
+  a.tiles = tiles;
+  a.ntiles = ntiles;
+  const int small = min(cap, n_routed + 1);
+  const int blocks = 8 * ((a.n_tiles * cap + 7) / 8 + 2 * ((a.n_tiles * small + 7) / 8));
+  hipLaunchKernelGGL(grouped_gemm_kernel<7>, dim3(blocks), dim3(512), 0, st, a, cap);
+  return hipGetLastError();
 }
 
 size_t prefill_scratch_bytes(const RmoeLayer& L, int T) {
