@@ -179,3 +179,105 @@ def test_reader_hashes_and_rejects_mismatch(tmp_path):
     with pytest.raises(ValueError, match="Short read"):
         r.read(data.size + 1)
     r.close()
+
+
+class _FakeLayer:
+    def __init__(self, log, layer, geom):
+        self.log, self.layer, self.geom = log, layer, geom
+        self.gu_expert_bytes = geom.gu_bytes
+        self.dn_expert_bytes = geom.hidden * geom.inter_pad * 9 // 8
+        self.uploads = []
+
+    def upload_d(self, bundle, expert0, data):
+        self.uploads.append((bundle, expert0, bytes(data)))
+
+    def set_router(self, *a):
+        self.log.append(("router", self.layer) + a)
+
+    def free(self):
+        self.log.append(("free", self.layer))
+
+
+class _FakeCtx:
+    def __init__(self, log):
+        self.log, self.layers = log, []
+
+    def create_layer_d(self, layer, geom):
+        lyr = _FakeLayer(self.log, layer, geom)
+        self.layers.append(lyr)
+        return lyr
+
+
+class _FakeBackend:
+    """Records what the loader registers (the host logic of GpuBackend.load_weights_d)."""
+
+    def __init__(self):
+        self.log = []
+        self.ctx = _FakeCtx(self.log)
+        self._layers, self.bundles, self.components = {}, {}, {}
+
+    def register_bundle(self, name, data, M, K, fmt):
+        self.bundles[name] = (bytes(data), M, K, fmt)
+
+    def register_component(self, name, bundle, r0, r1, orig_k=None):
+        self.components[name] = (bundle, r0, r1, orig_k)
+
+
+@pytest.fixture(scope="module")
+def real_dir(tmp_path_factory):
+    """L02's MoE bundles and L00's dense pair as real files (random bytes: the loader only
+    moves them) with a manifest that leaves the other bundles out."""
+    from weights_d_fixtures import manifest_entry
+
+    root = tmp_path_factory.mktemp("weights_d_real")
+    comps, bundles = W.canonical_specs()
+    rng = np.random.default_rng(9)
+    data, entries = {}, []
+    for name in ("L02/moe_b1", "L02/moe_b2", "L02/shared_gu", "L00/dense_gu", "L00/dense_down"):
+        buf = rng.integers(0, 256, W.canonical_size(bundles[name])[0], dtype=np.uint8)
+        sha = write_bundle(root, bundles[name], buf)
+        data[name] = buf
+        entries.append(manifest_entry(bundles[name], comps, bundles[name].rel_file, sha))
+    write_manifest(root, entries)
+    return root, data
+
+
+def test_loader_host_logic(real_dir):
+    tmp_path, data = real_dir
+    be = _FakeBackend()
+    w = np.zeros((128, 2560), np.uint16)
+    info = W.load_weights_d(be, tmp_path, require_complete=False, experts_per_read=40,
+                            routers={2: (w, None)}, routed_scaling_factor=2.5)
+    assert sorted(info["loaded"]) == sorted(["L02/moe_b1", "L02/moe_b2", "L02/shared_gu", "L00/dense_gu",
+                                            "L00/dense_down"])
+    lyr = be._layers[2]
+    # moe_b1 then moe_b2, streamed in slices of 40 experts, reassembling the files exactly
+    b1 = b"".join(d for b, _, d in lyr.uploads if b == 1)
+    b2 = b"".join(d for b, _, d in lyr.uploads if b == 2)
+    assert b1 == data["L02/moe_b1"].tobytes() and b2 == data["L02/moe_b2"].tobytes()
+    assert [e0 for b, e0, _ in lyr.uploads if b == 2] == [0, 40, 80, 120]
+    # the shared down is moe_b2's expert 128, a dense bfp16 [2560, 1280] served with K_in = 1088
+    sd, M, K, fmt = be.bundles["L02/shared_down"]
+    assert sd == data["L02/moe_b2"][128 * 3686400:].tobytes() and (M, K, fmt) == (2560, 1280, "bfp16_gemv")
+    assert be.components["model.layers.2.moe.shared_experts.down_proj.weight"] == ("L02/shared_down", 0, 2560, 1088)
+    assert be.components["model.layers.2.moe.shared_experts.up_proj.weight"] == ("L02/shared_gu", 1088, 2176, 2560)
+    assert be.bundles["L00/dense_gu"][1:] == (24064, 2560, "q4nx_gemv")
+    assert be.components["model.layers.0.mlp.down_proj.weight"] == ("L00/dense_down", 0, 2560, 12032)
+    assert ("router", 2, w, None, "sigmoid", True, 2.5) in be.log
+
+
+def test_loader_rejects_corrupt_expert_bundle(real_dir):
+    tmp_path, data = real_dir
+    path = tmp_path / "L02" / "moe_b2.bin"
+    bad = data["L02/moe_b2"].copy()
+    bad[7] ^= 1
+    path.write_bytes(bad.tobytes())
+    try:
+        be = _FakeBackend()
+        with pytest.raises(ValueError, match="sha256 mismatch for L02/moe_b2"):
+            W.load_weights_d(be, tmp_path, require_complete=False)
+        assert 2 not in be._layers and ("free", 2) in be.log
+    finally:
+        path.write_bytes(data["L02/moe_b2"].tobytes())
+    with pytest.raises(ValueError, match="not a MoE layer"):
+        W.load_weights_d(_FakeBackend(), tmp_path, require_complete=False, layers=[0])
