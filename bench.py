@@ -6,7 +6,7 @@ shape (H=2048, I=768, 128 routed experts + 1 shared, softmax top-8, SwiGLU, q4nx
 weights N(0, 0.02)), residual add between layers, batch 1.  One step = one token
 through all 48 layers in ONE persistent launch (router on the device, 8 routed +
 shared experts, ordered fp32 combine, residual).  Weights are synthesized and
-quantized on the GPU (seeded per layer); inputs are random N(0, 1) hidden states,
+quantized on the GPU (seeded per layer); inputs are random N(0, 0.25^2) hidden states,
 one per step, resident in HBM.
 
 Printed: one JSON line with tokens/s, the roofline of the dominant kernel (the
@@ -27,6 +27,12 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
+# Scale of the random hidden states of the 48-layer stack.  The stack adds each layer's
+# MoE output to its input with no normalisation and SwiGLU is quadratic in its input: with
+# N(0, 0.02) weights the stream grows by ~0.34 sigma^2 per layer, so N(0, 1) states
+# overflow to non-finite values after ~20 layers (and route every token to experts 0..7
+# from there on), while N(0, 0.25^2) states stay finite through 48 layers.
+STACK_HIDDEN_STD = 0.25
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 # HBM bytes per launch of the decode stack kernel measured with rocprofv3 FETCH_SIZE and
@@ -46,7 +52,7 @@ def log(msg: str) -> None:
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256, help="timed decode steps (tokens)")
+    ap.add_argument("--steps", type=int, default=256, help="timed decode steps (tokens); exactly this many")
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the oracle CPU sample")
@@ -80,17 +86,18 @@ def build_stack(ctx, geom, n_layers: int, seed: int):
 
 
 def decode_graph(ctx, layers, x_pool, out_pool, stream, n_launch: int):
-    """A HIP graph of n_launch decode steps: step i carries token x_pool[i] through every
-    layer in ONE persistent launch and writes out_pool[i]."""
+    """A HIP graph of n_launch decode steps: step i carries token x_pool[i % P] through
+    every layer in ONE persistent launch and writes out_pool[i % P]."""
     import torch
 
+    P = x_pool.shape[0]
     g = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
         ctx.decode_stack_dev(layers, x_pool[0], out_pool[0], residual=True, stream=stream)  # warm
         torch.cuda.synchronize()
         with torch.cuda.graph(g, stream=stream):
             for i in range(n_launch):
-                ctx.decode_stack_dev(layers, x_pool[i], out_pool[i], residual=True, stream=stream)
+                ctx.decode_stack_dev(layers, x_pool[i % P], out_pool[i % P], residual=True, stream=stream)
     return g
 
 
@@ -220,9 +227,11 @@ def configs_bench(ctx, layers, geom, seed: int, stream) -> dict:
     x = torch.randn(1, 2048, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
     y = torch.empty(1, 768, dtype=torch.int16, device="cuda")
     us = graph_us(lambda: mat.linear_dev(x, 1, y, stream=stream), 1000, stream)
-    b = 990208  # weights 983,040 + x 4,096 + y 3,072
+    b = 990208  # weights 983,040 + x 4,096 + y 3,072 (per-call algorithmic bytes)
     out["config1_gemv"] = {"workload": "q4nx GEMV [768, 2048] x 1 token, 1000 launches in a graph",
-                           "us_per_launch": round(us, 3), "GBps": round(b / us / 1e3, 1)}
+                           "us_per_launch": round(us, 3), "GBps": round(b / us / 1e3, 1),
+                           "frac_hbm_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+    out["_config1_bytes"] = mat.download()
     mat.free()
     # config 2: one decode layer (router + 8 routed + shared + combine), one persistent launch
     x1 = torch.randn(geom.hidden, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
@@ -244,7 +253,8 @@ def configs_bench(ctx, layers, geom, seed: int, stream) -> dict:
     wb = geom.n_experts * geom.expert_bytes
     out["config3_prefill_445"] = {"workload": "one BASELINE prefill layer, 445 tokens, softmax top-8 routing",
                                   "ms_per_layer": round(us / 1e3, 4), "tflops": round(fl / us / 1e6, 2),
-                                  "weight_GBps": round(wb / us / 1e3, 1)}
+                                  "weight_GBps": round(wb / us / 1e3, 1),
+                                  "frac_hbm_peak": round(wb / us / 1e3 / HBM_PEAK_GBS, 4)}
     # weights-d layer: moe_b1 (q4nx) + moe_b2 (bfp16) at H=2560, I=1088, 128+1 experts, top-6
     g = RAON_1_MINI
     rng = np.random.default_rng(seed + 23)
@@ -294,39 +304,163 @@ def configs_bench(ctx, layers, geom, seed: int, stream) -> dict:
     return out
 
 
-def cpu_baseline(lyr, geom, budget_s: float, seed: int):
-    """The NumPy oracle (reference CPU path, DWeights-style per-call dequant with an LRU of
-    32 experts) on this host: seconds per token-layer, extrapolated to the 48-layer stack."""
-    import numpy as np
-    from oracle import moe as om
-
+def _blas_threads() -> int:
     try:
         from threadpoolctl import threadpool_info
 
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        return max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
     except Exception:
-        threads = os.cpu_count() or 1
-    parts = [lyr.download_expert(e) for e in range(geom.n_experts)]
-    bank = om.ExpertBank(b"".join(p[0] for p in parts), b"".join(p[1] for p in parts), geom.n_experts,
-                         geom.hidden, geom.inter, cache=32)
-    import torch
+        return 1
 
-    gen = torch.Generator(device="cuda").manual_seed(seed * 1000)
-    rw = (torch.randn(geom.n_routed, geom.hidden, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
-    spec = om.RouterSpec(rw.view(torch.int16).cpu().numpy().view(np.uint16), geom.top_k, score="softmax")
-    wf = spec.weight_f32()
-    rng = np.random.default_rng(seed)
+
+def _timed_loop(fn, budget_s: float, min_n: int = 2) -> tuple[float, int]:
+    """Seconds per call of fn() over at least min_n calls and about budget_s seconds."""
     n, t0 = 0, time.perf_counter()
     while True:
-        x = om.f32_to_bf16(rng.standard_normal(geom.hidden).astype(np.float32))
-        out, *_ = om.moe_token(bank, spec, x, None, None, shared_id=geom.shared_id, router_w_f32=wf)
-        om.f32_to_bf16(om.bf16_to_f32(x) + om.bf16_to_f32(out))
+        fn(n)
         n += 1
         el = time.perf_counter() - t0
-        if el >= budget_s and n >= 2:
-            break
-    per_layer = el / n
-    return per_layer, n, threads
+        if el >= budget_s and n >= min_n:
+            return el / n, n
+
+
+def cpu_legs(layer0, geom, cfg1_bytes: bytes, args) -> dict:
+    """The reference CPU path restated by the oracle (test infrastructure), timed on this
+    host's cores beside the GPU figures, in two variants:
+
+    * "per_call_dequant" -- reference-faithful: the selected experts' q4nx bytes are
+      parsed and dequantized when used, with the DWeights LRU of 32 experts
+      (npu/backend.py:940-1058, 1246-1273), then NumpyBackend's fp32 GEMVs
+      (host/backend.py:402-417, 466-510) and RaonModel._moe_token (host/raon.py:1288-1330);
+    * "predequantized" -- the CPU's best case: every expert held as fp32 (dequantized
+      before timing), the same token-serial GEMVs.
+
+    Each with all BLAS threads and with one.  Configs 1-3 use the layer-0 weights of the
+    decode stack, config 4 extrapolates a token-layer x48 (every layer costs the same), and
+    config 5 is timed once with per-expert GEMMs over the whole 6,700-token batch
+    (pre-dequantized) -- the reference CPU path itself is token-serial and is given per
+    token instead.  Returns per-config figures and the headline (config 4) baseline."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+
+    from oracle import moe as om
+    from oracle.bf16 import f32_to_bf16
+    from oracle.q4nx import dequantize_grouped, dequantize_simple, parse_gemv
+
+    nthr = _blas_threads()
+    hostinfo = {"os_cpu_count": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)), "blas_threads": nthr}
+    budget = args.cpu_seconds
+    rng = np.random.default_rng(args.seed + 31)
+    out: dict = {"host": hostinfo}
+
+    # config 1: one q4nx GEMV [768, 2048] (990,208 algorithmic bytes per call)
+    x1 = f32_to_bf16(rng.standard_normal(2048).astype(np.float32))
+    w_pre = dequantize_simple(*parse_gemv(cfg1_bytes, K=2048, M=768))
+    c1 = {}
+    for tag, threads in (("all_threads", nthr), ("one_thread", 1)):
+        with threadpool_limits(threads):
+            per_i, _ = _timed_loop(lambda i: om.linear(dequantize_simple(*parse_gemv(cfg1_bytes, K=2048, M=768)), x1),
+                                   budget / 12)
+            per_p, _ = _timed_loop(lambda i: om.linear(w_pre, x1), budget / 12, min_n=20)
+        c1[tag] = {"per_call_dequant": {"us_per_call": round(per_i * 1e6, 1), "GBps": round(990208 / per_i / 1e9, 3)},
+                   "predequantized": {"us_per_call": round(per_p * 1e6, 1), "GBps": round(990208 / per_p / 1e9, 3)}}
+    out["config1"] = c1
+
+    # the layer: router from build_stack's seed, experts read back from the device
+    gen = torch.Generator(device="cuda").manual_seed(args.seed * 1000)
+    rw = (torch.randn(geom.n_routed, geom.hidden, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+    router = rw.view(torch.int16).cpu().numpy().view(np.uint16)
+    spec = om.RouterSpec(router, geom.top_k, score="softmax")
+    wf = spec.weight_f32()
+    parts = [layer0.download_expert(e) for e in range(geom.n_experts)]
+    gu_all, dn_all = b"".join(p[0] for p in parts), b"".join(p[1] for p in parts)
+    del parts
+    xs = f32_to_bf16(rng.standard_normal((445, geom.hidden)).astype(np.float32))
+
+    def token(bank, i):
+        x = xs[i % xs.shape[0]]
+        o, *_ = om.moe_token(bank, spec, x, None, None, shared_id=geom.shared_id, router_w_f32=wf)
+        return o
+
+    # variant (i): per-call dequant with an LRU of 32 experts
+    faithful = {}
+    for tag, threads, bud in (("all_threads", nthr, budget), ("one_thread", 1, budget / 2)):
+        bank = om.ExpertBank(gu_all, dn_all, geom.n_experts, geom.hidden, geom.inter, cache=32)
+        with threadpool_limits(threads):
+            per, n = _timed_loop(lambda i: token(bank, i), bud)
+        faithful[tag] = (per, n)
+    # variant (ii): every expert dequantized to fp32 before timing
+    bank_pre = om.ExpertBank(gu_all, dn_all, geom.n_experts, geom.hidden, geom.inter, cache=geom.n_experts)
+    for e in range(geom.n_experts):
+        gu = bank_pre.gate_up[e * bank_pre.gu_bytes:(e + 1) * bank_pre.gu_bytes]
+        w = dequantize_grouped(*parse_gemv(gu, K=geom.hidden, M=2 * geom.inter))
+        dn = bank_pre.down[e * bank_pre.dn_bytes:(e + 1) * bank_pre.dn_bytes]
+        d = dequantize_grouped(*parse_gemv(dn, K=geom.inter_pad, M=geom.hidden))[:, : geom.inter]
+        bank_pre._cache[e] = (np.ascontiguousarray(w[: geom.inter]), np.ascontiguousarray(w[geom.inter:]),
+                              np.ascontiguousarray(d))
+    with threadpool_limits(nthr):
+        t0 = time.perf_counter()
+        for i in range(xs.shape[0]):  # config 3 in full: 445 tokens, token-serial
+            token(bank_pre, i)
+        pre_all = ((time.perf_counter() - t0) / xs.shape[0], xs.shape[0])
+    with threadpool_limits(1):
+        pre_one = _timed_loop(lambda i: token(bank_pre, i), budget / 4)
+    pre = {"all_threads": pre_all, "one_thread": pre_one}
+
+    layer_bytes = geom.decode_bytes()
+    fl3 = 445 * (geom.top_k + 1) * geom.flops_per_assignment + 2 * 445 * geom.hidden * geom.n_routed
+
+    def per_layer(per, n, how):
+        return {"us_per_layer": round(per * 1e6, 1), "GBps": round(layer_bytes / per / 1e9, 4), "tokens": n,
+                "timed": how}
+
+    out["config2"] = {tag: {"per_call_dequant": per_layer(*faithful[tag], "token sample"),
+                            "predequantized": per_layer(*pre[tag], "445 tokens" if tag == "all_threads"
+                                                        else "token sample")} for tag in faithful}
+
+    def prefill(per, n, how):
+        return {"ms_per_layer": round(per * 445 * 1e3, 2), "tflops": round(fl3 / (per * 445) / 1e12, 6),
+                "timed": how}
+
+    out["config3"] = {tag: {"per_call_dequant": prefill(*faithful[tag], f"{faithful[tag][1]} tokens, x445"),
+                            "predequantized": prefill(*pre[tag], "all 445 tokens" if tag == "all_threads"
+                                                      else f"{pre[tag][1]} tokens, x445")} for tag in faithful}
+    out["config4"] = {tag: {"per_call_dequant": {"tokens_per_s": round(1.0 / (faithful[tag][0] * args.layers), 5)},
+                            "predequantized": {"tokens_per_s": round(1.0 / (pre[tag][0] * args.layers), 5)}}
+                      for tag in faithful}
+
+    # config 5 once: 6,700 Zipf-routed tokens, per-expert GEMMs on the pre-dequantized bank
+    T5 = args.prefill_tokens
+    zspec = om.RouterSpec(router, geom.top_k, score="softmax", bias=zipf_bias(geom.n_routed, args.zipf_tau, args.seed))
+    x5 = f32_to_bf16(rng.standard_normal((T5, geom.hidden)).astype(np.float32))
+    fl5 = T5 * (geom.top_k + 1) * geom.flops_per_assignment + 2 * T5 * geom.hidden * geom.n_routed
+    with threadpool_limits(nthr):
+        t0 = time.perf_counter()
+        om.prefill_layer(bank_pre, zspec, x5, geom.shared_id, None, None, batched=True)
+        s5 = time.perf_counter() - t0
+    out["config5"] = {"all_threads": {
+        "predequantized_grouped_gemm": {"ms_per_layer": round(s5 * 1e3, 1), "tflops": round(fl5 / s5 / 1e12, 5),
+                                        "timed": "once, whole batch"},
+        "per_call_dequant": {"ms_per_layer": round(faithful["all_threads"][0] * T5 * 1e3, 1),
+                             "tflops": round(fl5 / (faithful["all_threads"][0] * T5) / 1e12, 7),
+                             "timed": f"{faithful['all_threads'][1]} tokens, x{T5} (token-serial reference path)"}}}
+    per_f, n_f = faithful["all_threads"]
+    headline = {
+        "value": round(1.0 / (per_f * args.layers), 5),
+        "unit": "tokens/s",
+        "cores": nthr,
+        "kind": "port",
+        "sample": (f"NumPy oracle of the reference CPU path (route_token + moe_experts + shared + combine, "
+                   f"per-call dequant with the DWeights LRU of 32) on {n_f} tokens through layer 0 "
+                   f"({per_f * 1e3:.1f} ms per token-layer, {nthr} BLAS threads), extrapolated x{args.layers} layers; "
+                   f"one thread: {faithful['one_thread'][0] * 1e3:.1f} ms per token-layer; host "
+                   f"os.cpu_count()={hostinfo['os_cpu_count']}, usable CPUs {hostinfo['affinity_cpus']}"),
+        "one_thread_value": round(1.0 / (faithful["one_thread"][0] * args.layers), 5),
+        "predequantized_value": round(1.0 / (pre["all_threads"][0] * args.layers), 5),
+        **hostinfo,
+    }
+    return {"headline": headline, "configs": out}
 
 
 def profile_pass(ctx, layers, geom, args, stream, gen) -> int:
@@ -343,7 +477,8 @@ def profile_pass(ctx, layers, geom, args, stream, gen) -> int:
         dst.copy_(src)
     torch.cuda.synchronize()
     del src, dst
-    x = torch.randn(2, geom.hidden, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
+    x = (torch.randn(2, geom.hidden, device="cuda", generator=gen) * STACK_HIDDEN_STD).to(torch.bfloat16)
+    x = x.view(torch.int16)
     out = torch.empty_like(x)
     ctx.reserve_decode_stack(layers)
     for i in range(2):
@@ -384,25 +519,37 @@ def main() -> int:
     gen = torch.Generator(device="cuda").manual_seed(args.seed + 7)
     if args.profile_pass:
         return profile_pass(ctx, layers, geom, args, stream, gen)
-    n_launch = 32
-    x_pool = torch.randn(n_launch, geom.hidden, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
+    K, W = max(1, args.steps), max(0, args.warmup)
+    P = min(32, K)  # distinct tokens, resident in HBM; launch i carries token i % P
+    x_pool = (torch.randn(P, geom.hidden, device="cuda", generator=gen) * STACK_HIDDEN_STD).to(torch.bfloat16)
+    x_pool = x_pool.view(torch.int16)
     out_pool = torch.empty_like(x_pool)
     ctx.reserve_decode_stack(layers)
-    g = decode_graph(ctx, layers, x_pool, out_pool, stream, n_launch)
-    log(f"decode graph of {n_launch} steps captured (one persistent launch per step)")
-
-    reps_w = max(1, (args.warmup + n_launch - 1) // n_launch)
-    reps = max(1, (args.steps + n_launch - 1) // n_launch)
-    with torch.cuda.stream(stream):
-        for _ in range(reps_w):
-            g.replay()
+    g = decode_graph(ctx, layers, x_pool, out_pool, stream, K)
+    gw = decode_graph(ctx, layers, x_pool, out_pool, stream, W) if W else None
+    log(f"decode graphs captured: {W} warmup + {K} timed steps (one persistent launch per step)")
+    if gw is not None:
+        with torch.cuda.stream(stream):
+            gw.replay()
     torch.cuda.synchronize()
-    secs = time_graph(g, reps, stream)
-    steps = reps * n_launch
+    secs = time_graph(g, 1, stream)
+    steps = K
     tok_s = steps / secs
     ms_per_step = secs * 1e3 / steps
     bytes_per_token = args.layers * geom.decode_bytes()
     log(f"decode: {tok_s:.1f} tok/s, {ms_per_step:.4f} ms/token, {bytes_per_token * tok_s / 1e9:.1f} GB/s")
+    # The timed launches' outputs must equal eager launches on the same tokens.
+    check_ids = sorted({0, P - 1})
+    eager = torch.empty_like(x_pool[0])
+    with torch.cuda.stream(stream):
+        for i in check_ids:
+            ctx.decode_stack_dev(layers, x_pool[i], eager, residual=True, stream=stream)
+            torch.cuda.synchronize()
+            if not torch.equal(eager, out_pool[i]):
+                raise RuntimeError(f"decode step {i}: timed graph output differs from an eager launch")
+    if not torch.isfinite(out_pool.view(torch.bfloat16).float()).all():
+        raise RuntimeError("the residual stream overflowed: non-finite decode outputs")
+    log(f"timed outputs of tokens {check_ids} equal eager launches; all outputs finite")
     # The dominant kernel is the persistent decode kernel itself (one launch per step):
     # its average duration is the step time measured above.
     per_launch = secs / steps
@@ -432,7 +579,8 @@ def main() -> int:
     if not args.no_configs:
         configs = configs_bench(ctx, layers, geom, args.seed, stream)
         for k, v in configs.items():
-            log(f"{k}: {v}")
+            if not k.startswith("_"):
+                log(f"{k}: {v}")
 
     lm_head = None
     if not args.no_lm_head:
@@ -441,17 +589,28 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu:
-        per_layer, n, threads = cpu_baseline(layers[0], geom, args.cpu_seconds, args.seed)
-        cpu = {
-            "value": round(1.0 / (per_layer * args.layers), 4),
-            "unit": "tokens/s",
-            "cores": threads,
-            "kind": "port",
-            "sample": (f"NumPy oracle of the reference CPU path (route_token + moe_experts + shared + combine, "
-                       f"DWeights-style dequant with LRU 32) on {n} tokens through layer 0 "
-                       f"({per_layer * 1e3:.1f} ms per token-layer), extrapolated x{args.layers} layers"),
-        }
-        log(f"cpu baseline: {cpu['value']} tok/s ({per_layer * 1e3:.1f} ms/token-layer, {threads} BLAS threads)")
+        cfg1 = configs.pop("_config1_bytes", None) if configs else None
+        if cfg1 is None:
+            import torch as _t
+
+            w = _t.randn(768, 2048, device="cuda", generator=_t.Generator(device="cuda").manual_seed(args.seed + 21)) * 0.02
+            m = ctx.quantize_matrix(w, 768, 2048)
+            cfg1 = m.download()
+            m.free()
+        legs = cpu_legs(layers[0], geom, cfg1, args)
+        cpu = legs["headline"]
+        if configs:
+            c = legs["configs"]
+            configs["config1_gemv"]["cpu"] = c["config1"]
+            configs["config2_decode_layer"]["cpu"] = c["config2"]
+            configs["config3_prefill_445"]["cpu"] = c["config3"]
+        cpu["configs"] = {k: legs["configs"][k] for k in ("config4", "config5")}
+        if prefill is not None:
+            prefill["cpu"] = legs["configs"]["config5"]
+        log(f"cpu baseline: {cpu['value']} tok/s ({cpu['cores']} BLAS threads; one thread {cpu['one_thread_value']}, "
+            f"pre-dequantized {cpu['predequantized_value']})")
+    elif configs:
+        configs.pop("_config1_bytes", None)
 
     line = {
         "metric": "MoE decode tokens/s (48-layer q4nx stack, batch 1); prefill grouped-GEMM TFLOP/s in 'prefill'",
@@ -459,13 +618,13 @@ def main() -> int:
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": reps_w * n_launch,
+        "warmup": W,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,0.02) q4nx weights generated on the GPU; N(0,1) hidden states)",
+        "data": "synthetic (seeded N(0,0.02) q4nx weights generated on the GPU; N(0,0.25^2) hidden states)",
         "config": {
             "workload": "BASELINE config 4: 48-layer decode, batch 1",
             "layers": args.layers,

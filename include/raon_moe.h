@@ -135,6 +135,20 @@ int rmoe_layer_upload_experts(rmoe_ctx* ctx, int layer, const void* gate_up, siz
 #define RMOE_PART_DOWN 2
 int rmoe_layer_upload_expert_q4k(rmoe_ctx* ctx, int layer, int expert, int part, const void* q4k_bytes,
                                  size_t nbytes);
+/* A matrix handle that views one expert's weights in place (no copy, no upload):
+ * part RMOE_PART_GATE_UP gives the expert's gate/up [2I, H] (q4nx; gate rows, then up
+ * rows), RMOE_PART_DOWN its down [H, Ipad] (q4nx, or bfp16 in a weights-d layer; input
+ * columns past I are the zero padding).  The handle is served by rmoe_linear /
+ * rmoe_linear_dev / rmoe_matrix_download like an uploaded matrix; rmoe_matrix_free drops
+ * the handle only, and freeing or re-creating the layer invalidates it.  Replaces the
+ * component lookup that serves the shared expert's projections
+ * model.layers.{L}.moe.shared_experts.{gate,up,down}_proj.weight by name
+ * (npu/backend.py:360-392 specs, :3575-3609 lookup; called by RaonModel._moe_token,
+ * host/raon.py:1314-1323, and the prefill shared precompute, :1570-1577) -- here from the
+ * shared expert that a q4nx layer holds as expert n_routed (kernels/moe/pack.py:40-44),
+ * or from moe_b2's last expert in a weights-d layer (npu/backend.py:4068-4107). */
+#define RMOE_PART_GATE_UP 3
+int rmoe_layer_expert_matrix(rmoe_ctx* ctx, int layer, int expert, int part, int* handle);
 /* Quantize one expert from fp32 device weights (gate_up [2I, H], down [H, I] row-major;
  * the down input columns past I are zero-padded to Ipad).  Bit-exact quant/q4nx.py:127-200. */
 int rmoe_layer_quantize_expert_dev(rmoe_ctx* ctx, int layer, int expert, const float* gate_up_dev,

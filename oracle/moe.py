@@ -39,8 +39,17 @@ Pins (tests/test_oracle_moe.py):
   ``bench/moe/test_moe_ref.py:430-437``.
 * ``moe_experts_grouped``: equals the planner gather/scatter path
   (``oracle.planner``), restating ``kernels/moe_grouped/test_planner.py:67-105``.
-* ``residual_stack``: parity unpinned beyond its composition (no reference code
-  exists for it; it is built only from the pinned pieces above).
+* ``prefill_layer`` (tests/test_oracle_stack.py): byte-equal to ``moe_token`` per token,
+  as the reference's grouped-prefill parity test requires of its grouped path
+  (``host/test_prefill_grouped_parity.py:42-115``); equal to a closed form on
+  constant-weight experts (every projection ``c * sum(x)``, every sum exact), batched
+  and token-serial alike.
+* ``residual_stack`` (BASELINE config 4's stack; the reference has no such stack):
+  equal, bit for bit, to the same closed form evaluated with Python scalars and torch's
+  bf16 rounding over several layers; all-zero experts return the input unchanged; and
+  planted mistakes (one rounding around the residual add instead of two, no shared
+  expert, gate and up swapped, the lowest-scoring experts selected) all fail that
+  comparison.
 """
 
 from __future__ import annotations

@@ -26,6 +26,8 @@ FMT_Q4NX = 0
 FMT_BFP16 = 1
 BUNDLE_B1 = 1
 BUNDLE_B2 = 2
+PART_GATE_UP = 3
+PART_DOWN = 2
 
 _p = C.c_void_p
 _i = C.c_int
@@ -61,6 +63,7 @@ SIGNATURES: dict[str, list] = {
     "rmoe_layer_quantize_expert_dev": [_p, _i, _i, _p, _p, _p],
     "rmoe_layer_synthesize_dev": [_p, _i, C.c_uint64, _f, _p],
     "rmoe_layer_download_expert": [_p, _i, _i, _p, _sz, _p, _sz],
+    "rmoe_layer_expert_matrix": [_p, _i, _i, _i, _pi],
     "rmoe_layer_set_router": [_p, _i, _p, _p, _i, _i, _f],
     "rmoe_layer_set_router_dev": [_p, _i, _p, _p, _i, _i, _f],
     "rmoe_layer_free": [_p, _i],

@@ -116,6 +116,11 @@ class GpuBackend:
             raise ValueError(f"Unknown bundle format for {bundle}: {fmt!r}")
         self._bundles[bundle] = self.ctx.upload_matrix(packed, M, K, fmt=self._FORMATS[fmt])
 
+    def register_view(self, bundle: str, matrix: Matrix) -> None:
+        """Serve an existing device matrix (e.g. ``MoeLayer.expert_matrix``, a view of an
+        expert's tiles) under the bundle name ``bundle``."""
+        self._bundles[bundle] = matrix
+
     def register_component(self, name: str, bundle: str, row_start: int, row_end: int, orig_k: int | None = None) -> None:
         """Serve weight ``name`` as rows ``[row_start, row_end)`` of ``bundle``."""
         mat = self._bundles[bundle]
@@ -132,7 +137,30 @@ class GpuBackend:
         if router_weight is not None:
             lyr.set_router(router_weight, router_bias, score, renormalize, scaling)
         self._layers[int(layer)] = lyr
+        self._register_shared(lyr)
         return lyr
+
+    def _shared_prefix(self, layer: int) -> str:
+        return f"model.layers.{int(layer)}.moe.shared_experts"
+
+    def _register_shared(self, lyr: MoeLayer) -> None:
+        """Serve the shared expert of a q4nx layer (expert ``n_routed`` of its bundles,
+        kernels/moe/pack.py:40-44) under the names ``RaonModel`` asks ``linear`` /
+        ``linear_batch`` for (host/raon.py:1314-1323, 1570-1577): gate = rows [0, I) and
+        up = rows [I, 2I) of the expert's gate/up matrix, down = its ``[H, Ipad]`` matrix
+        with input width I.  The matrices are views of the layer's own tiles (no second
+        upload); gate and up share one bundle, so the bundle-reuse rule computes both rows
+        in one launch (npu/backend.py:3652-3663)."""
+        g = lyr.geom
+        if not g.n_shared:
+            return
+        pfx, d = self._shared_prefix(lyr.layer), f"L{lyr.layer:02d}"
+        e = g.shared_id
+        self.register_view(f"{d}/shared_gate_up", lyr.expert_matrix(e, "gate_up"))
+        self.register_view(f"{d}/shared_down", lyr.expert_matrix(e, "down"))
+        self.register_component(f"{pfx}.gate_proj.weight", f"{d}/shared_gate_up", 0, g.inter)
+        self.register_component(f"{pfx}.up_proj.weight", f"{d}/shared_gate_up", g.inter, 2 * g.inter)
+        self.register_component(f"{pfx}.down_proj.weight", f"{d}/shared_down", 0, g.hidden, orig_k=g.inter)
 
     def register_moe_layer_q4k(self, layer: int, geom: MoeGeometry, gate_exps, up_exps, down_exps,
                                router_weight: np.ndarray | None = None, router_bias: np.ndarray | None = None,
@@ -157,6 +185,7 @@ class GpuBackend:
         if router_weight is not None:
             lyr.set_router(router_weight, router_bias, score, renormalize, scaling)
         self._layers[int(layer)] = lyr
+        self._register_shared(lyr)
         return lyr
 
     def register_moe_layer_d(self, layer: int, geom: MoeGeometry, moe_b1: bytes | np.ndarray, moe_b2: bytes | np.ndarray,
@@ -191,8 +220,8 @@ class GpuBackend:
             self.register_bundle(f"{d}/shared_gu", shared_gu, 2 * g.inter, g.hidden, fmt="bfp16_gemv")
             self.register_component(f"{pfx}.gate_proj.weight", f"{d}/shared_gu", 0, g.inter)
             self.register_component(f"{pfx}.up_proj.weight", f"{d}/shared_gu", g.inter, 2 * g.inter)
-        per = lyr.dn_expert_bytes
-        self.register_bundle(f"{d}/shared_down", b2[g.n_routed * per:], g.hidden, g.inter_pad, fmt="bfp16_gemv")
+        # the shared down is moe_b2's last expert (npu/backend.py:4068-4107): a view, no copy
+        self.register_view(f"{d}/shared_down", lyr.expert_matrix(g.n_routed, "down"))
         self.register_component(f"{pfx}.down_proj.weight", f"{d}/shared_down", 0, g.hidden, orig_k=g.inter)
         return lyr
 
@@ -249,14 +278,14 @@ class GpuBackend:
 
     def linear_batch(self, name: str, x: np.ndarray) -> np.ndarray:
         """``[T, K]`` -> ``[T, M]``, byte-identical to stacked ``linear`` (host/backend.py:71-74)."""
-        xa = np.asarray(x)
-        if xa.ndim != 2:
-            raise ValueError("linear_batch expects [T, K]")
+        if not isinstance(x, np.ndarray) or x.dtype != np.uint16 or x.ndim != 2:
+            # npu/backend.py:3399-3400: only a [T, K] uint16 (bf16 bits) array is accepted
+            raise ValueError("linear_batch expects a [T, K] uint16 ndarray")
         mat, comp = self._resolve(name)
-        if xa.shape[1] != comp.orig_k:
-            raise ValueError(f"{name}: input width {xa.shape[1]} != {comp.orig_k}")
+        if x.shape[1] != comp.orig_k:
+            raise ValueError(f"{name}: input width {x.shape[1]} != {comp.orig_k}")
         t0 = time.perf_counter()
-        y = mat.linear(np.asarray(xa, dtype=np.uint16))[:, comp.row_start : comp.row_end].copy()
+        y = mat.linear(x)[:, comp.row_start : comp.row_end].copy()
         self._add_timing("linear_gpu", time.perf_counter() - t0)
         return y
 

@@ -257,7 +257,8 @@ int rmoe_destroy(rmoe_ctx* ctx) {
   if (!ctx) return RMOE_OK;
   hipSetDevice(ctx->device);
   hipStreamSynchronize(ctx->stream);
-  for (auto& kv : ctx->mats) hipFree(kv.second.tiles);
+  for (auto& kv : ctx->mats)
+    if (kv.second.view_of_layer < 0) hipFree(kv.second.tiles);
   for (auto& kv : ctx->layers) {
     hipFree(kv.second.gu);
     hipFree(kv.second.dn);
@@ -414,7 +415,7 @@ int rmoe_matrix_free(rmoe_ctx* ctx, int handle) {
   RmoeMatrix* m;
   TRY(find_matrix(ctx, handle, &m));
   HIP_TRY(hipStreamSynchronize(ctx->stream));
-  hipFree(m->tiles);
+  if (m->view_of_layer < 0) hipFree(m->tiles);
   ctx->mats.erase(handle);
   return RMOE_OK;
 }
@@ -584,6 +585,40 @@ int rmoe_layer_free(rmoe_ctx* ctx, int layer) {
   hipFree(it->second.router_w);
   hipFree(it->second.router_bias);
   ctx->layers.erase(it);
+  // Views of the layer's experts borrowed its memory: their handles go with it.
+  for (auto m = ctx->mats.begin(); m != ctx->mats.end();) {
+    if (m->second.view_of_layer == layer) m = ctx->mats.erase(m);
+    else ++m;
+  }
+  return RMOE_OK;
+}
+
+int rmoe_layer_expert_matrix(rmoe_ctx* ctx, int layer, int expert, int part, int* handle) {
+  RmoeLayer* L;
+  TRY(check_layer(ctx, layer, &L));
+  if (!handle) return fail(RMOE_EINVAL, "null argument");
+  RmoeMatrix m;
+  m.view_of_layer = layer;
+  if (part == RMOE_PART_GATE_UP) {
+    if (expert < 0 || expert >= L->gu_experts)
+      return fail(RMOE_EINVAL, "expert %d has no gate/up in layer %d (0..%d)", expert, layer, L->gu_experts - 1);
+    m.tiles = L->gu + (size_t)expert * L->gu_bytes;
+    m.M = 2 * L->I;
+    m.K = L->H;
+    m.fmt = RMOE_FMT_Q4NX;
+  } else if (part == RMOE_PART_DOWN) {
+    if (expert < 0 || expert >= L->dn_experts)
+      return fail(RMOE_EINVAL, "expert %d has no down projection in layer %d (0..%d)", expert, layer, L->dn_experts - 1);
+    m.tiles = L->dn + (size_t)expert * L->dn_bytes;
+    m.M = L->H;
+    m.K = L->Ipad;
+    m.fmt = L->dn_fmt;
+  } else {
+    return fail(RMOE_EINVAL, "part must be RMOE_PART_GATE_UP or RMOE_PART_DOWN, got %d", part);
+  }
+  TRY(check_mk(m.M, m.K));
+  *handle = ctx->next_handle++;
+  ctx->mats[*handle] = m;
   return RMOE_OK;
 }
 

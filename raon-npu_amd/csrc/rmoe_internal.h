@@ -228,6 +228,9 @@ struct RmoeMatrix {
   uint8_t* tiles = nullptr;  // device, tile layout of the format
   int M = 0, K = 0;
   int fmt = 0;               // RMOE_FMT_Q4NX or RMOE_FMT_BFP16
+  // A view (rmoe_layer_expert_matrix) borrows the tiles of one expert of this layer and
+  // owns no memory; -1 for a matrix that owns its tiles.
+  int view_of_layer = -1;
 };
 
 struct RmoeLayer {

@@ -12,7 +12,7 @@ import ctypes as C
 import numpy as np
 
 from . import _lib
-from ._lib import ACT_SITU, ACT_SWIGLU, BUNDLE_B1, BUNDLE_B2, SCORE_SIGMOID, SCORE_SOFTMAX, call, ptr
+from ._lib import ACT_SITU, ACT_SWIGLU, BUNDLE_B1, BUNDLE_B2, PART_DOWN, PART_GATE_UP, SCORE_SIGMOID, SCORE_SOFTMAX, call, ptr
 from .geometry import MoeGeometry
 
 
@@ -155,8 +155,19 @@ class Context:
 
     def decode_stack_dev(self, layers, x_dev, out_dev, residual: bool = True, gate_beta=None, value_beta=None,
                          ids_dev=None, wts_dev=None, stream=None):
-        """Device-pointer form of ``decode_stack`` (no allocation; capturable in a HIP graph)."""
+        """Device-pointer form of ``decode_stack`` (no allocation; capturable in a HIP graph).
+        x/out: int16 (bf16 bits) [H]; ids_dev/wts_dev (optional): int32/float32 [L, k].
+        Every tensor is checked against the shapes the kernel indexes before the launch."""
         ids = self._layer_ids(layers)
+        if not isinstance(layers[0], MoeLayer):
+            raise ValueError("decode_stack_dev takes MoeLayer objects (their geometry sizes the tensors)")
+        g = layers[0].geom
+        _check_dev(x_dev, (g.hidden,), "int16", "x")
+        _check_dev(out_dev, (g.hidden,), "int16", "out")
+        if ids_dev is not None:
+            _check_dev(ids_dev, (ids.size, g.top_k), "int32", "ids")
+        if wts_dev is not None:
+            _check_dev(wts_dev, (ids.size, g.top_k), "float32", "wts")
         act, gb, vb = act_code(gate_beta, value_beta)
         call("rmoe_moe_decode_stack_dev", self._h, ptr(ids), ids.size, ptr(x_dev), ptr(out_dev), int(bool(residual)),
              act, gb, vb, ptr(ids_dev), ptr(wts_dev), _stream_ptr(stream))
@@ -272,6 +283,20 @@ class MoeLayer:
         """Seeded N(0, std) weights for every expert, generated and quantized on the device."""
         call("rmoe_layer_synthesize_dev", self.ctx.handle, self.layer, int(seed) & (2**64 - 1), float(std),
              _stream_ptr(stream))
+
+    def expert_matrix(self, expert: int, part: str) -> "Matrix":
+        """A matrix handle viewing one expert's weights in place: ``part`` "gate_up" (q4nx
+        ``[2I, H]``, gate rows then up rows) or "down" (``[H, Ipad]``, bfp16 in a weights-d
+        layer).  No copy; freeing or re-creating the layer invalidates it."""
+        codes = {"gate_up": PART_GATE_UP, "down": PART_DOWN}
+        if part not in codes:
+            raise ValueError(f"part must be 'gate_up' or 'down', got {part!r}")
+        h = C.c_int()
+        call("rmoe_layer_expert_matrix", self.ctx.handle, self.layer, int(expert), codes[part], C.byref(h))
+        g = self.geom
+        if part == "gate_up":
+            return Matrix(self.ctx, h.value, 2 * g.inter, g.hidden, "q4nx")
+        return Matrix(self.ctx, h.value, g.hidden, g.inter_pad, "bfp16" if self.d_layout else "q4nx")
 
     def download_expert(self, expert: int) -> tuple[bytes, bytes]:
         """(gate_up, down) GEMV bytes of one expert; gate_up is b"" for the shared expert

@@ -6,15 +6,16 @@ A ``weights-d`` directory (``export/export_d.py``) holds one ``.bin`` per bundle
 * restates the canonical bundle and component map of the released model
   (``build_default_manifest_specs``, npu/backend.py:356-719), a table that has to match
   the exporter's entry for entry;
-* validates a manifest against it with the rules of ``_load_manifest_specs``
-  (npu/backend.py:729-929): known bundle names, no duplicates, format, padded and
-  original shapes, expert_count / expert_bytes of the expert bundles, canonical
-  size_bytes, a 64-digit sha256, file paths that stay inside the directory, the file's
-  size on disk, and the component list of each bundle;
+* checks a manifest against it with the rules of ``_load_manifest_specs``
+  (npu/backend.py:729-929), kept here as a table of per-field checks: known bundle
+  names, no duplicates, format, padded and original shapes, expert_count /
+  expert_bytes of the expert bundles, canonical size_bytes, a 64-digit sha256, file
+  paths that stay inside the directory, the file's size on disk, and the component
+  list of each bundle;
 * loads the MoE hot path's bundles into a ``GpuBackend``: ``moe_b1`` + ``moe_b2`` as a
-  weights-d MoE layer, ``shared_gu`` and the shared down (``moe_b2`` expert 128) as
-  dense bfp16 matrices served by ``linear``, and, when present, layer 0's ``dense_gu`` /
-  ``dense_down`` and the ``lm_head``.  Expert bundles are streamed from disk in slices
+  weights-d MoE layer, ``shared_gu`` as a dense bfp16 matrix and the shared down
+  (``moe_b2`` expert 128, a view of the layer's tiles) served by ``linear``, and, when
+  present, layer 0's ``dense_gu`` / ``dense_down`` and the ``lm_head``.  Expert bundles are streamed from disk in slices
   of experts and hashed on the way (``_verify_bundle_file``, npu/backend.py:316-340);
   a digest mismatch discards the layer before it is used.
 
@@ -141,169 +142,226 @@ def canonical_specs() -> tuple[dict[str, Component], dict[str, Bundle]]:
     return comps, bundles
 
 
+# ------------------------------------------------------------- bundle sizes --
+# A GEMV format stores a matrix in whole blocks of (rows, cols, bytes): q4nx blocks are
+# 32 x 256 weights in 5,120 B (quant/q4nx.py:23-28), bfp16ebs8 blocks are 8 weights of a
+# row in 9 B (quant/bfp16.py:35-47).  An expert bundle is expert_count such matrices.
+_BLOCK_OF_FAMILY = {"q4nx": (Q4NX_M_TILE, Q4NX_K_TILE, Q4NX_BLOCK_BYTES), "bfp16": (1, BFP16_BLOCK, BFP16_BLOCK_BYTES)}
+_FAMILY_OF_FORMAT = {"q4nx_gemv": "q4nx", "q4nx_gemv_bundle": "q4nx", "bfp16_gemv": "bfp16",
+                     "bfp16_gemv_bundle": "bfp16"}
+
+
 def canonical_size(meta: Bundle) -> tuple[int, int]:
-    """(whole bundle bytes, bytes per matrix) from the canonical geometry (npu/backend.py:729-752)."""
+    """``(bundle bytes, bytes of one matrix)`` of a canonical bundle, from its padded shape
+    and format (the sizes npu/backend.py:729-752 derives)."""
+    family = _FAMILY_OF_FORMAT.get(meta.fmt)
+    if family is None:
+        raise ValueError(f"{meta.name}: no block size is known for format {meta.fmt!r}")
     if len(meta.padded_shape) < 2:
-        raise ValueError(f"Canonical padded_shape is not a matrix for {meta.name}")
+        raise ValueError(f"{meta.name}: padded shape {meta.padded_shape} has no [rows, cols] matrix")
     rows, cols = meta.padded_shape[-2:]
-    if meta.fmt in ("q4nx_gemv", "q4nx_gemv_bundle"):
-        if rows % Q4NX_M_TILE or cols % Q4NX_K_TILE:
-            raise ValueError(f"Canonical q4nx shape is not tile-aligned for {meta.name}")
-        matrix = (rows // Q4NX_M_TILE) * (cols // Q4NX_K_TILE) * Q4NX_BLOCK_BYTES
-    elif meta.fmt in ("bfp16_gemv", "bfp16_gemv_bundle"):
-        if cols % BFP16_BLOCK:
-            raise ValueError(f"Canonical bfp16 shape is not block-aligned for {meta.name}")
-        matrix = rows * (cols // BFP16_BLOCK) * BFP16_BLOCK_BYTES
-    else:
-        raise ValueError(f"Unknown canonical bundle format for {meta.name}: {meta.fmt!r}")
-    return (matrix * meta.expert_count if meta.expert_count else matrix), matrix
+    br, bc, nbytes = _BLOCK_OF_FAMILY[family]
+    if rows % br or cols % bc:
+        raise ValueError(f"{meta.name}: [{rows}, {cols}] is not a whole number of {br}x{bc} {family} blocks")
+    one = (rows // br) * (cols // bc) * nbytes
+    return one * max(meta.expert_count, 1), one
 
 
 def component_names(comps: Mapping[str, Component], meta: Bundle) -> tuple[set[str], set[str]]:
-    """(required, allowed) component names of a bundle's manifest entry (npu/backend.py:755-784)."""
+    """``(required, allowed)`` component names of a bundle's manifest entry: the canonical
+    components served from it, plus the names the exporter writes for padding rows and
+    for the routed experts' rows (the contract of npu/backend.py:755-784)."""
     required = {c.hf_name for c in comps.values() if c.bundle == meta.name}
-    allowed = set(required) | {"padding"}
-    layer_dir, _, leaf = meta.name.partition("/")
-    if layer_dir.startswith("L") and layer_dir[1:].isdigit():
-        prefix = f"model.layers.{int(layer_dir[1:])}"
+    extra = {"padding"}
+    m = re.fullmatch(r"L(\d+)/(moe_b1|moe_b2|k_b|v_b)", meta.name)
+    if m:
+        layer, leaf = int(m.group(1)), m.group(2)
+        pfx = f"model.layers.{layer}"
         if leaf == "moe_b1" and meta.expert_count:
-            allowed.add(f"{prefix}.moe.experts.0..{meta.expert_count - 1}.(gate|up)_proj.weight")
+            extra.add(f"{pfx}.moe.experts.0..{meta.expert_count - 1}.(gate|up)_proj.weight")
         elif leaf == "moe_b2" and meta.expert_count:
-            allowed.add(f"{prefix}.moe.experts.0..{meta.expert_count - 2}.down_proj.weight")
-        elif leaf == "k_b":
-            allowed.add(f"{prefix}.self_attn.kv_b_proj.weight (key_part)")
-        elif leaf == "v_b":
-            allowed.add(f"{prefix}.self_attn.kv_b_proj.weight (val_part)")
-    return required, allowed
+            # the last expert of moe_b2 is the shared one: routed experts 0..count-2
+            extra.add(f"{pfx}.moe.experts.0..{meta.expert_count - 2}.down_proj.weight")
+        elif leaf in ("k_b", "v_b"):
+            extra.add(f"{pfx}.self_attn.kv_b_proj.weight ({'key' if leaf == 'k_b' else 'val'}_part)")
+    return required, required | extra
 
 
 def bundle_path(weights_dir: Path, rel_file: str, name: str) -> Path:
-    """A manifest file path that may not leave ``weights_dir`` (npu/backend.py:278-291)."""
+    """Where a manifest's relative file name points, refusing any path that is absolute,
+    climbs with ``..`` or resolves (symlinks included) outside ``weights_dir`` -- the
+    rule of npu/backend.py:278-291."""
     rel = Path(rel_file)
-    if rel.is_absolute() or ".." in rel.parts:
-        raise ValueError(f"Unsafe file path for {name}: {rel_file!r}")
+    if rel.is_absolute() or any(part == ".." for part in rel.parts):
+        raise ValueError(f"{name}: file path {rel_file!r} must be relative and stay below the weights directory")
     root = Path(weights_dir).resolve()
-    resolved = (root / rel).resolve(strict=False)
-    try:
-        resolved.relative_to(root)
-    except ValueError as exc:
-        raise ValueError(f"Manifest file escapes weights directory for {name}: {rel_file!r}") from exc
-    return resolved
-
-
-def _reject_constant(name: str):
-    raise ValueError(f"non-finite JSON number {name!r} is not allowed")
-
-
-def _finite_float(text: str) -> float:
-    v = float(text)
-    if not math.isfinite(v):
-        raise ValueError(f"non-finite JSON number {text!r} is not allowed")
-    return v
+    target = (root / rel).resolve(strict=False)
+    if target != root and root not in target.parents:
+        raise ValueError(f"{name}: file path {rel_file!r} escapes weights directory {root}")
+    return target
 
 
 def loads_strict(data: bytes | str) -> Any:
-    """JSON without NaN / Infinity / overflowing numbers (host/strict_json.py:23-34)."""
-    if isinstance(data, (bytes, bytearray)):
-        data = data.decode("utf-8")
+    """Parse JSON, refusing NaN, +-Infinity and numbers that overflow to them, and turning
+    pathological nesting into a ValueError (the decoding rules of host/strict_json.py)."""
+    text = data.decode("utf-8") if isinstance(data, (bytes, bytearray)) else data
+
+    def no_constant(tok: str):
+        raise ValueError(f"JSON number {tok} is non-finite")
+
+    def finite(tok: str) -> float:
+        v = float(tok)
+        if math.isinf(v) or math.isnan(v):
+            raise ValueError(f"JSON number {tok} is non-finite")
+        return v
+
     try:
-        return json.loads(data, parse_constant=_reject_constant, parse_float=_finite_float)
+        return json.loads(text, parse_constant=no_constant, parse_float=finite)
     except RecursionError as exc:
-        raise ValueError(f"JSON recursion limit exceeded: {exc}") from exc
+        raise ValueError("JSON nesting too deep") from exc
+
+
+# ------------------------------------------------------- manifest validation --
+def _is_int(v) -> bool:
+    return isinstance(v, int) and not isinstance(v, bool)
+
+
+def _expect_equal(key: str):
+    def check(value, meta: Bundle, want):
+        return None if value == want else f"{key} is {value!r}, expected {want!r}"
+    return check
+
+
+def _check_shape(key: str):
+    def check(value, meta: Bundle, want):
+        ok = isinstance(value, list) and list(value) == list(want)
+        return None if ok else f"{key} is {value!r}, expected {list(want)!r}"
+    return check
+
+
+def _check_count(key: str):
+    def check(value, meta: Bundle, want):
+        return None if _is_int(value) and value == want else f"{key} is {value!r}, expected {want}"
+    return check
+
+
+def _check_file(value, meta: Bundle, want):
+    return None if isinstance(value, str) and value else "has no file name"
+
+
+def _check_size(value, meta: Bundle, want):
+    if not _is_int(value) or value < 0:
+        return f"size_bytes {value!r} is not a byte count"
+    return None if value == want else f"size_bytes {value} differs from the canonical {want}"
+
+
+def _check_sha(value, meta: Bundle, want):
+    ok = isinstance(value, str) and re.fullmatch(r"[0-9a-fA-F]{64}", value) is not None
+    return None if ok else f"sha256 {value!r} is not 64 hex digits"
+
+
+# (manifest key, check, the canonical value it is compared with, applies to the bundle?)
+# in the order they are checked; the first failing rule names the entry and the field.
+_ENTRY_RULES = (
+    ("format", _expect_equal("format"), lambda m: m.fmt, lambda m: True),
+    ("padded_shape", _check_shape("padded_shape"), lambda m: m.padded_shape, lambda m: True),
+    ("original_shape", _check_shape("original_shape"), lambda m: m.orig_shape, lambda m: True),
+    ("expert_count", _check_count("expert_count"), lambda m: m.expert_count, lambda m: m.expert_count > 0),
+    ("expert_bytes", _check_count("expert_bytes"), lambda m: m.expert_bytes, lambda m: m.expert_count > 0),
+    ("file", _check_file, lambda m: None, lambda m: True),
+    ("size_bytes", _check_size, lambda m: canonical_size(m)[0], lambda m: True),
+    ("sha256", _check_sha, lambda m: None, lambda m: True),
+)
+
+
+def _check_components(item: dict, meta: Bundle, comps: Mapping[str, Component], require_complete: bool) -> None:
+    listed = item.get("components")
+    if not isinstance(listed, list):
+        raise ValueError(f"Manifest entry {meta.name}: components must be a list, got {listed!r}")
+    required, allowed = component_names(comps, meta)
+    named = set()
+    for c in listed:
+        if not isinstance(c, dict) or not isinstance(c.get("name"), str):
+            raise ValueError(f"Manifest entry {meta.name}: component {c!r} has no name")
+        cname = c["name"]
+        if cname not in allowed:
+            raise ValueError(f"Manifest entry {meta.name}: component {cname!r} does not belong to this bundle")
+        named.add(cname)
+        canon = comps.get(cname)
+        if canon is None:
+            continue
+        rows = (c.get("row_start"), c.get("row_end"))
+        if ("row_start" in c or "row_end" in c) and rows != (canon.row_start, canon.row_end):
+            raise ValueError(f"Manifest entry {meta.name}: component {cname} rows {rows} differ from "
+                             f"({canon.row_start}, {canon.row_end})")
+        if "expert_id" in c and "expert_id" in canon.extra and c["expert_id"] != canon.extra["expert_id"]:
+            raise ValueError(f"Manifest entry {meta.name}: component {cname} expert_id {c['expert_id']!r} differs "
+                             f"from {canon.extra['expert_id']}")
+    missing = required - named
+    if require_complete and missing:
+        raise ValueError(f"Manifest entry {meta.name}: missing canonical components " + ", ".join(sorted(missing)))
 
 
 def load_manifest(path: str | Path, comps: Mapping[str, Component], bundles: Mapping[str, Bundle], *,
                   weights_dir: str | Path | None = None, require_complete: bool = True) -> None:
-    """Validate ``manifest.json`` against the canonical map and record each bundle's file,
-    size and sha256 in ``bundles`` (npu/backend.py:787-929).  Raises ``ValueError`` (or
-    ``FileNotFoundError`` for a missing bundle file) on the first violation."""
+    """Check ``manifest.json`` against the canonical bundle map and record each bundle's
+    file, size and digest in ``bundles``.
+
+    The rules are those of npu/backend.py:787-929: the payload is a list of bundle
+    entries (or ``{"bundles": [...]}``); ``host_safetensors`` entries are skipped; every
+    other entry names a canonical bundle exactly once and carries its format, padded and
+    original shapes, the expert count and size of an expert bundle, a file that stays
+    inside the directory, the canonical size in bytes, a 64-digit sha256, and the
+    bundle's component list; with ``weights_dir`` the file must exist with that size;
+    with ``require_complete`` every canonical bundle and component must be listed.
+    Violations raise ``ValueError`` (``FileNotFoundError`` for a missing file)."""
     path = Path(path)
     payload = loads_strict(path.read_bytes())
-    if isinstance(payload, dict):
-        if not isinstance(payload.get("bundles"), list):
-            raise ValueError(f"Manifest dict missing 'bundles' list: {path}")
-        entries = payload["bundles"]
-    elif isinstance(payload, list):
+    if isinstance(payload, list):
         entries = payload
+    elif isinstance(payload, dict) and isinstance(payload.get("bundles"), list):
+        entries = payload["bundles"]
+    elif isinstance(payload, dict):
+        raise ValueError(f"{path}: manifest object has no 'bundles' list")
     else:
-        raise ValueError(f"Invalid manifest top-level structure in {path}")
+        raise ValueError(f"{path}: manifest top-level value must be a list or an object")
 
-    seen: set[str] = set()
+    listed: set[str] = set()
     for item in entries:
         if not isinstance(item, dict):
-            raise ValueError(f"Invalid manifest bundle entry: {item!r}")
-        fmt = item.get("format")
-        if fmt == "host_safetensors":
+            raise ValueError(f"{path}: manifest bundle entry {item!r} is not an object")
+        if item.get("format") == "host_safetensors":
             continue
         name = item.get("bundle")
-        meta = bundles.get(name) if isinstance(name, str) and name else None
+        meta = bundles.get(name) if isinstance(name, str) else None
         if meta is None:
-            raise ValueError(f"Unknown NPU bundle in manifest: {name!r}")
-        if name in seen:
-            raise ValueError(f"Duplicate NPU bundle in manifest: {name}")
-        seen.add(name)
-        if fmt != meta.fmt:
-            raise ValueError(f"Manifest format mismatch for {meta.name}: {fmt!r} != {meta.fmt!r}")
-        for key, want in (("padded_shape", meta.padded_shape), ("original_shape", meta.orig_shape)):
-            got = item.get(key)
-            if not isinstance(got, list) or list(got) != list(want):
-                raise ValueError(f"Manifest {key} mismatch for {meta.name}: {got!r} != {want!r}")
-        canonical, per_matrix = canonical_size(meta)
-        if meta.expert_count:
-            if meta.expert_bytes != per_matrix:
-                raise ValueError(f"Canonical expert_bytes mismatch for {meta.name}: {meta.expert_bytes} != {per_matrix}")
-            for key, want in (("expert_count", meta.expert_count), ("expert_bytes", meta.expert_bytes)):
-                got = item.get(key)
-                if isinstance(got, bool) or got != want:
-                    raise ValueError(f"Manifest {key} mismatch for {meta.name}: {got!r} != {want}")
-        rel_file = item.get("file")
-        if not isinstance(rel_file, str) or not rel_file:
-            raise ValueError(f"Manifest file missing for {meta.name}")
-        size = item.get("size_bytes")
-        if isinstance(size, bool) or not isinstance(size, int) or size < 0:
-            raise ValueError(f"Invalid size_bytes for {meta.name}: {size!r}")
-        if size != canonical:
-            raise ValueError(f"Manifest canonical size_bytes mismatch for {meta.name}: {size} != {canonical}")
-        sha = item.get("sha256")
-        if not isinstance(sha, str) or not re.fullmatch(r"[0-9a-fA-F]{64}", sha):
-            raise ValueError(f"Invalid sha256 for {meta.name}: {sha!r}")
+            raise ValueError(f"{path}: bundle {name!r} is not in the canonical map")
+        if name in listed:
+            raise ValueError(f"{path}: bundle {name} is listed twice")
+        listed.add(name)
+        if meta.expert_count and canonical_size(meta)[1] != meta.expert_bytes:
+            raise ValueError(f"canonical map: {name} expert_bytes {meta.expert_bytes} != one matrix "
+                             f"{canonical_size(meta)[1]}")
+        for key, check, want, applies in _ENTRY_RULES:
+            if applies(meta):
+                msg = check(item.get(key), meta, want(meta))
+                if msg:
+                    raise ValueError(f"Manifest entry {name}: {msg}")
         if weights_dir is not None:
-            resolved = bundle_path(Path(weights_dir), rel_file, meta.name)
+            target = bundle_path(Path(weights_dir), item["file"], name)
             try:
-                actual = resolved.stat().st_size
+                on_disk = target.stat().st_size
             except FileNotFoundError as exc:
-                raise FileNotFoundError(f"Missing D bundle binary: {resolved}") from exc
-            if actual != size:
-                raise ValueError(f"Manifest size_bytes mismatch for {meta.name}: file has {actual}, manifest has {size}")
-        meta.rel_file, meta.size_bytes, meta.sha256 = rel_file, size, sha.lower()
+                raise FileNotFoundError(f"Missing D bundle binary: {target}") from exc
+            if on_disk != item["size_bytes"]:
+                raise ValueError(f"Manifest entry {name}: file has {on_disk} bytes, size_bytes says {item['size_bytes']}")
+        meta.rel_file, meta.size_bytes, meta.sha256 = item["file"], item["size_bytes"], item["sha256"].lower()
+        _check_components(item, meta, comps, require_complete)
 
-        listed = item.get("components")
-        if not isinstance(listed, list):
-            raise ValueError(f"Invalid components for {meta.name}: {listed!r}")
-        required, allowed = component_names(comps, meta)
-        seen_c: set[str] = set()
-        for c in listed:
-            if not isinstance(c, dict) or not isinstance(c.get("name"), str):
-                raise ValueError(f"Invalid component entry for {meta.name}: {c!r}")
-            cname = c["name"]
-            if cname not in allowed:
-                raise ValueError(f"Unknown component for {meta.name}: {cname!r}")
-            seen_c.add(cname)
-            cm = comps.get(cname)
-            if cm is None:
-                continue
-            if cm.bundle != name:
-                raise ValueError(f"Component {cm.hf_name} bundle mismatch: {name} != {cm.bundle}")
-            if ("row_start" in c or "row_end" in c) and (c.get("row_start"), c.get("row_end")) != (cm.row_start, cm.row_end):
-                raise ValueError(f"Row range mismatch for {cm.hf_name}: ({c.get('row_start')}, {c.get('row_end')}) "
-                                 f"!= ({cm.row_start}, {cm.row_end})")
-            if "expert_id" in c and "expert_id" in cm.extra and c["expert_id"] != cm.extra["expert_id"]:
-                raise ValueError(f"Expert ID mismatch for {cm.hf_name}: {c['expert_id']} != {cm.extra['expert_id']}")
-        if require_complete and required - seen_c:
-            raise ValueError(f"Manifest missing canonical components for {meta.name}: " + ", ".join(sorted(required - seen_c)))
-
-    if require_complete and set(bundles) - seen:
-        raise ValueError("Manifest missing NPU bundles: " + ", ".join(sorted(set(bundles) - seen)))
+    if require_complete:
+        absent = set(bundles) - listed
+        if absent:
+            raise ValueError(f"{path}: manifest is missing NPU bundles " + ", ".join(sorted(absent)))
 
 
 class _Reader:
@@ -397,7 +455,6 @@ def load_weights_d(backend, weights_dir: str | Path, manifest_path: str | Path |
             if f"{d}/{leaf}" not in present:
                 raise FileNotFoundError(f"Missing D bundle binary: {bundle_path(wdir, bundles[f'{d}/{leaf}'].rel_file, leaf)}")
         lyr = backend.ctx.create_layer_d(int(layer), geom)
-        shared_down = b""
         try:
             for bundle_id, leaf in ((1, "moe_b1"), (2, "moe_b2")):
                 meta = bundles[f"{d}/{leaf}"]
@@ -407,9 +464,6 @@ def load_weights_d(backend, weights_dir: str | Path, manifest_path: str | Path |
                         n = min(experts_per_read, meta.expert_count - e0)
                         chunk = reader.read(n * meta.expert_bytes)
                         lyr.upload_d(bundle_id, e0, chunk)
-                        if bundle_id == 2 and e0 <= NUM_ROUTED_EXPERTS < e0 + n:
-                            off = (NUM_ROUTED_EXPERTS - e0) * meta.expert_bytes
-                            shared_down = chunk[off:off + meta.expert_bytes]
                     reader.finish()
                 finally:
                     reader.close()
@@ -423,10 +477,10 @@ def load_weights_d(backend, weights_dir: str | Path, manifest_path: str | Path |
         loaded += [f"{d}/moe_b1", f"{d}/moe_b2"]
         register_dense(f"{d}/shared_gu", "bfp16_gemv")
         # The shared expert's down projection (component fmt "shared_down") is moe_b2's
-        # expert 128, served by linear as a dense [2560, 1280] bfp16 matrix whose input
+        # expert 128, served by linear in place as a bfp16 [2560, 1280] matrix whose input
         # is zero-padded from 1088 columns.
         sd = comps[f"model.layers.{int(layer)}.moe.shared_experts.down_proj.weight"]
-        backend.register_bundle(f"{d}/shared_down", shared_down, HIDDEN_SIZE, sd.padded_k, fmt="bfp16_gemv")
+        backend.register_view(f"{d}/shared_down", lyr.expert_matrix(sd.extra["expert_id"], "down"))
         backend.register_component(sd.hf_name, f"{d}/shared_down", sd.row_start, sd.row_end, orig_k=sd.orig_k)
 
     if load_dense and {"L00/dense_gu", "L00/dense_down"} <= present:

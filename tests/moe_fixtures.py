@@ -49,9 +49,17 @@ def make_layer(geom, seed: int, std: float = 0.02, score: str = "softmax", bias:
     return SynthLayer(geom, b"".join(gu), b"".join(dn), router, bias, score)
 
 
-def random_tokens(n: int, hidden: int, seed: int) -> np.ndarray:
+def random_tokens(n: int, hidden: int, seed: int, std: float = 1.0) -> np.ndarray:
     rng = np.random.default_rng(seed)
-    return f32_to_bf16(rng.standard_normal((n, hidden)).astype(np.float32))
+    return f32_to_bf16((rng.standard_normal((n, hidden)) * std).astype(np.float32))
+
+
+# Hidden states of the 48-layer residual stack: the stack adds each
+# layer's MoE output to its input with no normalisation, and SwiGLU is quadratic in its
+# input, so with N(0, 0.02) weights the stream grows by ~0.34 sigma^2 per layer.  From
+# N(0, 1) states it overflows to non-finite values after ~20 layers; from N(0, 0.25^2) it
+# stays finite over 48 layers (sigma 0.25 -> ~0.3) and the routing stays informative.
+STACK_HIDDEN_STD = 0.25
 
 
 def routing_margin(x_u16: np.ndarray, spec: om.RouterSpec) -> float:
@@ -72,3 +80,66 @@ def compare_bf16(a_u16: np.ndarray, b_u16: np.ndarray) -> tuple[float, float, fl
     d = a - b
     rel = float(np.linalg.norm(d) / max(np.linalg.norm(b), 1e-30))
     return float(np.abs(d).max()), rel, float(np.mean(a_u16 == b_u16))
+
+
+TOL_ABS, TOL_REL = 1e-2, 1e-3
+
+
+def check_bf16(out: np.ndarray, ref: np.ndarray, label: str, same_min: float | None = None) -> dict:
+    """The BASELINE bar, max-abs 1e-2 and rel-L2 1e-3, asserted on every element whose
+    reference value has |ref| < 2.  From |ref| = 2 on, one bf16 ulp (2^-6) exceeds 1e-2,
+    so a single rounding tie that fp32 summation order decides differently moves an
+    element past 1e-2; there the bound is two ulps of the reference value, and such
+    elements are counted and reported separately (``ulp_bounded``).  Returns the figures."""
+    from oracle.bf16 import bf16_to_f32
+
+    a = bf16_to_f32(out).astype(np.float64)
+    b = bf16_to_f32(ref).astype(np.float64)
+    d = np.abs(a - b)
+    small = np.abs(b) < 2.0
+    rel = float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(b), 1e-30))) - 7)
+    big_bad = (~small) & (d > TOL_ABS)
+    res = {"max_abs_small": float(d[small].max()) if small.any() else 0.0, "rel_l2": rel,
+           "bit_identical": float(np.mean(out == ref)), "ulp_bounded": int(big_bad.sum()),
+           "n_big": int((~small).sum())}
+    print(f"{label}: max-abs(|ref|<2) {res['max_abs_small']:.3e} rel-L2 {rel:.3e} "
+          f"bit-identical {res['bit_identical']:.4f} ulp-bounded {res['ulp_bounded']}/{res['n_big']}")
+    assert res["max_abs_small"] <= TOL_ABS, (label, res)
+    assert np.all(d[~small] <= 2 * ulp[~small]), (label, res)
+    assert rel <= TOL_REL, (label, res)
+    if same_min is not None:
+        assert res["bit_identical"] >= same_min, (label, res)
+    return res
+
+
+class LazyBank:
+    """Duck-types ``oracle.moe.ExpertBank`` for a layer resident on the GPU: an expert's
+    pack_gemv bytes are downloaded and dequantized (as DWeights does) on first use only,
+    so the oracle can follow a few tokens through full-size layers."""
+
+    def __init__(self, gpu_layer, cache: int = 64):
+        from collections import OrderedDict
+
+        g = gpu_layer.geom
+        self.layer, self.hidden, self.inter, self.inter_pad = gpu_layer, g.hidden, g.inter, g.inter_pad
+        self._cache = OrderedDict()
+        self._cap = cache
+
+    def expert(self, e: int):
+        from oracle.q4nx import dequantize_simple, parse_gemv
+
+        if e in self._cache:
+            self._cache.move_to_end(e)
+            return self._cache[e]
+        gu, dn = self.layer.download_expert(int(e))
+        w = dequantize_simple(*parse_gemv(gu, K=self.hidden, M=2 * self.inter))
+        d = dequantize_simple(*parse_gemv(dn, K=self.inter_pad, M=self.hidden))[:, : self.inter]
+        out = (np.ascontiguousarray(w[: self.inter]), np.ascontiguousarray(w[self.inter:]), np.ascontiguousarray(d))
+        self._cache[e] = out
+        while len(self._cache) > self._cap:
+            self._cache.popitem(last=False)
+        return out
+
+    def down_proj(self, e: int):
+        return self.expert(e)[2]

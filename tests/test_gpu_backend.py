@@ -17,7 +17,7 @@ from oracle import moe as om
 from oracle.bf16 import bf16_to_f32, f32_to_bf16
 from oracle.q4nx import dequantize_simple, pack_gemv, quantize
 
-from moe_fixtures import compare_bf16, make_layer, random_tokens, routing_margin
+from moe_fixtures import check_bf16, compare_bf16, make_layer, random_tokens, routing_margin
 
 pytestmark = pytest.mark.gpu
 
@@ -201,3 +201,96 @@ def test_hooks_and_flags(be, moe):
     assert be.prefetch_linears([]) is None
     assert be.prefill_shared_precompute is True and be.prefill_grouped_moe is True
     assert be.preload(4) is None
+
+
+# ------------------------------------------------- RaonModel's call sequences --
+def _pfx(layer: int) -> str:
+    return f"model.layers.{layer}.moe"
+
+
+def test_shared_expert_components_are_views(be, moe):
+    """register_moe_layer serves the shared expert (expert n_routed of the bundles) under
+    the names RaonModel calls, in place: the views download to the uploaded bytes."""
+    geom, syn, bank = moe
+    gu_view = be._bundles["L03/shared_gate_up"]
+    dn_view = be._bundles["L03/shared_down"]
+    e = geom.shared_id
+    assert gu_view.download() == syn.gate_up[e * geom.gu_bytes:(e + 1) * geom.gu_bytes]
+    assert dn_view.download() == syn.down[e * geom.dn_bytes:(e + 1) * geom.dn_bytes]
+    x = random_tokens(1, geom.hidden, 30)[0]
+    g, u, d = bank.expert(e)
+    for name, w, xi in ((f"{_pfx(3)}.shared_experts.gate_proj.weight", g, x),
+                        (f"{_pfx(3)}.shared_experts.up_proj.weight", u, x),
+                        (f"{_pfx(3)}.shared_experts.down_proj.weight", d, x[: geom.inter])):
+        err, rel, same = compare_bf16(be.linear(name, xi), om.linear(w, xi))
+        assert err <= 1e-2 and rel <= 1e-3, name
+
+
+def test_raon_model_token_call_sequence(be, moe):
+    """RaonModel._moe_token (host/raon.py:1288-1330) replayed call for call: prestart hook,
+    host router (NumPy, as _route_token), moe_experts, linear of the shared gate/up/down
+    names with the host SiTU-GLU between, RTNE(routed + shared)."""
+    geom, syn, bank = moe
+    spec = syn.router_spec()
+    pfx = _pfx(3)
+    for t, x in enumerate(random_tokens(5, geom.hidden, 31)):
+        be.set_step(100 + t)
+        be.moe_prestart_shared(3, x)
+        top, w, _ = om.route_token(x, spec)
+        routed = be.moe_experts(3, x, top, w, gate_beta=4.0, value_beta=25.0)
+        sh_gate = be.linear(f"{pfx}.shared_experts.gate_proj.weight", x)
+        sh_up = be.linear(f"{pfx}.shared_experts.up_proj.weight", x)
+        sh_act = om.situ_glu(sh_gate, sh_up, 4.0, 25.0)
+        shared = be.linear(f"{pfx}.shared_experts.down_proj.weight", f32_to_bf16(sh_act))
+        out = f32_to_bf16(bf16_to_f32(routed) + bf16_to_f32(shared))
+        ref, rtop, _, _ = om.moe_token(bank, spec, x, 4.0, 25.0, shared_id=geom.shared_id)
+        assert top.tolist() == rtop.tolist()
+        check_bf16(out, ref, f"_moe_token replay {t}")
+
+
+def test_raon_model_prefill_call_sequence(be, moe):
+    """The grouped prefill branch (host/raon.py:1565-1602) replayed: linear_batch of the
+    shared gate and up names, per-token host routing, moe_experts_grouped with the
+    concatenated shared_gu, RTNE(routed + shared_down)."""
+    geom, syn, bank = moe
+    spec = syn.router_spec()
+    pfx = _pfx(3)
+    T = 29
+    xs = random_tokens(T, geom.hidden, 32)
+    sh_gate_all = be.linear_batch(f"{pfx}.shared_experts.gate_proj.weight", xs)
+    sh_up_all = be.linear_batch(f"{pfx}.shared_experts.up_proj.weight", xs)
+    routes = [om.route_token(xs[t], spec) for t in range(T)]
+    top_all = np.stack([r[0] for r in routes])
+    w_all = np.stack([r[1] for r in routes]).astype(np.float32, copy=False)
+    routed, shared_down = be.moe_experts_grouped(3, xs, top_all, w_all,
+                                                 np.concatenate([sh_gate_all, sh_up_all], axis=1),
+                                                 gate_beta=4.0, value_beta=25.0)
+    out = f32_to_bf16(bf16_to_f32(routed) + bf16_to_f32(shared_down))
+    ref, rtop, _ = om.prefill_layer(bank, spec, xs, geom.shared_id, 4.0, 25.0)
+    np.testing.assert_array_equal(top_all, rtop)
+    check_bf16(out, ref, "prefill branch replay")
+
+
+def test_linear_batch_rejects_non_bf16(be, moe):
+    """npu/backend.py:3399-3400: only a [T, K] uint16 ndarray is accepted."""
+    geom, _, _ = moe
+    name = f"{_pfx(3)}.shared_experts.gate_proj.weight"
+    xs = random_tokens(2, geom.hidden, 33)
+    for bad in (bf16_to_f32(xs), xs[0], xs.astype(np.int32), list(xs)):
+        with pytest.raises(ValueError):
+            be.linear_batch(name, bad)
+
+
+def test_view_handles_follow_the_layer(be):
+    """A view's handle goes with its layer: freed or re-created layers invalidate it."""
+    from raon_npu_amd.geometry import MoeGeometry
+
+    geom = MoeGeometry(**GEOM_ARGS)
+    syn = make_layer(geom, seed=34)
+    lyr = be.register_moe_layer(9, geom, syn.gate_up, syn.down)
+    view = be._bundles["L09/shared_down"]
+    x = random_tokens(1, geom.inter_pad, 35)
+    view.linear(x)
+    lyr.free()
+    with pytest.raises(KeyError):
+        view.linear(x)

@@ -17,7 +17,7 @@ from oracle import moe as om
 from oracle import planner as op
 from oracle.bf16 import bf16_to_f32, f32_to_bf16
 
-from moe_fixtures import compare_bf16, make_layer, random_tokens, routing_margin
+from moe_fixtures import LazyBank, check_bf16, make_layer, random_tokens, routing_margin
 
 pytestmark = pytest.mark.gpu
 
@@ -26,31 +26,14 @@ MARGIN = 1e-6
 
 
 def _check(out, ref, label, same_min=0.95):
-    """max-abs 1e-2 and rel-L2 1e-3.  A layer output passes two bf16 roundings in sequence
-    (the routed sum, then + shared) whose ties the fp32 summation order decides -- the
-    oracle's own BLAS order included -- for a few per cent of elements.  Near |ref| = 1..2
-    two such flips, and above 2 a single one, exceed 1e-2 by construction, so the
-    per-element bound is max(1e-2, two ulps of the reference value)."""
-    err, rel, same = compare_bf16(out, ref)
-    b = bf16_to_f32(ref).astype(np.float64)
-    d = np.abs(bf16_to_f32(out).astype(np.float64) - b)
-    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(b), 1e-30))) - 7)
-    bound = np.maximum(TOL_ABS, 2 * ulp)
-    print(f"{label}: max-abs {err:.3e} (max |d|/bound {np.max(d / bound):.3f}) rel-L2 {rel:.3e} "
-          f"bit-identical {same:.4f}")
-    assert np.all(d <= bound) and rel <= TOL_REL and same >= same_min, (label, err, rel, same)
+    """BASELINE bar via check_bf16: max-abs 1e-2 wherever |ref| < 2, two bf16 ulps above
+    (those elements are counted and reported), rel-L2 1e-3, and a floor on bit-identity."""
+    check_bf16(out, ref, label, same_min)
 
 
 def _check_ulp(out, ref, label):
-    """Residual-stream values reach |x| >= 2, where one bf16 ulp (0.0156) exceeds the 1e-2
-    max-abs bar; there the bound is two ulps of the reference value, with rel-L2 <= 1e-3."""
-    a = bf16_to_f32(out).astype(np.float64)
-    b = bf16_to_f32(ref).astype(np.float64)
-    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(b), 1e-30))) - 7)
-    bound = np.maximum(TOL_ABS, 2 * ulp)
-    rel = np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30)
-    print(f"{label}: max |d|/bound {np.max(np.abs(a - b) / bound):.3f} rel-L2 {rel:.3e} bit-identical {np.mean(out == ref):.4f}")
-    assert np.all(np.abs(a - b) <= bound) and rel <= TOL_REL
+    """Residual-stream values: the same bar without the bit-identity floor."""
+    check_bf16(out, ref, label)
 
 
 @pytest.fixture(scope="module")

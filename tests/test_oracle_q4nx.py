@@ -116,3 +116,12 @@ def test_padding_invariance():
     deq = dequantize_simple(*quantize(wp)).astype(np.float64)
     xp = np.pad(x, (0, 192)).astype(np.float64)
     np.testing.assert_allclose((deq @ xp)[:2100], deq[:2100, :576] @ x.astype(np.float64), rtol=1e-12, atol=1e-12)
+
+
+def test_dequantize_grouped_equals_simple():
+    from oracle.q4nx import dequantize_grouped
+
+    rng = np.random.default_rng(77)
+    w = (rng.standard_normal((96, 512)) * np.exp2(rng.integers(-20, 20, (96, 1)))).astype(np.float32)
+    c, s, m = quantize(w)
+    assert np.array_equal(dequantize_grouped(c, s, m), dequantize_simple(c, s, m))

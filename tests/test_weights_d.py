@@ -96,26 +96,26 @@ _DROP = object()
 
 
 @pytest.mark.parametrize("name,changes,pattern", [
-    ("L01/moe_b1", {"format": "q4nx_gemv"}, "format mismatch"),
-    ("L01/moe_b2", {"padded_shape": [129, 2560, 1088]}, "padded_shape mismatch"),
-    ("L01/moe_b2", {"original_shape": _DROP}, "original_shape mismatch"),
-    ("L02/moe_b1", {"expert_count": 129}, "expert_count mismatch"),
-    ("L02/moe_b1", {"expert_bytes": 3481601}, "expert_bytes mismatch"),
-    ("L02/shared_gu", {"size_bytes": True}, "Invalid size_bytes"),
-    ("L02/shared_gu", {"size_bytes": 6266881}, "canonical size_bytes mismatch"),
-    ("lm_head", {"sha256": "xyz"}, "Invalid sha256"),
-    ("lm_head", {"sha256": "ab" * 31}, "Invalid sha256"),
-    ("L00/f_b", {"file": "../f_b.bin"}, "Unsafe file path"),
-    ("L00/f_b", {"file": "/etc/passwd"}, "Unsafe file path"),
-    ("L00/f_b", {"file": ""}, "Manifest file missing"),
-    ("L00/f_b", {"components": "none"}, "Invalid components"),
-    ("L00/f_b", {"components": [{"name": "model.layers.0.mlp.gate_proj.weight"}]}, "Unknown component|bundle mismatch"),
+    ("L01/moe_b1", {"format": "q4nx_gemv"}, "format is"),
+    ("L01/moe_b2", {"padded_shape": [129, 2560, 1088]}, "padded_shape is"),
+    ("L01/moe_b2", {"original_shape": _DROP}, "original_shape is"),
+    ("L02/moe_b1", {"expert_count": 129}, "expert_count is"),
+    ("L02/moe_b1", {"expert_bytes": 3481601}, "expert_bytes is"),
+    ("L02/shared_gu", {"size_bytes": True}, "is not a byte count"),
+    ("L02/shared_gu", {"size_bytes": 6266881}, "differs from the canonical"),
+    ("lm_head", {"sha256": "xyz"}, "is not 64 hex digits"),
+    ("lm_head", {"sha256": "ab" * 31}, "is not 64 hex digits"),
+    ("L00/f_b", {"file": "../f_b.bin"}, "must be relative"),
+    ("L00/f_b", {"file": "/etc/passwd"}, "must be relative"),
+    ("L00/f_b", {"file": ""}, "has no file name"),
+    ("L00/f_b", {"components": "none"}, "components must be a list"),
+    ("L00/f_b", {"components": [{"name": "model.layers.0.mlp.gate_proj.weight"}]}, "does not belong to this bundle"),
     ("L01/shared_gu", {"components": [{"name": "model.layers.1.moe.shared_experts.gate_proj.weight", "row_start": 0,
-                                       "row_end": 1000}]}, "Row range mismatch"),
+                                       "row_end": 1000}]}, "rows .* differ"),
     ("L01/moe_b2", {"components": [{"name": "model.layers.1.moe.shared_experts.down_proj.weight", "expert_id": 127}]},
-     "Expert ID mismatch"),
+     "expert_id .* differs"),
     ("L01/moe_b2", {"components": []}, "missing canonical components"),
-    ("L04/o_proj", {"bundle": "L04/o_proj_v2"}, "Unknown NPU bundle"),
+    ("L04/o_proj", {"bundle": "L04/o_proj_v2"}, "not in the canonical map"),
 ])
 def test_manifest_rules(full_dir, name, changes, pattern):
     root, entries = full_dir
@@ -125,16 +125,16 @@ def test_manifest_rules(full_dir, name, changes, pattern):
 
 def test_manifest_rules_structure(full_dir, tmp_path):
     root, entries = full_dir
-    with pytest.raises(ValueError, match="Duplicate NPU bundle"):
+    with pytest.raises(ValueError, match="listed twice"):
         _validate(root, entries + [entries[3]])
     with pytest.raises(ValueError, match="missing NPU bundles"):
         _validate(root, entries[:-1])
     _validate(root, entries[:-1], require_complete=False)
-    with pytest.raises(ValueError, match="Invalid manifest bundle entry"):
+    with pytest.raises(ValueError, match="is not an object"):
         _validate(root, entries + [7])
     comps, bundles = W.canonical_specs()
     for text, pattern in (('{"bundles": [], "x": NaN}', "non-finite"), ('{"b": 1e999}', "non-finite"),
-                          ('{"nobundles": []}', "missing 'bundles'"), ('"x"', "top-level")):
+                          ('{"nobundles": []}', "no 'bundles' list"), ('"x"', "top-level")):
         (tmp_path / "m.json").write_text(text)
         with pytest.raises(ValueError, match=pattern):
             W.load_manifest(tmp_path / "m.json", comps, bundles)
@@ -191,6 +191,9 @@ class _FakeLayer:
     def upload_d(self, bundle, expert0, data):
         self.uploads.append((bundle, expert0, bytes(data)))
 
+    def expert_matrix(self, expert, part):
+        return ("view", self.layer, expert, part)
+
     def set_router(self, *a):
         self.log.append(("router", self.layer) + a)
 
@@ -221,6 +224,9 @@ class _FakeBackend:
 
     def register_component(self, name, bundle, r0, r1, orig_k=None):
         self.components[name] = (bundle, r0, r1, orig_k)
+
+    def register_view(self, name, matrix):
+        self.bundles[name] = matrix
 
 
 @pytest.fixture(scope="module")
@@ -256,9 +262,8 @@ def test_loader_host_logic(real_dir):
     b2 = b"".join(d for b, _, d in lyr.uploads if b == 2)
     assert b1 == data["L02/moe_b1"].tobytes() and b2 == data["L02/moe_b2"].tobytes()
     assert [e0 for b, e0, _ in lyr.uploads if b == 2] == [0, 40, 80, 120]
-    # the shared down is moe_b2's expert 128, a dense bfp16 [2560, 1280] served with K_in = 1088
-    sd, M, K, fmt = be.bundles["L02/shared_down"]
-    assert sd == data["L02/moe_b2"][128 * 3686400:].tobytes() and (M, K, fmt) == (2560, 1280, "bfp16_gemv")
+    # the shared down is moe_b2's expert 128 in place (a view of the layer), served with K_in = 1088
+    assert be.bundles["L02/shared_down"] == ("view", 2, 128, "down")
     assert be.components["model.layers.2.moe.shared_experts.down_proj.weight"] == ("L02/shared_down", 0, 2560, 1088)
     assert be.components["model.layers.2.moe.shared_experts.up_proj.weight"] == ("L02/shared_gu", 1088, 2176, 2560)
     assert be.bundles["L00/dense_gu"][1:] == (24064, 2560, "q4nx_gemv")
