@@ -214,6 +214,19 @@ int rmoe_moe_experts_dev(rmoe_ctx* ctx, int layer, const void* x_dev, const void
                          const void* top_weights_dev, int k, int act, float gate_beta, float value_beta,
                          void* out_dev, void* stream);
 
+/* rmoe_moe_experts_dev without context scratch: the same kernels and results, with their
+ * working memory (arrival counters, fp32 partial sums, activations, expert outputs) in a
+ * file-scope device array of 4 MiB that each GPU holds until the process ends, set up
+ * once per device by rmoe_create.  It allocates nothing and needs no rmoe_reserve, for
+ * callers that cannot allocate: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation.  A layer and k whose scratch exceeds 4 MiB is
+ * rejected with RMOE_EINVAL (the BASELINE shape at k=8 needs ~0.7 MiB, the reference
+ * model's at k=6 ~0.9 MiB).  All calls on one GPU share the array: calls that overlap on
+ * one GPU (any context, any stream) race.  No counterpart in the reference. */
+int rmoe_moe_experts_static_dev(rmoe_ctx* ctx, int layer, const void* x_dev, const void* top_ids_dev,
+                                const void* top_weights_dev, int k, int act, float gate_beta, float value_beta,
+                                void* out_dev, void* stream);
+
 /* Router + routed + shared expert + combine for one decode token, all on the device:
  * RaonModel._moe_token (host/raon.py:1288-1330) with the router moved onto the GPU.
  * out = RTNE(f32(routed) + f32(shared)); with residual != 0 also adds x:

@@ -70,6 +70,7 @@ SIGNATURES: dict[str, list] = {
     "rmoe_route": [_p, _i, _p, _i, _p, _p, _p],
     "rmoe_moe_experts": [_p, _i, _p, _p, _p, _i, _i, _f, _f, _p],
     "rmoe_moe_experts_dev": [_p, _i, _p, _p, _p, _i, _i, _f, _f, _p, _p],
+    "rmoe_moe_experts_static_dev": [_p, _i, _p, _p, _p, _i, _i, _f, _f, _p, _p],
     "rmoe_moe_decode_dev": [_p, _i, _p, _p, _i, _i, _f, _f, _p, _p, _p],
     "rmoe_moe_decode_stage_dev": [_p, _i, _i, _p, _p, _i, _i, _f, _f, _p],
     "rmoe_reserve_decode_stack": [_p, _p, _i],

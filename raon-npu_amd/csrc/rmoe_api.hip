@@ -7,6 +7,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <set>
 
 #include "../../include/raon_moe.h"
@@ -216,6 +217,46 @@ int check_ids(const int32_t* ids, int T, int k, int n_routed) {
   return RMOE_OK;
 }
 
+// ------------------------------------------------------- static decode scratch --
+// rmoe_moe_experts_static_dev runs the routed-expert decode kernels on this file-scope
+// device array instead of context scratch, so it never allocates.  Each GPU holds its
+// own copy until the process ends.  Layout: the kernels' arrival counters (which must
+// be zero when a launch starts, and which every complete launch leaves at zero), then
+// the fp32 partial sums, the activations h and the expert outputs.
+constexpr size_t kStaticScratchBytes = 4u << 20;
+constexpr size_t kStaticCounterBytes = 64u << 10;
+
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+namespace {
+
+// scratch's device address per device id, from hipGetSymbolAddress: in host code the
+// array's name is not a device address.
+std::mutex g_scratch_mu;
+std::map<int, uint8_t*> g_scratch_ptr;
+
+// Called by rmoe_create with the context's device current: the first context on a
+// device looks up the array's address and zeroes it (its counters must start at zero).
+int init_static_scratch(rmoe_ctx* ctx) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr.count(ctx->device)) return RMOE_OK;
+  void* p = nullptr;
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p) return fail(RMOE_EDEVICE, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+  HIP_TRY(hipMemsetAsync(p, 0, kStaticScratchBytes, ctx->stream));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  g_scratch_ptr[ctx->device] = static_cast<uint8_t*>(p);
+  return RMOE_OK;
+}
+
+uint8_t* static_scratch(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  auto it = g_scratch_ptr.find(device);
+  return it == g_scratch_ptr.end() ? nullptr : it->second;
+}
+
 }  // namespace
 
 extern "C" {
@@ -243,6 +284,13 @@ int rmoe_create(int device, rmoe_ctx** out) {
   }
   hipMemsetAsync(ctx->s.err, 0, sizeof(int), ctx->stream);
   hipStreamSynchronize(ctx->stream);
+  if (init_static_scratch(ctx) != RMOE_OK) {
+    const std::string msg = g_err;
+    hipFree(ctx->s.err);
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return fail(RMOE_EDEVICE, "%s", msg.c_str());
+  }
   // The persistent decode kernel runs one workgroup per CU and needs all of them
   // resident at once.
   int n_cu = 0, per_cu = 0;
@@ -837,6 +885,46 @@ int rmoe_moe_experts_dev(rmoe_ctx* ctx, int layer, const void* x_dev, const void
                                          nullptr, (uint16_t*)out_dev, ctx->s, pick_stream(ctx, stream));
   if (e == hipErrorInvalidValue)
     return fail(RMOE_EINVAL, "scratch too small for layer %d with k=%d: call rmoe_reserve", layer, k);
+  HIP_TRY(e);
+  return RMOE_OK;
+}
+
+int rmoe_moe_experts_static_dev(rmoe_ctx* ctx, int layer, const void* x_dev, const void* top_ids_dev,
+                                const void* top_weights_dev, int k, int act, float gate_beta, float value_beta,
+                                void* out_dev, void* stream) {
+  RmoeLayer* L;
+  TRY(check_layer(ctx, layer, &L));
+  if (!x_dev || !top_ids_dev || !top_weights_dev || !out_dev) return fail(RMOE_EINVAL, "null argument");
+  if (k < 1 || k > 16 || k > L->n_routed) return fail(RMOE_EINVAL, "k (%d) must be in 1..min(16, n_routed)", k);
+  if (act != RMOE_ACT_SITU && act != RMOE_ACT_SWIGLU) return fail(RMOE_EINVAL, "unknown activation %d", act);
+  uint8_t* base = static_scratch(ctx->device);
+  if (!base) return fail(RMOE_EDEVICE, "static scratch of device %d was not set up", ctx->device);
+  // The same scratch the routed-expert decode kernels take from a context (k slots, no
+  // shared slot), carved out of the static array.
+  RmoeLayer Lk = *L;
+  Lk.top_k = k;
+  Lk.n_shared = 0;
+  const size_t nc = rmoe::decode_scratch_counters(Lk), nf = rmoe::decode_scratch_floats(Lk);
+  const size_t nh = (size_t)k * L->Ipad, nd = (size_t)k * L->H;
+  const size_t off_f = kStaticCounterBytes, off_h = align_up(off_f + nf * 4, 256);
+  const size_t off_d = align_up(off_h + nh * 2, 256), need = off_d + nd * 4;
+  if (nc * 4 > kStaticCounterBytes || need > kStaticScratchBytes)
+    return fail(RMOE_EINVAL, "layer %d with k=%d needs %zu bytes of static decode scratch, more than its %zu",
+                layer, k, need, kStaticScratchBytes);
+  RmoeScratch s{};
+  s.counters = reinterpret_cast<unsigned*>(base);
+  s.n_counters = kStaticCounterBytes / 4;
+  s.part = reinterpret_cast<float*>(base + off_f);
+  s.part_floats = nf;
+  s.h = reinterpret_cast<uint16_t*>(base + off_h);
+  s.h_elems = nh;
+  s.dout = reinterpret_cast<float*>(base + off_d);
+  s.dout_elems = nd;
+  s.err = ctx->s.err;
+  hipError_t e = rmoe::launch_moe_decode(*L, (const uint16_t*)x_dev, (const int32_t*)top_ids_dev,
+                                         (const float*)top_weights_dev, k, false, act, gate_beta, value_beta, false,
+                                         nullptr, (uint16_t*)out_dev, s, pick_stream(ctx, stream));
+  if (e == hipErrorInvalidValue) return fail(RMOE_EINVAL, "layer %d with k=%d does not fit the static scratch", layer, k);
   HIP_TRY(e);
   return RMOE_OK;
 }

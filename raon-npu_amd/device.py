@@ -363,6 +363,19 @@ class MoeLayer:
         call("rmoe_moe_experts_dev", self.ctx.handle, self.layer, ptr(x_dev), ptr(ids_dev), ptr(wts_dev), k, act, gb,
              vb, ptr(out_dev), _stream_ptr(stream))
 
+    def moe_experts_static_dev(self, x_dev, ids_dev, wts_dev, out_dev, gate_beta=4.0, value_beta=25.0, stream=None):
+        """``moe_experts_dev`` on the library's static per-device scratch: allocates nothing
+        and needs no ``reserve``; calls overlapping on one GPU race."""
+        g = self.geom
+        _check_dev(x_dev, (g.hidden,), "int16", "x")
+        _check_dev(out_dev, (g.hidden,), "int16", "out")
+        k = int(ids_dev.shape[0]) if hasattr(ids_dev, "shape") and len(ids_dev.shape) == 1 else -1
+        _check_dev(ids_dev, (k,), "int32", "ids")
+        _check_dev(wts_dev, (k,), "float32", "wts")
+        act, gb, vb = act_code(gate_beta, value_beta)
+        call("rmoe_moe_experts_static_dev", self.ctx.handle, self.layer, ptr(x_dev), ptr(ids_dev), ptr(wts_dev), k,
+             act, gb, vb, ptr(out_dev), _stream_ptr(stream))
+
     def moe_decode(self, x, residual: bool = False, gate_beta=None, value_beta=None):
         """Router + routed + shared + combine for one token; returns (out, top_ids, weights)."""
         xa = _u16(x, "x").reshape(-1)
