@@ -20,9 +20,10 @@
 //     stream them, each with the h of its 128 columns.
 // Hand-offs between workgroups (per layer):
 //   h         tagged words (below): DN waves poll the words of their own columns
-//   band[b]   counter: every slot has written d of band b; the last one to arrive
-//             combines the band, writes x_{l+1}[band] and the band's share of the router
-//             logits of layer l+1                                   -> ready[l+1]
+//   d         tagged words: the combiner of band b (the workgroup whose first DN unit is
+//             slot 0 of band b) polls the band's words of every slot, combines the band,
+//             writes x_{l+1}[band] and the band's share of the router logits of layer l+1
+//                                                                    -> ready[l+1]
 //   ready     counter: all bands of x_l and of its partial router logits are written
 // Every workgroup computes the top-k of a layer itself from the partial logits (the
 // same reads in the same order give the same routing everywhere), and loads the weight
@@ -138,7 +139,7 @@ __device__ __forceinline__ float tile_dot(const TileRegs& r, const uint32_t* xw,
   return acc;
 }
 
-// Counters of layer l: kReadyCopies copies of ready, then the nb2 band counters.
+// Counters of layer l: kReadyCopies copies of ready.
 // Every counter sits on its own 256-byte line: atomics and polls on one line are served
 // one at a time at the memory side, and a layer's counters see hundreds of them.
 constexpr int kCntPad = 64;  // uint32 per counter line
@@ -475,6 +476,32 @@ __device__ __forceinline__ void load_router_slice(const StackArgs& a, const uint
   }
 }
 
+// The router slice of band b (64 columns of every expert row, 128 B each) copied into
+// LDS as [expert, E rounded up to 8][128 B] by waves 1..7 (w = wave - 1): one copy
+// instruction moves 8 expert rows (lane L: row 8j + L/8, bytes 16(L%8)..; rows past E
+// copy row E-1 into slots nobody reads), dealt round robin to the 7 waves.
+__device__ __forceinline__ int router_rows8(const StackArgs& a) { return (a.E + 7) & ~7; }
+__device__ __forceinline__ void dma_router_slice(const StackArgs& a, const uint16_t* rw, int b, uint8_t* dst, int w,
+                                                 int lane) {
+  for (int j = w; j < router_rows8(a) / 8; j += kWaves - 1) {
+    const int e = min(8 * j + (lane >> 3), a.E - 1);
+    const uint16_t* src = rw + (size_t)e * a.H + 64 * b + 8 * (lane & 7);
+    __builtin_amdgcn_global_load_lds((global_void_ptr)src, (lds_void_ptr)(dst + (size_t)j * 1024), 16, 0, 0);
+  }
+}
+// This thread's items of a router slice in LDS (the register layout of load_router_slice:
+// item tid + kThreads * it is expert item / 4, columns 16 * (item % 4)..).
+template <int NIT>
+__device__ __forceinline__ void read_router_slice(const StackArgs& a, const uint8_t* src, uint4 (&wv)[NIT][2]) {
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int idx = threadIdx.x + kThreads * it;
+    const int i = idx < a.E * 4 ? idx : 0;
+    wv[it][0] = *reinterpret_cast<const uint4*>(src + 32 * i);
+    wv[it][1] = *reinterpret_cast<const uint4*>(src + 32 * i + 16);
+  }
+}
+
 // DNPOS: DN tiles per DN wave (waves 1..7 stream the tiles of both DN units:
 // 2 * Ipad/128 <= 7 * DNPOS); NIT: router items per thread (n_routed <= 128 * NIT);
 // They size register and LDS arrays, so they are template
@@ -497,7 +524,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
   __shared__ float cmb[kMaxSlots][64];                         // d of every slot of a band
   __shared__ __attribute__((aligned(16))) uint32_t xband[32];  // x_{l+1} of a band, bf16 pairs
   __shared__ __attribute__((aligned(16))) float lrow[kLRow];   // partial logits being summed
-  __shared__ unsigned flag, band_last_d[kMaxDnUnits];
+  __shared__ unsigned flag;
   // DN tiles of this workgroup's units: [kMaxDnUnits][nkt2] tiles, then a 1 KB sink.
   extern __shared__ __attribute__((aligned(16))) uint8_t dn_lds[];
   uint8_t* dn_sink = dn_lds + (size_t)kMaxDnUnits * a.nkt2 * kTileBytes;
@@ -543,14 +570,22 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
   }
 
   for (int l = 0; l < a.L; ++l) {
+    // The thread index passes through an empty asm at the top of every layer, so values
+    // derived from it (LDS and row addresses of every phase) are recomputed per layer
+    // instead of being hoisted out of the loop, where together they held enough
+    // registers across all phases to force spills: scratch reloads on the hand-off path,
+    // each one a memory round trip, and s_waitcnt vmcnt(0) after them also waited for
+    // the wave's weight loads.
+    int tid_o = (int)threadIdx.x;
+    asm volatile("" : "+v"(tid_o));
+    const int tid = tid_o, lane = tid & 63, wave = tid >> 6;
     unsigned* c_ready = cnt_at(a, l, g % kReadyCopies);
-    auto c_band = [&](int b) { return cnt_at(a, l, kReadyCopies + b); };
     uint8_t* lay = a.scratch + (size_t)l * a.layer_bytes;
     const uint32_t* xin = reinterpret_cast<const uint32_t*>(lay);
     const float* lpart = reinterpret_cast<const float*>(lay + a.off_lpart);
     uint64_t* hbuf = reinterpret_cast<uint64_t*>(lay + a.off_h);  // [S][Ipad/2] tagged h pairs
     const int hstride = a.Ipad / 2;
-    float* dout = reinterpret_cast<float*>(lay + a.off_dout);
+    uint64_t* dtag = reinterpret_cast<uint64_t*>(lay + a.off_dout);  // [S][H] tagged d words
 
     if (!wait_geq(a, c_ready, (unsigned)a.nb2, &flag)) return;
 
@@ -707,8 +742,8 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
       gu_unit(s, hb);
     }
 
-    // ---- DN units, both of a workgroup at once, and the combine of a band by the last
-    // slot to finish it.
+    // ---- DN units, both of a workgroup at once, and the combine of a band by its
+    // combiner.
     if (n_dn_t > 0) {
       // h of each of this wave's DN tiles: lane covers columns 128kt + 2*lane (+1), one
       // tagged word per tile, polled until it carries this launch's tag (columns past I
@@ -787,60 +822,75 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
           }
         }
       }
-      // Router weights of the next layer for the band shares of the logits: issued now,
-      // in flight during the band hand-off (holding them from the start of the layer
-      // would cost registers through the GU and DN phases).
-      uint4 rwv[kMaxDnUnits][NIT][2];
-#pragma unroll
-      for (int d = 0; d < kMaxDnUnits; ++d)
-        load_router_slice<NIT>(a, a.rw[l + 1 < a.L ? l + 1 : l], dn_d[d][1], dn_d[d][0] >= 0 && l + 1 < a.L, dummy,
-                               rwv[d]);
       red[wave][0][lane] = acc[0];
       red[wave][1][lane] = acc[1];
       __syncthreads();
+      // The combiner of band b is the workgroup whose first DN unit is (slot 0, band b):
+      // slot 0's units are units 0..nb2-1, and unit v is the first unit of workgroup
+      // (n_gu + v) mod G, so every band has exactly one.
+      const bool comb = dn_d[0][0] == 0;
+      const int cb = dn_d[0][1];
+      // The next layer's router weights of the combined band, copied into the DN tiles'
+      // LDS (every wave is done with the tiles) by waves 1..7 while wave 0 hands d over.
+      // They are drained before the logits.
+      uint8_t* rw_lds = dn_lds;  // [E rounded up to 8][128 B]
+      if (comb && wave > 0 && l + 1 < a.L) dma_router_slice(a, a.rw[l + 1], cb, rw_lds, wave - 1, lane);
       if (wave == 0) {
-        // Expert outputs of both units, then both arrivals (issued together).
-        static_assert(kMaxDnUnits == 2, "two DN units per workgroup");
-        const bool has0 = dn_d[0][0] >= 0, has1 = dn_d[1][0] >= 0;
+        // d of both units as tagged words: no store acknowledgement and no counter; the
+        // combiner polls the words of its band.
 #pragma unroll
         for (int d = 0; d < kMaxDnUnits; ++d) {
           if (dn_d[d][0] < 0) continue;
           float dd = 0.f;
 #pragma unroll
           for (int w = 1; w < kWaves; ++w) dd += red[w][d][lane];
-          st_dev(&dout[(size_t)dn_d[d][0] * a.H + 64 * dn_d[d][1] + lane], bf16_round(dd));
+          st_dev_u64(&dtag[(size_t)dn_d[d][0] * a.H + 64 * dn_d[d][1] + lane],
+                     (uint64_t)__float_as_uint(bf16_round(dd)) | ((uint64_t)tag << 32));
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_s_waitcnt(0);
-        unsigned prev0 = 0u, prev1 = 0u;
-        if (lane == 0) {
-          if (has0) prev0 = __hip_atomic_fetch_add(c_band(dn_d[0][1]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          if (has1) prev1 = __hip_atomic_fetch_add(c_band(dn_d[1][1]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        prev0 = __builtin_amdgcn_readfirstlane(prev0);
-        prev1 = __builtin_amdgcn_readfirstlane(prev1);
-        if (lane == 0) {
-          band_last_d[0] = (has0 && prev0 + 1u == (unsigned)a.S) ? 1u : 0u;
-          band_last_d[1] = (has1 && prev1 + 1u == (unsigned)a.S) ? 1u : 0u;
-        }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
       }
-      __syncthreads();
-      for (int d = 0; d < kMaxDnUnits; ++d) {
-        if (band_last_d[d] == 0u) continue;
-        const int b = dn_d[d][1];
+      if (comb) {
+        const int row = 64 * cb + lane;
+        bool cfailed = false;
         if (wave == 0) {
-          const int row = 64 * b + lane;
-          // d of every slot for this band into LDS, up to 9 loads in flight.
-          for (int q0 = 0; q0 < a.S; q0 += 9) {
-            float dv[9];
+          // d of every slot of the band into LDS: each lane polls its row's word of every
+          // slot (up to 9 loads in flight) until all carry this launch's tag.  Bounded
+          // like the h wait.
+          unsigned need = (1u << a.S) - 1u;
+          unsigned it = 0;
+          while (true) {
+            for (int q0 = 0; q0 < a.S; q0 += 9) {
+              uint64_t dv[9];
 #pragma unroll
-            for (int i = 0; i < 9; ++i)
-              if (q0 + i < a.S) dv[i] = ld_hand_f32(&dout[(size_t)(q0 + i) * a.H + row]);
+              for (int i = 0; i < 9; ++i)
+                dv[i] = (q0 + i < a.S && ((need >> (q0 + i)) & 1u)) ? ld_dev_u64(&dtag[(size_t)(q0 + i) * a.H + row])
+                                                                    : 0ull;
 #pragma unroll
-            for (int i = 0; i < 9; ++i)
-              if (q0 + i < a.S) cmb[q0 + i][lane] = dv[i];
+              for (int i = 0; i < 9; ++i) {
+                if (q0 + i < a.S && ((need >> (q0 + i)) & 1u) && (uint32_t)(dv[i] >> 32) == tag) {
+                  cmb[q0 + i][lane] = __uint_as_float((uint32_t)dv[i]);
+                  need &= ~(1u << (q0 + i));
+                }
+              }
+            }
+            if (!__any(need != 0u)) break;
+            ++it;
+            if ((it & 63u) == 0u && ld_dev_u32(abort_flag(a)) != 0u) {
+              cfailed = true;
+              break;
+            }
+            if (it > kSpinLimit) {
+              if (lane == 0) {
+                st_dev_u32(abort_flag(a), 1u);
+                __hip_atomic_fetch_or(a.err, 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              }
+              cfailed = true;
+              break;
+            }
+            __builtin_amdgcn_s_sleep(1);
           }
+        }
+        if (__syncthreads_or(cfailed ? 1 : 0)) return;
+        if (wave == 0) {
           // Ascending expert id: the slot order, then each slot's value and weight, read
           // from LDS in batches, then summed in order.
           float acc2 = 0.f;
@@ -874,13 +924,16 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
           }
         }
         if (l + 1 < a.L) {
+          if (wave > 0) __builtin_amdgcn_s_waitcnt(0);  // the router slice is in LDS
           __syncthreads();
           float* lnext = reinterpret_cast<float*>(lay + a.layer_bytes + a.off_lpart);
-          band_logits<NIT>(a, xband, rwv[d], lnext, b);
+          uint4 rwv[NIT][2];
+          read_router_slice<NIT>(a, rw_lds, rwv);
+          band_logits<NIT>(a, xband, rwv, lnext, cb);
           block_publish_ready(a, l + 1);
         }
-        __syncthreads();  // xband / cmb are reused by the next band
       }
+      if (wave > 0) __builtin_amdgcn_s_waitcnt(0);  // router slice copies have landed
     }
   }
 
@@ -906,7 +959,11 @@ struct StackShape {
 size_t al256(size_t v) { return (v + 255) / 256 * 256; }
 
 // Dynamic LDS of the kernel: the DN tiles of kMaxDnUnits units plus the 1 KB sink.
-size_t dn_lds_bytes(int nkt2) { return (size_t)kMaxDnUnits * nkt2 * kTileBytes + 1024; }
+// The same LDS holds the next layer's router slice of the combined band once the DN
+// tiles are consumed (E rounded up to 8 rows of 128 B each).
+size_t dn_lds_bytes(int nkt2, int n_routed) {
+  return std::max((size_t)kMaxDnUnits * nkt2 * kTileBytes + 1024, (size_t)((n_routed + 7) & ~7) * 128);
+}
 constexpr size_t kLdsLimit = 160 * 1024;   // per CU on gfx950
 constexpr size_t kStaticLds = 48 * 1024;   // bound on the kernel's static LDS
 
@@ -926,9 +983,9 @@ StackShape stack_shape(const RmoeLayer& L) {
   sh.off_h = off;
   off += al256((size_t)sh.S * (L.Ipad / 2) * 8);
   sh.off_dout = off;
-  off += al256((size_t)sh.S * L.H * 4);
+  off += al256((size_t)sh.S * L.H * 8);  // tagged d words
   sh.layer_bytes = off;
-  sh.cnt_stride = kReadyCopies + sh.nb2;
+  sh.cnt_stride = kReadyCopies;
   return sh;
 }
 
@@ -947,7 +1004,7 @@ size_t stack_counter_count(const RmoeLayer& L, int n_layers) {
 hipError_t stack_check(const RmoeLayer& L, int n_cu) {
   const StackShape sh = stack_shape(L);
   if (L.H > kMaxH || L.n_routed > kMaxE || sh.S > kMaxSlots || kMaxDnUnits * sh.nkt2 > (kWaves - 1) * kMaxDnPos ||
-      L.I % 64 != 0 || dn_lds_bytes(sh.nkt2) + kStaticLds > kLdsLimit)
+      L.I % 64 != 0 || dn_lds_bytes(sh.nkt2, L.n_routed) + kStaticLds > kLdsLimit)
     return hipErrorInvalidValue;
 
   if (sh.n_dn > kMaxDnUnits * n_cu || n_cu < sh.nb2) return hipErrorInvalidValue;
@@ -1011,7 +1068,7 @@ hipError_t launch_decode_stack(const RmoeLayer* const* layers, int n_layers, con
     a.rw[l] = Ll.router_w;
     a.rb[l] = Ll.router_bias;
   }
-  const size_t lds = dn_lds_bytes(sh.nkt2);
+  const size_t lds = dn_lds_bytes(sh.nkt2, L0.n_routed);
   const dim3 grid(n_cu), block(kThreads);
   const int pos_need = (kMaxDnUnits * sh.nkt2 + kWaves - 2) / (kWaves - 1);
   if (pos_need <= 2 && a.E <= 128)
