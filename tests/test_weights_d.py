@@ -102,7 +102,7 @@ _DROP = object()
     ("L02/moe_b1", {"expert_count": 129}, "expert_count is"),
     ("L02/moe_b1", {"expert_bytes": 3481601}, "expert_bytes is"),
     ("L02/shared_gu", {"size_bytes": True}, "is not a byte count"),
-    ("L02/shared_gu", {"size_bytes": 6266881}, "differs from the canonical"),
+    ("L02/shared_gu", {"size_bytes": 6266881}, "canonical size_bytes mismatch"),
     ("lm_head", {"sha256": "xyz"}, "is not 64 hex digits"),
     ("lm_head", {"sha256": "ab" * 31}, "is not 64 hex digits"),
     ("L00/f_b", {"file": "../f_b.bin"}, "must be relative"),
