@@ -7,6 +7,9 @@
 // to four waves covers one 64-row band over a range of K tiles; bands split over K
 // write fp32 partials and the last workgroup of a band (device-scope counter) adds
 // them in K order, so the result does not depend on arrival order.
+// Matrices with at most kBandMaxTiles K tiles take linear_band_kernel instead: one
+// workgroup per 16, 32 or 64 rows with the K tiles spread over its lanes and waves, no
+// split and no partials.
 #include <algorithm>
 
 #include "rmoe_internal.h"
@@ -115,16 +118,133 @@ __global__ __launch_bounds__(256) void linear_kernel(LinearArgs a) {
   }
 }
 
+constexpr int kBandMaxTiles = 32;  // K tiles handled by one workgroup in linear_band_kernel
+constexpr int kBandMaxWaves = 16;
+constexpr int kXPad = 4;           // dwords of padding after each K tile's x in LDS
+
+// One workgroup per R rows of a 64-row band (and group of kNT tokens), no K split and
+// no partials.  The wave's lanes form 64 / R groups of R rows; group g of wave w takes
+// K tile w * (64 / R) + g (then every waves * (64 / R)-th further tile), so a band is
+// spread over 64 / R workgroups and every SIMD streams about one tile's worth of work.
+// Every lane requests its first tile before x is staged, so the latencies of the
+// weights and of x overlap.  Group sums of x come from registers while x is staged.
+// The lane groups' sums meet by shuffles (a fixed tree), the waves' in LDS, added in
+// wave order: the result does not depend on timing.
+template <int R>
+__global__ __launch_bounds__(1024) void linear_band_kernel(LinearArgs a) {
+  constexpr int G = 64 / R;
+  // Dynamic LDS: x as bf16 pairs [kNT][nkt][64 + kXPad] (the padding puts the lane
+  // groups' tiles in different banks), the group sums [kNT][nkt * 4], then the waves'
+  // sums [waves][kNT][R].
+  extern __shared__ __attribute__((aligned(16))) uint32_t lin_lds[];
+  const int nkt = a.K / kTileCols;
+  const int row0 = blockIdx.x * R;
+  const int rsub = row0 % kTileRows;
+  const int tok0 = blockIdx.y * kNT;
+  const int nt = min(kNT, a.T - tok0);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int g = lane / R, r = lane % R;
+  const int tstride = 64 + kXPad;
+  const int xstride = nkt * tstride;
+  uint32_t* xs = lin_lds;
+  float* ssum = reinterpret_cast<float*>(lin_lds + kNT * xstride);
+  float* red = ssum + kNT * nkt * 4;
+
+  // This thread's first 16 bytes of x are requested before the weights: loads complete
+  // in order, so x is then not held up behind the tiles and its staging overlaps them.
+  const int units = nkt * 16;  // 16-byte units of x per token (8 values each)
+  const int total = nt * units;
+  const uint8_t* band = a.tiles + (size_t)(row0 / kTileRows) * nkt * kTileBytes + (size_t)(rsub + r) * 16;
+  const int kt0 = wave * G + g;
+  uint4 c[4], smq;
+  {
+    const uint8_t* tile = band + (size_t)(kt0 < nkt ? kt0 : 0) * kTileBytes;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c[j] = load_stream16(tile + j * 1024);
+    smq = load_stream16(tile + kCodeBytes);
+  }
+
+  // x in 16-byte units; the 4 units of a 32-column group are held by 4 neighbouring
+  // lanes, whose sums are added by shuffles.
+  for (int i = tid; i < total; i += blockDim.x) {
+    const int t = i / units, u = i % units;
+    const uint4 v = reinterpret_cast<const uint4*>(a.x + (size_t)(tok0 + t) * a.K)[u];
+    *reinterpret_cast<uint4*>(xs + t * xstride + (u >> 4) * tstride + (u & 15) * 4) = v;
+    float sv = ((bf16_to_f32(v.x & 0xffffu) + bf16_to_f32(v.x >> 16)) +
+                (bf16_to_f32(v.y & 0xffffu) + bf16_to_f32(v.y >> 16))) +
+               ((bf16_to_f32(v.z & 0xffffu) + bf16_to_f32(v.z >> 16)) +
+                (bf16_to_f32(v.w & 0xffffu) + bf16_to_f32(v.w >> 16)));
+    sv += __shfl_xor(sv, 1, 64);
+    sv += __shfl_xor(sv, 2, 64);
+    if ((u & 3) == 0) ssum[t * nkt * 4 + (u >> 2)] = sv;
+  }
+  __syncthreads();
+
+  float acc[kNT];
+#pragma unroll
+  for (int t = 0; t < kNT; ++t) acc[t] = 0.f;
+  for (int kt = kt0; kt < nkt; kt += nwaves * G) {
+    if (kt != kt0) {
+      const uint8_t* tile = band + (size_t)kt * kTileBytes;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c[j] = load_stream16(tile + j * 1024);
+      smq = load_stream16(tile + kCodeBytes);
+    }
+    const uint32_t sm[4] = {smq.x, smq.y, smq.z, smq.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int t = 0; t < kNT; ++t) {
+        if (t < nt) {
+          const float d = group_dot(c[j], xs + t * xstride + kt * tstride + j * 16);
+          acc[t] = group_apply(sm[j], d, ssum[t * nkt * 4 + kt * 4 + j], acc[t]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kNT; ++t) {
+    float v = acc[t];
+#pragma unroll
+    for (int m = R; m < 64; m *= 2) v += __shfl_xor(v, m, 64);
+    if (g == 0) red[(wave * kNT + t) * R + r] = v;
+  }
+  __syncthreads();
+  for (int t = wave; t < nt; t += nwaves) {
+    if (lane < R) {
+      float v = 0.f;
+      for (int w = 0; w < nwaves; ++w) v += red[(w * kNT + t) * R + lane];
+      a.y[(size_t)(tok0 + t) * a.M + row0 + lane] = (uint16_t)f32_to_bf16(v);
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t launch_linear(const uint8_t* tiles, int M, int K, const uint16_t* x, int T, uint16_t* y, RmoeScratch& s,
                          hipStream_t st) {
   const int nkt = K / kTileCols, n_rt = M / kTileRows;
+  const int ychunks = (T + kNT - 1) / kNT;
+  // The band kernel reads x in 16-byte pieces; other x take the K-split kernel.
+  if (nkt <= kBandMaxTiles && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    // Rows per workgroup: whole bands when the bands alone fill the chip, else 32 or 16
+    // rows, so that a small matrix still spreads over many CUs.
+    const int R = n_rt >= 64 ? 64 : n_rt >= 32 ? 32 : 16;
+    const int G = 64 / R;
+    const int waves = std::min(kBandMaxWaves, (nkt + G - 1) / G);
+    const size_t lds = ((size_t)kNT * nkt * (64 + kXPad + 4) + (size_t)waves * kNT * R) * 4;
+    LinearArgs a{tiles, M, K, x, T, y, nullptr, nullptr, 1};
+    const dim3 grid(M / R, ychunks), block(64 * waves);
+    if (R == 64) hipLaunchKernelGGL(linear_band_kernel<64>, grid, block, lds, st, a);
+    else if (R == 32) hipLaunchKernelGGL(linear_band_kernel<32>, grid, block, lds, st, a);
+    else hipLaunchKernelGGL(linear_band_kernel<16>, grid, block, lds, st, a);
+    return hipGetLastError();
+  }
   // Up to 4 K tiles per workgroup (one per wave); tall matrices, whose row bands alone
   // fill the chip, split K less (down to one workgroup per band) and skip the partials.
   int ksplit = std::min((nkt + 3) / 4, (kFillGroups + n_rt - 1) / n_rt);
   ksplit = std::max({1, ksplit, (nkt + kMaxRange - 1) / kMaxRange});
-  const int ychunks = (T + kNT - 1) / kNT;
   const size_t need_part = (size_t)ychunks * n_rt * ksplit * kNT * 64;
   const size_t need_cnt = (size_t)ychunks * n_rt;
   if (ksplit > 1 && (need_part > s.part_floats || need_cnt > s.n_counters)) return hipErrorInvalidValue;

@@ -41,7 +41,9 @@ def test_config1_gemv(gpu_ctx):
 
 
 @pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 9])
-@pytest.mark.parametrize("M,K", [(128, 256), (1536, 2048), (2048, 768), (2176, 2560)])
+# K <= 4096 runs one workgroup per row band (linear_band_kernel); K = 5120 runs the K-split
+# kernel with its partials and ordered final sum.
+@pytest.mark.parametrize("M,K", [(128, 256), (1536, 2048), (2048, 768), (2176, 2560), (256, 5120)])
 def test_gemv_tokens_and_shapes(gpu_ctx, T, M, K):
     blob, wf, rng = _case(M, K, M * 7 + K + T)
     x = f32_to_bf16(rng.standard_normal((T, K)).astype(np.float32))
