@@ -274,6 +274,16 @@ int rmoe_moe_experts_grouped(rmoe_ctx* ctx, int layer, const uint16_t* x, int T,
                              const float* top_weights, const uint16_t* shared_gu, int act, float gate_beta,
                              float value_beta, uint16_t* routed, uint16_t* shared_down);
 
+/* rmoe_moe_experts_grouped on device-resident operands (the same contract,
+ * npu/backend.py:4845-4979): x_dev bf16 [T, H], top_ids_dev int32 [T, k], top_weights_dev
+ * fp32 [T, k], shared_gu_dev bf16 [T, 2I] -> routed_dev and shared_down_dev bf16 [T, H], on
+ * `stream` (null: the context's stream), asynchronously.  T must not exceed the tokens
+ * reserved with rmoe_reserve; an expert id out of range is reported by the next
+ * synchronous call. */
+int rmoe_moe_experts_grouped_dev(rmoe_ctx* ctx, int layer, const void* x_dev, int T, const void* top_ids_dev,
+                                 const void* top_weights_dev, const void* shared_gu_dev, int act, float gate_beta,
+                                 float value_beta, void* routed_dev, void* shared_down_dev, void* stream);
+
 /* Full prefill MoE layer on the device (host/raon.py:1565-1602 grouped branch): router,
  * dispatch, grouped gate/up + activation, grouped down, ordered combine, shared expert.
  * out [T, H] = RTNE(f32(routed) + f32(shared_down)) (+ x when residual != 0). */

@@ -80,6 +80,7 @@ SIGNATURES: dict[str, list] = {
     "rmoe_dispatch": [_p, _p, _i, _i, _i, _p, _p],
     "rmoe_moe_experts_grouped": [_p, _i, _p, _i, _p, _p, _p, _i, _f, _f, _p, _p],
     "rmoe_moe_prefill_dev": [_p, _i, _p, _i, _p, _i, _i, _f, _f, _p, _p, _p],
+    "rmoe_moe_experts_grouped_dev": [_p, _i, _p, _i, _p, _p, _p, _i, _f, _f, _p, _p, _p],
 }
 _RESTYPES = {"rmoe_last_error": C.c_char_p, "rmoe_version": C.c_char_p, "rmoe_stream": _p}
 

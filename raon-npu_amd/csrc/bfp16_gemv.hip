@@ -100,6 +100,27 @@ __global__ __launch_bounds__(256) void b16_relayout_out_kernel(const uint8_t* __
     dst[ref_group(R, kt * kTileCols + 8 * g, kb_n) + r16] = (uint8_t)(e[g >> 2] >> (8 * (g & 3)));
 }
 
+// Per row of a tiled bfp16 matrix, the largest kernel exponent max(e, 7) over the
+// blocks of its first k_valid columns (columns past k_valid are padding whose bytes are
+// not guaranteed).  The grouped prefill GEMM shifts each weight row by it so that every
+// m * 2^(e - 133) of the row is an exact fp16 value.  One thread per row.
+__global__ __launch_bounds__(256) void b16_rowexp_kernel(const uint8_t* __restrict__ tiles, int M, int K, int k_valid,
+                                                         uint8_t* __restrict__ rowexp) {
+  const int R = blockIdx.x * blockDim.x + threadIdx.x;
+  if (R >= M) return;
+  const int nkt = K / kTileCols, nblk = k_valid / 8;
+  const uint8_t* base = tiles + (size_t)(R / kTileRows) * nkt * kB16TileBytes + kB16MantBytes + (R % kTileRows) * 16;
+  uint32_t m = 7u;
+  for (int kt = 0; kt < nkt; ++kt) {
+    const uint4 v = *reinterpret_cast<const uint4*>(base + (size_t)kt * kB16TileBytes);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int g = 0; g < 16; ++g)
+      if (16 * kt + g < nblk) m = max(m, (w[g >> 2] >> (8 * (g & 3))) & 0xffu);
+  }
+  rowexp[R] = (uint8_t)m;
+}
+
 // ------------------------------------------------------------------------ GEMV --
 constexpr int kNT = 4;         // tokens per workgroup
 constexpr int kMaxRange = 32;  // K tiles per workgroup (x staged in LDS: <= 32 KB)
@@ -213,6 +234,11 @@ int bfp16_ksplit(int M, int K) {
 hipError_t launch_b16_relayout_in(const uint8_t* packed, uint8_t* tiles, int M, int K, hipStream_t st) {
   const size_t n = (size_t)(M / kTileRows) * (K / kTileCols) * 64;
   hipLaunchKernelGGL(b16_relayout_in_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, packed, tiles, M, K);
+  return hipGetLastError();
+}
+
+hipError_t launch_b16_rowexp(const uint8_t* tiles, int M, int K, int k_valid, uint8_t* rowexp, hipStream_t st) {
+  hipLaunchKernelGGL(b16_rowexp_kernel, dim3((unsigned)((M + 255) / 256)), dim3(256), 0, st, tiles, M, K, k_valid, rowexp);
   return hipGetLastError();
 }
 

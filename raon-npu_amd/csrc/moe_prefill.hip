@@ -15,6 +15,7 @@
 // scales are normalised by a power of two (largest scale in [2^11, 2^12)); the
 // exponents are undone exactly in fp32.  The correction (second sum) is a small GEMM over the groups, done on bf16 MFMA
 // with S and the coefficient split exactly into three bf16 parts (six leading products).
+#include "../../include/raon_moe.h"
 #include "rmoe_internal.h"
 
 namespace rmoe {
@@ -376,6 +377,9 @@ struct GemmArgs {
   int8_t* out_exp;          // mode 0: exponents of the h rows per 128-unit chunk [rows][exp_stride(out_ld)]
   int act;
   float gb, vb;
+  // bfp16 weights (down of a weights-d layer): per expert and weight row the largest
+  // max(e, 7) of the row's blocks ([experts][N_total]).
+  const uint8_t* rowexp;
 };
 
 __device__ __forceinline__ int group_end(const GemmArgs& a, int e) {
@@ -426,6 +430,9 @@ __device__ __forceinline__ void ring_wait(int pending) {
   switch (pending) {
     case 7: asm volatile("s_waitcnt vmcnt(7) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
     case 6: asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
     default: asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
   }
 }
@@ -433,6 +440,23 @@ __device__ __forceinline__ void ring_wait(int pending) {
 #define RMOE_WAIT_TIED(N, c)                                                                             \
   asm volatile("s_waitcnt vmcnt(" #N ") lgkmcnt(0)\n\ts_barrier"                                        \
                : "+v"(c[0][0]), "+v"(c[0][1]), "+v"(c[1][0]), "+v"(c[1][1])::"memory")
+// RMOE_WAIT_TIED with a count known only at run time, among the values the grouped GEMM
+// uses (they depend on the tile class and the wave).
+__device__ __forceinline__ void wait_tied(int pending, u32x4v (&c)[2][2]) {
+  switch (pending) {
+    case 17: RMOE_WAIT_TIED(17, c); break;
+    case 15: RMOE_WAIT_TIED(15, c); break;
+    case 14: RMOE_WAIT_TIED(14, c); break;
+    case 13: RMOE_WAIT_TIED(13, c); break;
+    case 12: RMOE_WAIT_TIED(12, c); break;
+    case 11: RMOE_WAIT_TIED(11, c); break;
+    case 10: RMOE_WAIT_TIED(10, c); break;
+    case 9: RMOE_WAIT_TIED(9, c); break;
+    case 8: RMOE_WAIT_TIED(8, c); break;
+    case 6: RMOE_WAIT_TIED(6, c); break;
+    default: RMOE_WAIT_TIED(0, c); break;
+  }
+}
 // (x & m) | o in one instruction (the compiler keeps the two-instruction form).
 __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
   uint32_t r;
@@ -506,7 +530,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint32_t* __r
   // Fragment f of this wave: weight tile (w/4) + 2f of the four, rows 16*(w%4)..+15.
   const int ft0 = wave >> 2, frow = 16 * (wave & 3) + l16;
 
-  // Copy descriptors.  Activations: copy q = wave + 8i (i < 4) fills LDS rows 4q..4q+3;
+  // Copy descriptors.  Activations: copy q = wave + 8i (i < MF / 2: the tile's 16 * MF
+  // live rows; the others are never read) fills LDS rows 4q..4q+3;
   // lane L brings row 4q + L/16 into position L%16 of the row: 16-byte chunk
   // tau((L%16) ^ (row%16)), tau(4a + b) = 4b + a.  A row's chunk c then sits at position
   // tau(c) ^ (row%16): the K loop's reads of chunks 4lq + j land on positions
@@ -526,10 +551,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint32_t* __r
     const int v = min(wave + 8 * i, 19), t = v / 5, p = v % 5;
     wg[i] = W + (size_t)band[t] * nkt * kTileBytes + 1024 * p + 16 * lane;
   }
+  constexpr int kXCopies = MF / 2;
   auto issue_to = [&](int kt, int slot) {
     const uint32_t sb = lds0 + (uint32_t)(slot * kStageBytes);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(xg[i] + (size_t)kt * 256, sb + 1024u * (uint32_t)(wave + 8 * i));
+    for (int i = 0; i < kXCopies; ++i) dma16(xg[i] + (size_t)kt * 256, sb + 1024u * (uint32_t)(wave + 8 * i));
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
       if (i < n_wcopy) {
@@ -539,7 +565,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint32_t* __r
     }
   };
   auto issue = [&](int kt) { issue_to(kt, kt % kStages); };
-  const int per_stage = 4 + n_wcopy;
+  const int per_stage = kXCopies + n_wcopy;
 
   // Group sums, planar per row: [hi | mid | lo] planes of Gp (G rounded up to 8) bf16.
   // Block b (groups 32b..32b+31) goes to half (b & 1) of ring slot 2 as 24 copies of
@@ -644,10 +670,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint32_t* __r
     }
   };
   // Block 0: past it are in flight group-sum block 1 (3) and K steps 0 and 1.
-  if (per_stage == 7) RMOE_WAIT_TIED(17, cf0); else RMOE_WAIT_TIED(15, cf0);
+  wait_tied(3 + 2 * per_stage, cf0);
   corr_block(0, cf0);
   if (nblk > 1) {
-    if (per_stage == 7) RMOE_WAIT_TIED(14, cf1); else RMOE_WAIT_TIED(12, cf1);
+    wait_tied(2 * per_stage, cf1);
     corr_block(1, cf1);
   }
   for (int blk = 2; blk < nblk; ++blk) {  // K > 2048: blocks reuse the halves of slot 2
@@ -920,11 +946,173 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint32_t* __r
   }
 }
 
+// The down GEMM of a bfp16 weight matrix (moe_b2 of a weights-d layer), with MF live
+// 16-row fragments.  Same tiling, copies of the activation rows, fragment assignment,
+// row exponents and epilogue as gemm_tile's mode 1; what differs:
+//   - a weight is m * 2^(e - 133) with an int8 mantissa m and the block's exponent byte e
+//     (e raised to 7; one exponent per 8 columns); a lane's 8 K columns of one MFMA are
+//     exactly one block.  With the row's largest exponent emax, B = m * 2^(e - emax + 8)
+//     is an exact fp16 value (|B| <= 2^15) for every block within 32 binades of emax
+//     (smaller blocks, below 2^-32 of the row's largest weight, underflow to 0), and the
+//     accumulator is undone by 2^(emax - 141) with the row exponent of the activations;
+//   - so there is no correction term: acc = sum_k x[m,k] * B[r,k] is the whole product;
+//   - a bfp16 tile is 9 KB: a ring stage (128 activation rows + four weight tiles) is
+//     68 KB and the ring is two stages deep (one step's copies land under the previous
+//     step's MFMAs).
+// B from the bytes: u = m + 128 (m ^ 0x80); v_perm_b32 pairs two u bytes with 0x64 bytes,
+// i.e. the fp16 values 1024 + u, and (1024 + u - 1152) * 2^p is m * 2^p, both steps exact.
+constexpr int kB16Stage = kXBytes + 4 * kB16TileBytes;  // 69,632
+static_assert(2 * kB16Stage <= kGemmLds, "two bfp16 stages fit the ring");
+
+template <int MF>
+__device__ __forceinline__ void gemm_tile_b16(const GemmArgs& a, const uint32_t* __restrict__ tl, int mt, int nt,
+                                              uint8_t* lds, int* rowidx, int8_t* row_e) {
+  const uint32_t te = tl[mt];
+  const int e = (int)(te & 511u), row0 = (int)(te >> 9);
+  const int rend = group_end(a, e);
+  const int nrows = min(kBM, rend - row0);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, lq = lane >> 4;
+  const int nkt = a.K / kTileCols;
+  const uint8_t* W = a.wbase + (size_t)e * a.wstride;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
+
+  if (tid < kBM) {
+    const int src = row0 + (tid < nrows ? tid : 0);  // sorted row of the down input
+    rowidx[tid] = src;
+    row_e[tid] = a.aexp[src];
+  }
+  __syncthreads();
+
+  const int ft0 = wave >> 2, frow = 16 * (wave & 3) + l16;
+  // Weight-row shifts: the lane's row of fragment f is row 64 * (4nt + ft0 + 2f) + frow.
+  int emax[2], fx[2];
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    emax[f] = a.rowexp[(size_t)e * a.N_total + 64 * (4 * nt + ft0 + 2 * f) + frow];
+    fx[f] = emax[f] - 141;
+  }
+  // Activation copies as in gemm_tile: copy q = wave + 8i fills LDS rows 4q..4q+3, lane L
+  // brings row 4q + L/16 into position L%16, chunk tau((L%16) ^ (row%16)).
+  const uint8_t* xg[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = wave + 8 * i, r = 4 * q + (lane >> 4);
+    const int pc = (lane & 15) ^ (r & 15), c = ((pc & 3) << 2) | (pc >> 2);
+    xg[i] = reinterpret_cast<const uint8_t*>(a.src + (size_t)rowidx[r] * a.K) + 16 * c;
+  }
+  // Weights: copy v = wave + 8i (v < 36) is 1 KB piece v%9 of tile v/9 (band 4nt + v/9).
+  const int n_wcopy = wave < 4 ? 5 : 4;
+  auto issue_to = [&](int kt, int slot) {
+    const uint32_t sb = lds0 + (uint32_t)(slot * kB16Stage);
+#pragma unroll
+    for (int i = 0; i < MF / 2; ++i) dma16(xg[i] + (size_t)kt * 256, sb + 1024u * (uint32_t)(wave + 8 * i));
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+      if (i < n_wcopy) {
+        const int v = wave + 8 * i, t = v / 9, p = v % 9;
+        dma16(W + ((size_t)(4 * nt + t) * nkt + kt) * kB16TileBytes + 1024 * p + 16 * lane,
+              sb + (uint32_t)(kXBytes + t * kB16TileBytes + 1024 * p));
+      }
+    }
+  };
+
+  f32x4_t acc[MF][2];
+#pragma unroll
+  for (int m = 0; m < MF; ++m) {
+    acc[m][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    acc[m][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  const uint32_t xrow = (uint32_t)l16 * 256u;
+  const f16x2_t k1152 = {(_Float16)1152.0f, (_Float16)1152.0f};
+  const uint32_t wrow0 = (uint32_t)(ft0 * kB16TileBytes + frow * 16);
+
+  issue_to(0, 0);
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int slot = kt & 1;
+    // Step kt's copies have landed in every wave, and every wave is past step kt-1,
+    // whose slot takes step kt+1's copies.
+    ring_wait(0);
+    if (kt + 1 < nkt) issue_to(kt + 1, slot ^ 1);
+    const uint8_t* ws = lds + slot * kB16Stage + kXBytes + wrow0;
+    uint32_t ew[2];
+#pragma unroll
+    for (int f = 0; f < 2; ++f) ew[f] = *reinterpret_cast<const uint32_t*>(ws + 2 * f * kB16TileBytes + kB16MantBytes + 4 * lq);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // A: chunk 4lq + j of row 16m + l16 (the swizzled position, as in gemm_tile).
+      const uint32_t xc = 16u * (uint32_t)((4 * j + lq) ^ l16);
+      const uint8_t* pa = lds + slot * kB16Stage + (xrow + xc);
+      uint4 av[MF];
+#pragma unroll
+      for (int m = 0; m < MF; ++m) av[m] = *reinterpret_cast<const uint4*>(pa + m * 4096);
+      uint4 b[2];
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        // Columns 32lq + 8j .. +7: mantissa chunk 2lq + j/2, bytes 8(j%2)..; exponent byte j.
+        const uint2 mv = *reinterpret_cast<const uint2*>(ws + 2 * f * kB16TileBytes + 1024 * (2 * lq + (j >> 1)) + 8 * (j & 1));
+        const int ex = (int)((ew[f] >> (8 * j)) & 0xffu);
+        // Blocks of the padding columns (past I; their h columns are zero) may carry
+        // exponents above emax: capped, their B stays finite, so 0 * B adds nothing.
+        const int pw = min(max(ex, 7) - emax[f] + 8, 8);
+        const uint32_t hb = pw >= -14 ? (uint32_t)(pw + 15) << 10 : (pw >= -24 ? 1u << (pw + 24) : 0u);
+        const f16x2_t sc = __builtin_bit_cast(f16x2_t, hb | (hb << 16));
+        const uint32_t u0 = mv.x ^ 0x80808080u, u1 = mv.y ^ 0x80808080u;
+        const f16x2_t h0 = (__builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, u0, 0x04010400u)) - k1152) * sc;
+        const f16x2_t h1 = (__builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, u0, 0x04030402u)) - k1152) * sc;
+        const f16x2_t h2 = (__builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, u1, 0x04010400u)) - k1152) * sc;
+        const f16x2_t h3 = (__builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, u1, 0x04030402u)) - k1152) * sc;
+        b[f] = make_uint4(__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1),
+                          __builtin_bit_cast(uint32_t, h2), __builtin_bit_cast(uint32_t, h3));
+      }
+#pragma unroll
+      for (int f = 0; f < 2; ++f)
+#pragma unroll
+        for (int m = 0; m < MF; ++m) acc[m][f] = mfma16h(av[m], b[f], acc[m][f]);
+    }
+  }
+  // acc is in units of 2^-(row exponent + fx).
+#pragma unroll
+  for (int m = 0; m < MF; ++m) {
+    const uint32_t e4 = *reinterpret_cast<const uint32_t*>(row_e + 16 * m + 4 * lq);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int er = (int)(int8_t)(e4 >> (8 * i));
+#pragma unroll
+      for (int f = 0; f < 2; ++f) acc[m][f][i] = __builtin_amdgcn_ldexpf(acc[m][f][i], er + fx[f]);
+    }
+  }
+  // Every wave is past its last ring read: slot 0 becomes the output staging.
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  uint16_t* stage0 = reinterpret_cast<uint16_t*>(lds);
+#pragma unroll
+  for (int m = 0; m < MF; ++m)
+#pragma unroll
+    for (int f = 0; f < 2; ++f)
+#pragma unroll
+      for (int i = 0; i < 4; i += 2) {
+        const int r = 16 * m + 4 * lq + i;
+        uint16_t* st = stage0 + f * (kStageBytes / 2);
+        const uint32_t p2 = cvt_bf16x2(acc[m][f][i], acc[m][f][i + 1]);
+        st[r * kOutStride + 16 * wave + l16] = (uint16_t)(p2 & 0xffffu);
+        st[(r + 1) * kOutStride + 16 * wave + l16] = (uint16_t)(p2 >> 16);
+      }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int cid = tid + 512 * q, r = cid >> 5, c = cid & 31;
+    const uint16_t* st = stage0 + (c >> 4) * (kStageBytes / 2);
+    if (r < nrows)
+      *reinterpret_cast<uint4*>(a.out + (size_t)(row0 + r) * a.out_ld + 256 * nt + 8 * c) =
+          *reinterpret_cast<const uint4*>(st + r * kOutStride + 8 * (c & 15));
+  }
+}
+
 // Grid: per class in kMask (bit c: class c), 8 x ceil(n_tiles * tiles / 8) workgroups;
 // 512 threads.  Class c's tile count sits in ntiles[c], its tiles at tiles + c * cap.
 // All three classes share one launch (kMask = 7): separate launches leave the chip
 // idle in each launch's tail, which costs a mid-size prefill (445 tokens) ~20 %.
-template <int kMask>
+template <int kMask, bool kB16>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void grouped_gemm_kernel(GemmArgs a, int cap) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kGemmLds];
   __shared__ int rowidx[kBM];
@@ -955,14 +1143,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   if (lid >= n) return;
   const int mt = lid / a.n_tiles, nt = lid % a.n_tiles;
   const uint32_t* tl = a.tiles + (size_t)c * cap;
-  if constexpr ((kMask & 4) != 0) {
-    if (c == 2) gemm_tile<class_fragments(2)>(a, tl, mt, nt, lds, rowidx, row_e);
-  }
-  if constexpr ((kMask & 3) != 0) {
-    if (c == 1)
-      gemm_tile<class_fragments(1)>(a, tl, mt, nt, lds, rowidx, row_e);
-    else if (c == 0)
-      gemm_tile<class_fragments(0)>(a, tl, mt, nt, lds, rowidx, row_e);
+  if constexpr (kB16) {
+    if (c == 2) gemm_tile_b16<class_fragments(2)>(a, tl, mt, nt, lds, rowidx, row_e);
+    else if (c == 1) gemm_tile_b16<class_fragments(1)>(a, tl, mt, nt, lds, rowidx, row_e);
+    else gemm_tile_b16<class_fragments(0)>(a, tl, mt, nt, lds, rowidx, row_e);
+  } else {
+    if constexpr ((kMask & 4) != 0) {
+      if (c == 2) gemm_tile<class_fragments(2)>(a, tl, mt, nt, lds, rowidx, row_e);
+    }
+    if constexpr ((kMask & 3) != 0) {
+      if (c == 1)
+        gemm_tile<class_fragments(1)>(a, tl, mt, nt, lds, rowidx, row_e);
+      else if (c == 0)
+        gemm_tile<class_fragments(0)>(a, tl, mt, nt, lds, rowidx, row_e);
+    }
   }
 }
 
@@ -1042,60 +1236,59 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   }
 }
 
-// Zero h[:, I:Ipad], the group sums of those columns and the exponents of the 128-unit
-// chunks that no gate/up tile writes (thread per row).
-__global__ void zero_pad_cols_kernel(uint16_t* __restrict__ h, uint16_t* __restrict__ hsum, int8_t* __restrict__ hexp,
-                                     int rows, int I, int Ipad) {
-  const int r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= rows) return;
-  for (int c = I; c < Ipad; ++c) h[(size_t)r * Ipad + c] = 0;
-  // Groups entirely past I (and the planes' padding); a group straddling I gets its sum
-  // from the GEMM epilogue only when I is a multiple of 32 (guaranteed: I % 64 == 0).
+// One wave per row: the h columns past I are zeroed, with the group sums of the groups
+// past I (and the planes' padding) and the chunk exponents past the last live chunk.
+__global__ __launch_bounds__(256) void zero_pad_cols_kernel(uint16_t* __restrict__ h, uint16_t* __restrict__ hsum,
+                                                            int8_t* __restrict__ hexp, int rows, int I, int Ipad) {
+  const size_t r = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (r >= (size_t)rows) return;
+  // I % 64 == 0: 4-column pieces of 8 bytes stay aligned.
+  for (int c = I + 4 * lane; c < Ipad; c += 256) *reinterpret_cast<uint64_t*>(h + r * Ipad + c) = 0ull;
+  // Groups entirely past I; a group straddling I gets its sum from the GEMM epilogue only
+  // when I is a multiple of 32 (guaranteed: I % 64 == 0).
   const int Gp = sum_planes_gp(Ipad / 32);
-  uint16_t* d = hsum + (size_t)r * 3 * Gp;
-  for (int g = I / 32; g < Gp; ++g) d[g] = d[Gp + g] = d[2 * Gp + g] = 0;
+  uint16_t* d = hsum + r * 3 * Gp;
+  for (int g = I / 32 + lane; g < Gp; g += 64) d[g] = d[Gp + g] = d[2 * Gp + g] = 0;
   const int es = exp_stride(Ipad);
-  for (int c = (I + 127) / 128; c < es; ++c) hexp[(size_t)r * es + c] = 0;
+  for (int c = (I + 127) / 128 + lane; c < es; c += 64) hexp[r * es + c] = 0;
 }
 
-// h[shared_base + t] = RTNE(act(shared_gu[t])) (padded to Ipad) as the fp16 operand of
-// the down GEMM, with its group sums and chunk exponents.  Thread per (row, 128-unit
-// chunk): the bf16 values are written first, then rewritten scaled by the chunk's
-// exponent (f16_exp_chunk).  Ipad is a multiple of 256, so no planar padding groups.
-__global__ void shared_act_kernel(const uint16_t* __restrict__ gu, int T, int I, int Ipad, int act, float gb, float vb,
-                                  uint16_t* __restrict__ h, uint16_t* __restrict__ hsum, int8_t* __restrict__ hexp) {
+// h rows of the shared expert from a given shared_gu [T, 2I] (gate then up):
+// RTNE(act(g, u)) as the gate/up epilogue writes them (fp16 operand with one exponent
+// per 128-unit chunk, planar group sums, zero past I).  One wave per (token, chunk):
+// lane L takes columns 2L, 2L+1 of the chunk; a group's 32 columns are 16 lanes, summed
+// by shuffles.
+__global__ __launch_bounds__(256) void shared_act_kernel(const uint16_t* __restrict__ gu, int T, int I, int Ipad,
+                                                         int act, float gb, float vb, uint16_t* __restrict__ h,
+                                                         uint16_t* __restrict__ hsum, int8_t* __restrict__ hexp) {
   const int nch = Ipad / 128, Gp = sum_planes_gp(Ipad / 32), es = exp_stride(Ipad);
-  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (size_t)T * nch) return;
-  const int t = (int)(idx / nch), ch = (int)(idx % nch);
-  uint16_t* hr = h + (size_t)t * Ipad + 128 * ch;
-  float mx = 0.f;
-  for (int q = 0; q < 4; ++q) {
-    float s = 0.f;
-    for (int c = 0; c < 32; ++c) {
-      const int col = 128 * ch + 32 * q + c;
-      uint16_t v = 0;
-      if (col < I) {
-        const float gg = bf16_to_f32(gu[(size_t)t * 2 * I + col]);
-        const float uu = bf16_to_f32(gu[(size_t)t * 2 * I + I + col]);
-        v = (uint16_t)f32_to_bf16(act_apply(act, gg, uu, gb, vb));
-      }
-      hr[32 * q + c] = v;
-      s += bf16_to_f32(v);
-      mx = fmaxf(mx, fabsf(bf16_to_f32(v)));
-    }
-    store_split3_planar(hsum + (size_t)t * 3 * Gp + 4 * ch + q, Gp, s);
+  const size_t wid = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (wid >= (size_t)T * nch) return;
+  const int t = (int)(wid / nch), ch = (int)(wid % nch);
+  const int col = 128 * ch + 2 * lane;
+  uint32_t hv = 0u;
+  if (col < I) {  // I even: col and col + 1 are both live or both past I
+    const uint32_t g2 = *reinterpret_cast<const uint32_t*>(gu + (size_t)t * 2 * I + col);
+    const uint32_t u2 = *reinterpret_cast<const uint32_t*>(gu + (size_t)t * 2 * I + I + col);
+    const uint32_t o0 = f32_to_bf16(act_apply(act, bf16_to_f32(g2 & 0xffffu), bf16_to_f32(u2 & 0xffffu), gb, vb));
+    const uint32_t o1 = f32_to_bf16(act_apply(act, bf16_to_f32(g2 >> 16), bf16_to_f32(u2 >> 16), gb, vb));
+    hv = o0 | (o1 << 16);
   }
+  const float v0 = bf16_to_f32(hv & 0xffffu), v1 = bf16_to_f32(hv >> 16);
+  float sv = v0 + v1;
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) sv += __shfl_xor(sv, off, 64);
+  float mx = fmaxf(fabsf(v0), fabsf(v1));
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
   const int ex = f16_exp_chunk(mx);
-  for (int c = 0; c < 128; c += 2) {
-    const uint32_t w = (uint32_t)hr[c] | ((uint32_t)hr[c + 1] << 16);
-    const uint32_t o = bf16x2_to_f16x2(w, ex);
-    hr[c] = (uint16_t)(o & 0xffffu);
-    hr[c + 1] = (uint16_t)(o >> 16);
-  }
-  hexp[(size_t)t * es + ch] = (int8_t)ex;
+  *reinterpret_cast<uint32_t*>(h + (size_t)t * Ipad + col) = bf16x2_to_f16x2(hv, ex);
+  if ((lane & 15) == 0) store_split3_planar(hsum + (size_t)t * 3 * Gp + 4 * ch + (lane >> 4), Gp, sv);
+  if (lane == 0) hexp[(size_t)t * es + ch] = (int8_t)ex;
   if (ch == 0)
-    for (int c = nch; c < es; ++c) hexp[(size_t)t * es + c] = 0;
+    for (int c = nch + lane; c < es; c += 64) hexp[(size_t)t * es + c] = 0;
 }
 
 // One exponent per h row for the down GEMM: the row's chunks (128 units, one exponent
@@ -1161,12 +1354,16 @@ hipError_t launch_topk(const float* logits, int T, int E, int k, int score, cons
 // The grouped GEMM over the tiles of all three classes in one launch; the grid is sized
 // for the worst case (a class-0/1 tile is a group's last, so at most one per group),
 // 8 x ceil(tiles / 8) workgroups per class (the XCD mapping deals each class in eighths).
-static hipError_t launch_grouped(GemmArgs a, uint32_t* tiles, int* ntiles, int cap, int n_routed, hipStream_t st) {
+static hipError_t launch_grouped(GemmArgs a, uint32_t* tiles, int* ntiles, int cap, int n_routed, hipStream_t st,
+                                 bool b16 = false) {
   a.tiles = tiles;
   a.ntiles = ntiles;
   const int small = min(cap, n_routed + 1);
   const int blocks = 8 * ((a.n_tiles * cap + 7) / 8 + 2 * ((a.n_tiles * small + 7) / 8));
-  hipLaunchKernelGGL(grouped_gemm_kernel<7>, dim3(blocks), dim3(512), 0, st, a, cap);
+  if (b16)
+    hipLaunchKernelGGL((grouped_gemm_kernel<7, true>), dim3(blocks), dim3(512), 0, st, a, cap);
+  else
+    hipLaunchKernelGGL((grouped_gemm_kernel<7, false>), dim3(blocks), dim3(512), 0, st, a, cap);
   return hipGetLastError();
 }
 
@@ -1191,6 +1388,9 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   const int k = L.top_k, E = L.n_routed;
   const size_t A = (size_t)T * k, R = A + T;
   if (L.n_shared < 1 || prefill_scratch_bytes(L, T) > scratch_bytes) return hipErrorInvalidValue;
+  // A weights-d layer's gate/up bundle holds the routed experts only: the shared
+  // expert's gate/up comes from the caller.
+  if (L.d_layout && !shared_gu) return hipErrorInvalidValue;
   if (L.H % 128 || L.H > 64 * kPrepMaxChunks * 8 || L.Ipad % 256) return hipErrorInvalidValue;
   if (A > s.order_elems || (size_t)((A + 1023) / 1024) * E > s.chunk_elems) return hipErrorInvalidValue;
   uint8_t* p = scratch;
@@ -1230,7 +1430,7 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   if (L.Ipad > L.I) {
     // h columns past I (their group sums and chunk exponents) feed the zero-padded down
     // columns.
-    hipLaunchKernelGGL(zero_pad_cols_kernel, dim3((unsigned)((R + 255) / 256)), dim3(256), 0, st, h, hsum, hexp,
+    hipLaunchKernelGGL(zero_pad_cols_kernel, dim3((unsigned)((R + 3) / 4)), dim3(256), 0, st, h, hsum, hexp,
                        (int)R, L.I, L.Ipad);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
@@ -1264,8 +1464,8 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(512), 0, st, s.offsets, E, g.shared_rows, tiles, ntiles, tile_cap);
   if ((err = hipGetLastError()) != hipSuccess) return err;
   if (shared_gu) {
-    const size_t n = (size_t)T * (L.Ipad / 128);
-    hipLaunchKernelGGL(shared_act_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, shared_gu, T, L.I,
+    const size_t n = (size_t)T * (L.Ipad / 128);  // waves, 4 per block
+    hipLaunchKernelGGL(shared_act_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, shared_gu, T, L.I,
                        L.Ipad, act, gb, vb, h + A * L.Ipad, hsum + A * 3 * Gph, hexp + A * exp_stride(L.Ipad));
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
@@ -1293,7 +1493,8 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   d.out_ld = L.H;
   d.out_ssum = nullptr;
   d.out_exp = nullptr;
-  if ((err = launch_grouped(d, tiles, ntiles, tile_cap, E, st)) != hipSuccess) return err;
+  d.rowexp = L.dn_rowexp;
+  if ((err = launch_grouped(d, tiles, ntiles, tile_cap, E, st, L.dn_fmt == RMOE_FMT_BFP16)) != hipSuccess) return err;
   hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, st, D, L.H, ids, wts, s.inv, k, (int)A,
                      residual ? x : nullptr, out, routed, shared_down, 1);
   return hipGetLastError();

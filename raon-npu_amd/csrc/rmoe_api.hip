@@ -78,9 +78,6 @@ int io_area(rmoe_ctx* ctx, size_t bytes, uint8_t** out) {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Tokens per launch of a weights-d layer's grouped path (bounds its decode scratch).
-constexpr int kDChunk = 1024;
-
 int check_layer(rmoe_ctx* ctx, int layer, RmoeLayer** out) {
   if (!ctx) return fail(RMOE_EINVAL, "null context");
   auto it = ctx->layers.find(layer);
@@ -110,15 +107,12 @@ int reserve_layer(rmoe_ctx* ctx, const RmoeLayer& L, int T, int k) {
   linear_needs(2 * L.I, L.H, T, f1, c1);
   linear_needs(L.H, L.Ipad, T, f2, c2);
   Lk.n_shared = 1;
-  // A weights-d layer's grouped path runs the decode kernels over up to kDChunk tokens per
-  // launch: one copy of the decode scratch per token of a chunk.
-  const size_t dtok = L.d_layout ? (size_t)std::min(T, kDChunk) : 1;
-  const size_t floats = std::max({rmoe::decode_scratch_floats(Lk) * dtok, f1, f2});
-  const size_t counters = std::max({rmoe::decode_scratch_counters(Lk) * dtok, c1, c2, (size_t)T});
+  const size_t floats = std::max({rmoe::decode_scratch_floats(Lk), f1, f2});
+  const size_t counters = std::max({rmoe::decode_scratch_counters(Lk), c1, c2, (size_t)T});
   TRY(grow(s.part, s.part_floats, floats, ctx));
   TRY(grow(s.counters, s.n_counters, counters, ctx));
-  TRY(grow(s.h, s.h_elems, (size_t)(kk + 1) * L.Ipad * dtok, ctx));
-  TRY(grow(s.dout, s.dout_elems, (size_t)(kk + 1) * L.H * dtok, ctx));
+  TRY(grow(s.h, s.h_elems, (size_t)(kk + 1) * L.Ipad, ctx));
+  TRY(grow(s.dout, s.dout_elems, (size_t)(kk + 1) * L.H, ctx));
   size_t re = s.route_elems;
   TRY(grow(s.ids, re, (size_t)T * kk, ctx));
   re = s.route_elems;
@@ -133,7 +127,7 @@ int reserve_layer(rmoe_ctx* ctx, const RmoeLayer& L, int T, int k) {
   TRY(grow(s.inv, oe, (size_t)T * kk, ctx));
   s.order_elems = oe;
   TRY(grow(s.offsets, s.offset_elems, 257, ctx));
-  if (L.n_shared > 0 && !L.d_layout) TRY(grow(s.pf, s.pf_bytes, rmoe::prefill_scratch_bytes(Lk, T), ctx));
+  if (L.n_shared > 0) TRY(grow(s.pf, s.pf_bytes, rmoe::prefill_scratch_bytes(Lk, T), ctx));
   if (L.n_shared > 0 && !L.d_layout) TRY(reserve_stack(ctx, L, 1));
   s.max_tokens = std::max(s.max_tokens, T);
   return RMOE_OK;
@@ -191,6 +185,14 @@ int place_layer(rmoe_ctx* ctx, int layer, RmoeLayer& L) {
   if (hipMalloc((void**)&L.dn, (size_t)L.dn_experts * L.dn_bytes) != hipSuccess) {
     hipFree(L.gu);
     return fail(RMOE_ENOMEM, "hipMalloc of expert down failed");
+  }
+  if (L.dn_fmt == RMOE_FMT_BFP16 &&
+      (hipMalloc((void**)&L.dn_rowexp, (size_t)L.dn_experts * L.H) != hipSuccess ||
+       hipMemset(L.dn_rowexp, 7, (size_t)L.dn_experts * L.H) != hipSuccess)) {
+    hipFree(L.gu);
+    hipFree(L.dn);
+    hipFree(L.dn_rowexp);
+    return fail(RMOE_ENOMEM, "hipMalloc of the down row exponents failed");
   }
   ctx->layers[layer] = L;
   return reserve_layer(ctx, L, 1, L.top_k);
@@ -310,6 +312,7 @@ int rmoe_destroy(rmoe_ctx* ctx) {
   for (auto& kv : ctx->layers) {
     hipFree(kv.second.gu);
     hipFree(kv.second.dn);
+    hipFree(kv.second.dn_rowexp);
     hipFree(kv.second.router_w);
     hipFree(kv.second.router_bias);
   }
@@ -615,8 +618,10 @@ int rmoe_layer_upload_d(rmoe_ctx* ctx, int layer, int bundle, int expert0, int n
                            ctx->stream));
     if (b1)
       HIP_TRY(rmoe::launch_relayout_in(ctx->s.staging, base + e * per, 2 * L->I, L->H, ctx->stream));
-    else
+    else {
       HIP_TRY(rmoe::launch_b16_relayout_in(ctx->s.staging, base + e * per, L->H, L->Ipad, ctx->stream));
+      HIP_TRY(rmoe::launch_b16_rowexp(base + e * per, L->H, L->Ipad, L->I, L->dn_rowexp + e * L->H, ctx->stream));
+    }
     // The staging buffer is reused by the next expert: wait for the re-layout.
     HIP_TRY(hipStreamSynchronize(ctx->stream));
   }
@@ -630,6 +635,7 @@ int rmoe_layer_free(rmoe_ctx* ctx, int layer) {
   hipStreamSynchronize(ctx->stream);
   hipFree(it->second.gu);
   hipFree(it->second.dn);
+  hipFree(it->second.dn_rowexp);
   hipFree(it->second.router_w);
   hipFree(it->second.router_bias);
   ctx->layers.erase(it);
@@ -1074,9 +1080,9 @@ int rmoe_moe_experts_grouped(rmoe_ctx* ctx, int layer, const uint16_t* x, int T,
   TRY(reserve_layer(ctx, *L, T, L->top_k));
   const int k = L->top_k;
   const size_t xb = align_up((size_t)T * L->H * 2, 256), ib = align_up((size_t)T * k * 4, 256),
-               gb = align_up((size_t)T * 2 * L->I * 2, 256), hb = align_up((size_t)T * L->Ipad * 2, 256);
+               gb = align_up((size_t)T * 2 * L->I * 2, 256);
   uint8_t* io;
-  TRY(io_area(ctx, 3 * xb + 2 * ib + gb + (L->d_layout ? hb : 0), &io));
+  TRY(io_area(ctx, 3 * xb + 2 * ib + gb, &io));
   uint16_t* xd = (uint16_t*)io;
   uint16_t* rd = (uint16_t*)(io + xb);
   uint16_t* sd = (uint16_t*)(io + 2 * xb);
@@ -1087,25 +1093,35 @@ int rmoe_moe_experts_grouped(rmoe_ctx* ctx, int layer, const uint16_t* x, int T,
   HIP_TRY(hipMemcpyAsync(idd, top_ids, (size_t)T * k * 4, hipMemcpyHostToDevice, ctx->stream));
   HIP_TRY(hipMemcpyAsync(wd, top_weights, (size_t)T * k * 4, hipMemcpyHostToDevice, ctx->stream));
   HIP_TRY(hipMemcpyAsync(gd, shared_gu, (size_t)T * 2 * L->I * 2, hipMemcpyHostToDevice, ctx->stream));
-  if (L->d_layout) {
-    // Weights-d layer: the routed experts of all T tokens run through the decode kernels
-    // (q4nx gate/up, bfp16 down, ordered combine per token) in one launch each; the
-    // shared down is the bfp16 GEMV of moe_b2's last expert over RTNE(act(shared_gu)).
-    uint16_t* hd = (uint16_t*)(io + 3 * xb + 2 * ib + gb);
-    for (int t0 = 0; t0 < T; t0 += kDChunk)
-      HIP_TRY(rmoe::launch_moe_decode(*L, xd + (size_t)t0 * L->H, idd + (size_t)t0 * k, wd + (size_t)t0 * k, k, false,
-                                      act, gate_beta, value_beta, false, nullptr, rd + (size_t)t0 * L->H, ctx->s,
-                                      ctx->stream, 3, std::min(kDChunk, T - t0)));
-    HIP_TRY(rmoe::launch_act_rows(gd, T, L->I, L->Ipad, act, gate_beta, value_beta, hd, ctx->stream));
-    HIP_TRY(rmoe::launch_linear_bfp16(L->dn + (size_t)L->n_routed * L->dn_bytes, L->H, L->Ipad, hd, T, sd, ctx->s,
-                                      ctx->stream));
-  } else {
-    HIP_TRY(rmoe::launch_moe_prefill(*L, xd, T, idd, wd, nullptr, nullptr, gd, act, gate_beta, value_beta, false,
-                                     nullptr, rd, sd, ctx->s.pf, ctx->s.pf_bytes, ctx->s, ctx->stream));
-  }
+  // The grouped MFMA path for both layouts: a weights-d layer runs its q4nx moe_b1 through
+  // the gate/up GEMM and its bfp16 moe_b2 (routed experts and the shared expert, its last)
+  // through the bfp16 down GEMM.
+  HIP_TRY(rmoe::launch_moe_prefill(*L, xd, T, idd, wd, nullptr, nullptr, gd, act, gate_beta, value_beta, false,
+                                   nullptr, rd, sd, ctx->s.pf, ctx->s.pf_bytes, ctx->s, ctx->stream));
   HIP_TRY(hipMemcpyAsync(routed, rd, (size_t)T * L->H * 2, hipMemcpyDeviceToHost, ctx->stream));
   HIP_TRY(hipMemcpyAsync(shared_down, sd, (size_t)T * L->H * 2, hipMemcpyDeviceToHost, ctx->stream));
   return sync_and_check(ctx, ctx->stream);
+}
+
+int rmoe_moe_experts_grouped_dev(rmoe_ctx* ctx, int layer, const void* x_dev, int T, const void* top_ids_dev,
+                                 const void* top_weights_dev, const void* shared_gu_dev, int act, float gate_beta,
+                                 float value_beta, void* routed_dev, void* shared_down_dev, void* stream) {
+  RmoeLayer* L;
+  TRY(check_layer(ctx, layer, &L));
+  if (!x_dev || !top_ids_dev || !top_weights_dev || !shared_gu_dev || !routed_dev || !shared_down_dev)
+    return fail(RMOE_EINVAL, "null argument");
+  if (T < 1) return fail(RMOE_EINVAL, "T must be >= 1");
+  if (L->n_shared < 1) return fail(RMOE_EINVAL, "layer %d has no shared expert", layer);
+  if (act != RMOE_ACT_SITU && act != RMOE_ACT_SWIGLU) return fail(RMOE_EINVAL, "unknown activation %d", act);
+  if (T > ctx->s.max_tokens) return fail(RMOE_EINVAL, "T=%d exceeds the reserved %d tokens: call rmoe_reserve", T, ctx->s.max_tokens);
+  hipError_t e = rmoe::launch_moe_prefill(*L, (const uint16_t*)x_dev, T, (const int32_t*)top_ids_dev,
+                                          (const float*)top_weights_dev, nullptr, nullptr,
+                                          (const uint16_t*)shared_gu_dev, act, gate_beta, value_beta, false, nullptr,
+                                          (uint16_t*)routed_dev, (uint16_t*)shared_down_dev, ctx->s.pf, ctx->s.pf_bytes,
+                                          ctx->s, pick_stream(ctx, stream));
+  if (e == hipErrorInvalidValue) return fail(RMOE_EINVAL, "scratch too small for T=%d: call rmoe_reserve", T);
+  HIP_TRY(e);
+  return RMOE_OK;
 }
 
 int rmoe_moe_prefill_dev(rmoe_ctx* ctx, int layer, const void* x_dev, int T, void* out_dev, int residual, int act,

@@ -246,6 +246,9 @@ struct RmoeLayer {
   int dn_fmt = 0;                     // RMOE_FMT_Q4NX or RMOE_FMT_BFP16
   uint8_t* gu = nullptr;              // gu_experts experts, tile layout
   uint8_t* dn = nullptr;              // dn_experts experts, tile layout of dn_fmt
+  // bfp16 down only: per expert and row, the largest max(e, 7) over the blocks of the
+  // first I columns ([dn_experts][H]; filled on upload).
+  uint8_t* dn_rowexp = nullptr;
   uint16_t* router_w = nullptr;  // [n_routed, H] bf16
   float* router_bias = nullptr;  // [n_routed] or null
   bool has_router = false;
@@ -320,6 +323,7 @@ hipError_t launch_linear(const uint8_t* tiles, int M, int K, const uint16_t* x, 
 // (at most (K/128 + 3)/4, so the q4nx scratch sizing covers it).
 hipError_t launch_b16_relayout_in(const uint8_t* packed, uint8_t* tiles, int M, int K, hipStream_t st);
 hipError_t launch_b16_relayout_out(const uint8_t* tiles, uint8_t* packed, int M, int K, hipStream_t st);
+hipError_t launch_b16_rowexp(const uint8_t* tiles, int M, int K, int k_valid, uint8_t* rowexp, hipStream_t st);
 int bfp16_ksplit(int M, int K);
 hipError_t launch_linear_bfp16(const uint8_t* tiles, int M, int K, const uint16_t* x, int T, uint16_t* y,
                                RmoeScratch& s, hipStream_t st);

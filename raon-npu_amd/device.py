@@ -424,6 +424,23 @@ class MoeLayer:
              vb, ptr(routed), ptr(sdown))
         return routed, sdown
 
+    def moe_experts_grouped_dev(self, x_dev, ids_dev, wts_dev, shared_gu_dev, routed_dev, sdown_dev, gate_beta=4.0,
+                                value_beta=25.0, stream=None):
+        """moe_experts_grouped on device tensors: x int16 [T, H], ids int32 [T, k], wts
+        float32 [T, k], shared_gu int16 [T, 2I] -> routed, sdown int16 [T, H], queued on
+        `stream` (asynchronous; call reserve(T) first)."""
+        g = self.geom
+        T = int(x_dev.shape[0]) if hasattr(x_dev, "shape") else -1
+        _check_dev(x_dev, (T, g.hidden), "int16", "x")
+        _check_dev(ids_dev, (T, g.top_k), "int32", "ids")
+        _check_dev(wts_dev, (T, g.top_k), "float32", "wts")
+        _check_dev(shared_gu_dev, (T, 2 * g.inter), "int16", "shared_gu")
+        _check_dev(routed_dev, (T, g.hidden), "int16", "routed")
+        _check_dev(sdown_dev, (T, g.hidden), "int16", "shared_down")
+        act, gb, vb = act_code(gate_beta, value_beta)
+        call("rmoe_moe_experts_grouped_dev", self.ctx.handle, self.layer, ptr(x_dev), T, ptr(ids_dev), ptr(wts_dev),
+             ptr(shared_gu_dev), act, gb, vb, ptr(routed_dev), ptr(sdown_dev), _stream_ptr(stream))
+
     def moe_prefill_dev(self, x_dev, T: int, out_dev, residual: bool = False, gate_beta=None, value_beta=None,
                         ids_dev=None, wts_dev=None, stream=None):
         act, gb, vb = act_code(gate_beta, value_beta)

@@ -143,3 +143,46 @@ class LazyBank:
 
     def down_proj(self, e: int):
         return self.expert(e)[2]
+
+
+def check_grouped_dev(be, layer_id: int, x, top, wts, sgu, gate_beta=4.0, value_beta=25.0, replays: int = 3):
+    """moe_experts_grouped_dev (device operands, a caller's stream) equals the host entry
+    point moe_experts_grouped bit for bit (the same kernels), eagerly and on every replay of
+    a captured graph, with other eager work and output clearing between the replays."""
+    import torch
+
+    routed, sdown = be.moe_experts_grouped(layer_id, x, top, wts, sgu, gate_beta, value_beta)
+    lyr = be.layer(layer_id)
+    T, H = x.shape
+    lyr.reserve(T)
+    xd = torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).cuda()
+    idd = torch.from_numpy(np.ascontiguousarray(top, dtype=np.int32)).cuda()
+    wd = torch.from_numpy(np.ascontiguousarray(wts, dtype=np.float32)).cuda()
+    sd = torch.from_numpy(np.ascontiguousarray(sgu).view(np.int16)).cuda()
+    ro = torch.empty(T, H, dtype=torch.int16, device="cuda")
+    so = torch.empty(T, H, dtype=torch.int16, device="cuda")
+    st = torch.cuda.Stream()
+
+    def run():
+        lyr.moe_experts_grouped_dev(xd, idd, wd, sd, ro, so, gate_beta, value_beta, stream=st)
+
+    def check(label):
+        assert np.array_equal(ro.cpu().numpy().view(np.uint16), routed), label
+        assert np.array_equal(so.cpu().numpy().view(np.uint16), sdown), label
+
+    with torch.cuda.stream(st):
+        run()
+    torch.cuda.synchronize()
+    check("eager")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        run()
+    for rep in range(replays):
+        ro.zero_()
+        so.zero_()
+        be.moe_experts_grouped(layer_id, x[:2], top[:2], wts[:2], sgu[:2], gate_beta, value_beta)  # eager work
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        check(f"replay {rep}")
+    return routed, sdown

@@ -17,7 +17,7 @@ from oracle import moe as om
 from oracle.bf16 import bf16_to_f32, f32_to_bf16
 from oracle.q4nx import dequantize_simple, pack_gemv, quantize
 
-from moe_fixtures import check_bf16, compare_bf16, make_layer, random_tokens, routing_margin
+from moe_fixtures import check_bf16, check_grouped_dev, compare_bf16, make_layer, random_tokens, routing_margin
 
 pytestmark = pytest.mark.gpu
 
@@ -167,6 +167,8 @@ def test_moe_experts_grouped_matches_oracle(be, moe):
     one = be.moe_experts(3, xs[5], top[5], wts[5], 4.0, 25.0)
     err, rel, _ = compare_bf16(routed[5], one)
     assert err <= 1e-2 and rel <= 1e-3
+    # the device-resident form equals the host call, eagerly and under graph replay
+    check_grouped_dev(be, 3, xs, top, wts, sgu, 4.0, 25.0)
 
 
 def test_grouped_validation(be, moe):

@@ -20,7 +20,7 @@ from oracle import moe as om
 from oracle.bf16 import bf16_to_f32, f32_to_bf16
 from oracle.q4nx import pack_gemv, quantize
 
-from moe_fixtures import compare_bf16, random_tokens
+from moe_fixtures import check_grouped_dev, compare_bf16, random_tokens
 from weights_d_fixtures import manifest_entry, random_bfp16_bundle, random_q4nx_bundle, write_bundle, write_manifest
 
 pytestmark = pytest.mark.gpu
@@ -117,8 +117,11 @@ def test_d_layer_grouped(small_d):
         err, rel, same = compare_bf16(got, ref)
         print(f"d-layer grouped {what}: max-abs {err:.3e} rel-L2 {rel:.3e} identical {same:.4f}")
         assert err <= 1e-2 and rel <= 1e-3
-    # per-token decode of the same rows agrees bit for bit (same kernels)
-    assert np.array_equal(routed[3], be.moe_experts(970, x[3], ids[3], w[3]))
+    # The grouped MFMA path and the per-token decode kernels agree within the same bar.
+    err, rel, _ = compare_bf16(routed[3], be.moe_experts(970, x[3], ids[3], w[3]))
+    assert err <= 1e-2 and rel <= 1e-3
+    # the device-resident form equals the host call, eagerly and under graph replay
+    check_grouped_dev(be, 970, x, ids, w, sgu)
 
 
 def test_d_layer_rejects_what_it_cannot_serve(small_d, gpu_ctx):
@@ -185,6 +188,20 @@ def test_load_weights_d_real_shapes(gpu_ctx, tmp_path, small_d):
         sbe.moe_experts(970, random_tokens(1, sgeom.hidden, 50 + t)[0], np.arange(sgeom.top_k),
                         np.ones(sgeom.top_k, np.float32))
         assert np.array_equal(be.moe_experts(1, x[t], ids, w), got)
+    # The grouped MFMA path at the real shapes: I = 1088 leaves the last gate/up n-tile
+    # partial, and the bfp16 down K is padded to 1280 with non-zero padding weights.
+    # Routes are drawn from 12 experts so that the oracle dequantizes few of them.
+    T = 48
+    xg = random_tokens(T, 2560, 56)
+    gids = np.stack([rng.choice(12, 6, replace=False) for _ in range(T)]).astype(np.int64)
+    gw = rng.uniform(0.05, 0.4, (T, 6)).astype(np.float32)
+    gsgu = random_tokens(T, 2 * 1088, 57)
+    routed, sdown = be.moe_experts_grouped(1, xg, gids, gw, gsgu)
+    r_ref, s_ref = om.moe_experts_grouped_batched(bank, xg, gids, gw, gsgu, 128)
+    for got, ref, what in ((routed, r_ref, "routed"), (sdown, s_ref, "shared_down")):
+        err, rel, same = compare_bf16(got, ref)
+        print(f"weights-d L01 grouped T={T} {what}: max-abs {err:.3e} rel-L2 {rel:.3e} identical {same:.4f}")
+        assert err <= 1e-2 and rel <= 1e-3
     sg, su, sd = bank.expert(128)
     g = be.linear("model.layers.1.moe.shared_experts.gate_proj.weight", x[0])
     act = f32_to_bf16(om.situ_glu(g, be.linear("model.layers.1.moe.shared_experts.up_proj.weight", x[0])))
@@ -242,10 +259,10 @@ def test_moe_experts_dev_matches_host_and_replays(small_d):
         lyr.moe_experts_dev(xd[0], idd[0][:2].contiguous(), wd[0], od[0])
 
 
-def test_d_layer_grouped_across_launch_chunks(small_d):
-    """More tokens than one launch of the weights-d grouped path takes (1,024): rows on both
-    sides of the chunk boundary equal the one-token path bit for bit, and the whole call
-    matches the batched oracle."""
+def test_d_layer_grouped_many_tokens(small_d):
+    """1,100 tokens: groups of ~410 rows span full 128-row tiles and a partial one of each
+    tile class; the whole call matches the batched oracle, and sampled tokens match the
+    per-token decode kernels within the same bar."""
     be, lyr, geom, bank, _ = small_d
     T = 1100
     rng = np.random.default_rng(53)
@@ -254,10 +271,49 @@ def test_d_layer_grouped_across_launch_chunks(small_d):
     w = rng.uniform(0.1, 1.0, (T, geom.top_k)).astype(np.float32)
     sgu = random_tokens(T, 2 * geom.inter, 55)
     routed, sdown = be.moe_experts_grouped(970, x, ids, w, sgu)
-    for t in (0, 1023, 1024, 1099):
-        assert np.array_equal(routed[t], be.moe_experts(970, x[t], ids[t], w[t])), t
+    for t in (0, 517, 1099):
+        err, rel, _ = compare_bf16(routed[t], be.moe_experts(970, x[t], ids[t], w[t]))
+        assert err <= 1e-2 and rel <= 1e-3, t
     r_ref, s_ref = om.moe_experts_grouped_batched(bank, x, ids, w, sgu, geom.n_routed)
     for got, ref, what in ((routed, r_ref, "routed"), (sdown, s_ref, "shared_down")):
         err, rel, same = compare_bf16(got, ref)
         print(f"d-layer grouped T={T} {what}: max-abs {err:.3e} rel-L2 {rel:.3e} identical {same:.4f}")
         assert err <= 1e-2 and rel <= 1e-3
+
+
+def test_d_layer_grouped_ignores_down_padding(gpu_ctx):
+    """moe_b2's columns past I are padding whose bytes are not guaranteed: here they hold
+    values ~1e30 (block exponents far above the real ones).  The bfp16 down GEMM shifts
+    each weight row by the largest exponent of its real columns only, and the h columns
+    past I are zero, so the result equals the oracle, which reads columns < I."""
+    from raon_npu_amd.backend import GpuBackend
+
+    geom = G.MoeGeometry(hidden=512, inter=320, n_routed=8, n_shared=1, top_k=3)
+    rng = np.random.default_rng(61)
+    b1, _, sgu, router = _small_d_bundles(geom, 62)
+    b2 = []
+    for _ in range(geom.n_routed + 1):
+        d = np.empty((geom.hidden, geom.inter_pad), np.float32)
+        d[:, : geom.inter] = rng.normal(0, 0.02, (geom.hidden, geom.inter))
+        d[:, geom.inter:] = rng.normal(0, 1e30, (geom.hidden, geom.inter_pad - geom.inter))
+        b2.append(B.pack_gemv(d))
+    b2 = b"".join(b2)
+    be = GpuBackend(context=gpu_ctx)
+    lyr = be.register_moe_layer_d(971, geom, b1, b2, shared_gu=sgu, router_weight=router, score="sigmoid",
+                                  scaling=2.5)
+    try:
+        bank = om.DExpertBank(b1, b2, geom.n_routed, geom.hidden, geom.inter, shared_gu=sgu, cache=16)
+        T = 40
+        x = random_tokens(T, geom.hidden, 63)
+        ids = np.stack([rng.choice(geom.n_routed, geom.top_k, replace=False) for _ in range(T)]).astype(np.int64)
+        w = rng.uniform(0.1, 1.0, (T, geom.top_k)).astype(np.float32)
+        sgu_rows = random_tokens(T, 2 * geom.inter, 64)
+        routed, sdown = be.moe_experts_grouped(971, x, ids, w, sgu_rows)
+        r_ref, s_ref = om.moe_experts_grouped(bank, x, ids, w, sgu_rows, geom.n_routed)
+        for got, ref, what in ((routed, r_ref, "routed"), (sdown, s_ref, "shared_down")):
+            assert np.all(np.isfinite(bf16_to_f32(got))), what
+            err, rel, same = compare_bf16(got, ref)
+            print(f"d-layer grouped, garbage padding, {what}: max-abs {err:.3e} rel-L2 {rel:.3e} identical {same:.4f}")
+            assert err <= 1e-2 and rel <= 1e-3
+    finally:
+        lyr.free()
