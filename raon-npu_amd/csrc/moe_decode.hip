@@ -378,30 +378,6 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a0) {
   }
 }
 
-// One thread per element of h[T, Ipad].
-__global__ __launch_bounds__(256) void act_rows_kernel(const uint16_t* __restrict__ gu, int T, int I, int Ipad, int act,
-                                                       float gb, float vb, uint16_t* __restrict__ h) {
-  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (size_t)T * Ipad) return;
-  const int t = (int)(idx / Ipad), c = (int)(idx % Ipad);
-  uint32_t v = 0u;
-  if (c < I) {
-    const uint16_t* row = gu + (size_t)t * 2 * I;
-    v = f32_to_bf16(act_apply(act, bf16_to_f32(row[c]), bf16_to_f32(row[I + c]), gb, vb));
-  }
-  h[idx] = (uint16_t)v;
-}
-
-}  // namespace
-
-hipError_t launch_act_rows(const uint16_t* gu, int T, int I, int Ipad, int act, float gb, float vb, uint16_t* h,
-                           hipStream_t st) {
-  const size_t n = (size_t)T * Ipad;
-  hipLaunchKernelGGL(act_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gu, T, I, Ipad, act, gb,
-                     vb, h);
-  return hipGetLastError();
-}
-
 hipError_t launch_route(const RmoeLayer& L, const uint16_t* x, int T, int32_t* ids, float* wts, float* logits,
                         RmoeScratch& s, hipStream_t st) {
   if (L.n_routed > kMaxExperts || L.top_k > kMaxTopK || L.top_k > L.n_routed) return hipErrorInvalidValue;

@@ -341,9 +341,6 @@ hipError_t launch_moe_decode(const RmoeLayer& L, const uint16_t* x, const int32_
                              uint16_t* out_routed, RmoeScratch& s, hipStream_t st, int stages = 3, int ntok = 1);
 
 // h[T, Ipad] = RTNE(act(gu[t, :I], gu[t, I:2I])) with zero columns [I, Ipad).
-hipError_t launch_act_rows(const uint16_t* gu, int T, int I, int Ipad, int act, float gb, float vb, uint16_t* h,
-                           hipStream_t st);
-
 hipError_t launch_dispatch(const int32_t* ids, int T, int k, int n_experts, int32_t* order, int32_t* inv,
                            int32_t* offsets, RmoeScratch& s, hipStream_t st);
 
