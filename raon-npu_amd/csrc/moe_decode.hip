@@ -378,6 +378,8 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a0) {
   }
 }
 
+}  // namespace
+
 hipError_t launch_route(const RmoeLayer& L, const uint16_t* x, int T, int32_t* ids, float* wts, float* logits,
                         RmoeScratch& s, hipStream_t st) {
   if (L.n_routed > kMaxExperts || L.top_k > kMaxTopK || L.top_k > L.n_routed) return hipErrorInvalidValue;

@@ -48,6 +48,28 @@ constexpr int kMaxDnUnits = 2;    // DN units per workgroup and layer (prefetche
 constexpr int kLRow = 4096;       // floats of partial logits staged in LDS at a time
 constexpr unsigned kSpinLimit = 1u << 21;
 
+// Per-layer timeline of the stack, in the timeline build only (RMOE_DECODE_TIMELINE; see
+// raon-npu_amd/decode_timeline.py): one wave of each workgroup stores the device clock
+// (s_memrealtime, 100 MHz) at fixed points of every layer.  Other builds compile the
+// stamps to nothing.
+constexpr int kTimelineLayers = 48, kTimelineGroups = 256, kTimelineEvents = 16;
+#ifdef RMOE_DECODE_TIMELINE
+__device__ unsigned long long g_stack_timeline[kTimelineLayers][kTimelineGroups][kTimelineEvents];
+#define RMOE_STAMP(l, g, ev, who)                                                           \
+  do {                                                                                       \
+    if (threadIdx.x == (who) && (l) < kTimelineLayers && (g) < kTimelineGroups)              \
+      g_stack_timeline[l][g][ev] = __builtin_amdgcn_s_memrealtime();                         \
+  } while (0)
+#else
+#define RMOE_STAMP(l, g, ev, who) \
+  do {                            \
+  } while (0)
+#endif
+// Stamp points (event index): ready seen 0, x and partial logits summed 1, routing done 2,
+// gate/up unit done 3, h received 4, down tiles in LDS 5, wave 1's down dot products 6,
+// down partials summed 7, d stored 8, combiner holds every d 9, x band stored 10, ready
+// published 11.
+
 struct StackArgs {
   int L, H, I, Ipad, E, k, S, score, renorm, act, residual;
   float scaling, gb, vb;
@@ -588,6 +610,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     uint64_t* dtag = reinterpret_cast<uint64_t*>(lay + a.off_dout);  // [S][H] tagged d words
 
     if (!wait_geq(a, c_ready, (unsigned)a.nb2, &flag)) return;
+    RMOE_STAMP(l, g, 0, 0);
 
     // ---- x_l and the routing of this layer.  Every device-scope load of a thread is
     // issued before the first use, so the latencies overlap.
@@ -651,8 +674,10 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
       if (pe < a.E && pp == 0) sl.lg[pe] = lacc;
     }
     __syncthreads();
+    RMOE_STAMP(l, g, 1, 0);
     const SelectParams sp{a.E, a.k, a.S, a.score, a.renorm, a.scaling};
     select_rank(sp, a.rb[l], sl);
+    RMOE_STAMP(l, g, 2, 0);
 
     // ---- issue every weight load of this workgroup's units for this layer.
     // A GU unit (slot s, half band hb) is the 32 gate rows 32hb.. and the 32 matching up
@@ -732,6 +757,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     };
     if (gu_d[0] >= 0) {
       gu_unit(gu_d[0], gu_d[1]);
+      RMOE_STAMP(l, g, 3, 0);
       issue_dn();
     }
     for (int u = g + G; u < a.n_gu; u += G) {
@@ -807,9 +833,11 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
         }
       }
       if (__syncthreads_or(failed ? 1 : 0)) return;
+      RMOE_STAMP(l, g, 4, 0);
       // This wave's DN tiles were copied into LDS by its own loads: drain them.
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
+      RMOE_STAMP(l, g, 5, 0);
       float acc[kMaxDnUnits] = {0.f, 0.f};
       if (wave > 0) {
 #pragma unroll
@@ -822,9 +850,11 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
           }
         }
       }
+      RMOE_STAMP(l, g, 6, 64);
       red[wave][0][lane] = acc[0];
       red[wave][1][lane] = acc[1];
       __syncthreads();
+      RMOE_STAMP(l, g, 7, 0);
       // The combiner of band b is the workgroup whose first DN unit is (slot 0, band b):
       // slot 0's units are units 0..nb2-1, and unit v is the first unit of workgroup
       // (n_gu + v) mod G, so every band has exactly one.
@@ -848,6 +878,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
                      (uint64_t)__float_as_uint(bf16_round(dd)) | ((uint64_t)tag << 32));
         }
       }
+      RMOE_STAMP(l, g, 8, 0);
       if (comb) {
         const int row = 64 * cb + lane;
         bool cfailed = false;
@@ -890,6 +921,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
           }
         }
         if (__syncthreads_or(cfailed ? 1 : 0)) return;
+        RMOE_STAMP(l, g, 9, 0);
         if (wave == 0) {
           // Ascending expert id: the slot order, then each slot's value and weight, read
           // from LDS in batches, then summed in order.
@@ -928,9 +960,11 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
           __syncthreads();
           float* lnext = reinterpret_cast<float*>(lay + a.layer_bytes + a.off_lpart);
           uint4 rwv[NIT][2];
+          RMOE_STAMP(l, g, 10, 0);
           read_router_slice<NIT>(a, rw_lds, rwv);
           band_logits<NIT>(a, xband, rwv, lnext, cb);
           block_publish_ready(a, l + 1);
+          RMOE_STAMP(l, g, 11, 0);
         }
       }
       if (wave > 0) __builtin_amdgcn_s_waitcnt(0);  // router slice copies have landed
@@ -990,6 +1024,14 @@ StackShape stack_shape(const RmoeLayer& L) {
 }
 
 }  // namespace
+
+#ifdef RMOE_DECODE_TIMELINE
+extern "C" int rmoe_debug_stack_timeline(unsigned long long* host, size_t n) {
+  if (n != sizeof(g_stack_timeline) / sizeof(unsigned long long)) return -1;
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_stack_timeline), sizeof(g_stack_timeline), 0,
+                                  hipMemcpyDeviceToHost);
+}
+#endif
 
 size_t stack_scratch_bytes(const RmoeLayer& L, int n_layers) {
   const StackShape sh = stack_shape(L);
