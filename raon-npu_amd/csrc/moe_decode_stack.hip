@@ -45,7 +45,12 @@ constexpr int kMaxE = 256;
 constexpr int kMaxSlots = 17;
 constexpr int kMaxDnPos = 4;      // DN tiles per DN wave (waves 1..7, both units): Ipad <= 1792
 constexpr int kMaxDnUnits = 2;    // DN units per workgroup and layer (prefetched)
-constexpr int kLRow = 4096;       // floats of partial logits staged in LDS at a time
+constexpr int kLRow = 4096;       // floats of partial logits copied into LDS at a time
+// LDS rows of partial logits are Ep + kLPad floats apart: band b starts at bank 16 b mod 64,
+// so the four bands that one instruction reads (see the sum below) fall in four distinct
+// bank groups.
+constexpr int kLPad = 16;
+constexpr int kLRowLds = 4608;    // LDS floats for one pass (32 rows of 128 + 16)
 constexpr unsigned kSpinLimit = 1u << 21;
 
 // Per-layer timeline of the stack, in the timeline build only (RMOE_DECODE_TIMELINE; see
@@ -341,8 +346,9 @@ __device__ __forceinline__ bool select_fast(const SelectParams a, const float* b
   return a.score == 1 && bias == nullptr;
 }
 
+template <int NC>
 __device__ __forceinline__ void select_rank(const SelectParams a, const float* __restrict__ bias, SelectLds& sl) {
-  constexpr int NC = kMaxE / 64;
+  static_assert(NC >= 1 && NC <= kMaxE / 64, "64-expert chunks");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int E = a.E, K = a.k;
   const int nc = (E + 63) >> 6;     // 64-key chunks; keys in [E, 64*nc) are 0
@@ -413,14 +419,18 @@ __device__ __forceinline__ void select_rank(const SelectParams a, const float* _
         if (lane < 16 && i < E && cnt < K) sl.id[cnt] = i;
       }
     };
-    if (nc <= 2) rank_pass(std::integral_constant<int, 16>{});
-    else rank_pass(std::integral_constant<int, 32>{});
+    if constexpr (NC <= 2) {
+      rank_pass(std::integral_constant<int, 16>{});
+    } else {
+      if (nc <= 2) rank_pass(std::integral_constant<int, 16>{});
+      else rank_pass(std::integral_constant<int, 32>{});
+    }
   }
   __syncthreads();
 }
 
+template <int NC>
 __device__ __forceinline__ void select_finish(const SelectParams a, const float* __restrict__ bias, SelectLds& sl) {
-  constexpr int NC = kMaxE / 64;
   const int lane = threadIdx.x & 63;
   const int E = a.E, K = a.k;
   const int nc = (E + 63) >> 6;
@@ -545,7 +555,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
   __shared__ float hsum[kWaves][DNPOS][4];
   __shared__ float cmb[kMaxSlots][64];                         // d of every slot of a band
   __shared__ __attribute__((aligned(16))) uint32_t xband[32];  // x_{l+1} of a band, bf16 pairs
-  __shared__ __attribute__((aligned(16))) float lrow[kLRow];   // partial logits being summed
+  __shared__ __attribute__((aligned(16))) float lrow[kLRowLds];  // partial logits being summed
   __shared__ unsigned flag;
   // DN tiles of this workgroup's units: [kMaxDnUnits][nkt2] tiles, then a 1 KB sink.
   extern __shared__ __attribute__((aligned(16))) uint8_t dn_lds[];
@@ -646,26 +656,45 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
           if ((idx & 7) == 0 && 2 * idx < Hp) xsum[idx >> 3] = sv;
         }
       }
-      const int nbc = kLRow / a.Ep;  // bands per chunk
+      const int lstride = a.Ep + kLPad;
+      const int nbc = min(kLRow / a.Ep, kLRowLds / lstride);  // bands per pass
       // P threads per expert (neighbouring lanes) sum every P-th band; then a fixed tree.
       const int P = a.E <= 128 ? 4 : 2;
       const int pe = tid / P, pp = tid % P;
       float lacc = 0.f;
       for (int b0 = 0; b0 < a.nb2; b0 += nbc) {
-        const int nf4 = (min(nbc, a.nb2 - b0) * a.Ep) / 4;
+        const int nb = min(nbc, a.nb2 - b0);
+        const int nf4 = (nb * a.Ep) / 4, rq = a.Ep / 4;
         const uint4* src = reinterpret_cast<const uint4*>(lpart + (size_t)b0 * a.Ep);
-        uint4* dst = reinterpret_cast<uint4*>(lrow);
-        // Two 16-byte loads per thread (kLRow = 4096 floats), both issued before either store.
+        // Two 16-byte loads per thread (kLRow = 4096 floats), both issued before either
+        // store; piece j of row j / rq goes to the padded row.
         static_assert(kLRow / 4 == 2 * kThreads, "two 16-byte pieces per thread");
         const bool h0 = tid < nf4, h1 = tid + kThreads < nf4;
         const uint4 v0 = h0 ? src[tid] : make_uint4(0u, 0u, 0u, 0u);
         const uint4 v1 = h1 ? src[tid + kThreads] : make_uint4(0u, 0u, 0u, 0u);
-        if (h0) dst[tid] = v0;
-        if (h1) dst[tid + kThreads] = v1;
+        // Row of piece j by a float reciprocal, not an integer division: j < 1024 and
+        // rq >= 8, so (j + 0.5) / rq stays >= 1/16 away from an integer, far beyond the
+        // reciprocal's rounding.
+        const float rinv = 1.0f / (float)rq;
+        const int j1 = tid + kThreads;
+        const int r0 = (int)(((float)tid + 0.5f) * rinv), r1 = (int)(((float)j1 + 0.5f) * rinv);
+        if (h0) *reinterpret_cast<uint4*>(lrow + r0 * lstride + 4 * (tid - r0 * rq)) = v0;
+        if (h1) *reinterpret_cast<uint4*>(lrow + r1 * lstride + 4 * (j1 - r1 * rq)) = v1;
         __syncthreads();
         if (pe < a.E) {
-          const int nb = min(nbc, a.nb2 - b0);
-          for (int b = pp; b < nb; b += P) lacc += lrow[b * a.Ep + pe];
+          // Eight of the thread's bands are read at a time (one LDS round trip, not one
+          // per band), then added in band order.
+          for (int bb = pp; bb < nb; bb += 8 * P) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const int b = bb + P * i;
+              v[i] = b < nb ? lrow[b * lstride + pe] : 0.f;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              if (bb + P * i < nb) lacc += v[i];
+          }
         }
         __syncthreads();
       }
@@ -676,7 +705,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     __syncthreads();
     RMOE_STAMP(l, g, 1, 0);
     const SelectParams sp{a.E, a.k, a.S, a.score, a.renorm, a.scaling};
-    select_rank(sp, a.rb[l], sl);
+    select_rank<2 * NIT>(sp, a.rb[l], sl);  // E <= 128 * NIT: at most 2 * NIT chunks of 64
     RMOE_STAMP(l, g, 2, 0);
 
     // ---- issue every weight load of this workgroup's units for this layer.
@@ -718,7 +747,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     // ---- slot weights and id order (read by the combine, after later barriers), while
     // the weight loads are in flight.
     if (wave == 0) {
-      select_finish(sp, a.rb[l], sl);
+      select_finish<2 * NIT>(sp, a.rb[l], sl);
       if (g == 0 && tid < a.k) {
         if (a.ids_out) a.ids_out[(size_t)l * a.k + tid] = sl.id[tid];
         if (a.wts_out) a.wts_out[(size_t)l * a.k + tid] = sl.w[tid];
@@ -882,6 +911,20 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
       if (comb) {
         const int row = 64 * cb + lane;
         bool cfailed = false;
+        // The combine's operands known since the routing (the first 8 slots in ascending
+        // expert id with their weights, and x_l of the row for the residual), read before
+        // the wait so that they are not on the path after it.
+        int o8p[8];
+        float w8p[8];
+        uint32_t xres = 0u;
+        if (wave == 0) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            o8p[i] = i < a.k ? sl.ord[i] : 0;
+            w8p[i] = sl.w[o8p[i]];
+          }
+          xres = (xs[row >> 1] >> (16 * (row & 1))) & 0xffffu;
+        }
         if (wave == 0) {
           // d of every slot of the band into LDS: each lane polls its row's word of every
           // slot (up to 9 loads in flight) until all carry this launch's tag.  Bounded
@@ -930,11 +973,11 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
             int o8[8];
             float c8[8], w8[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) o8[i] = r0 + i < a.k ? sl.ord[r0 + i] : 0;
+            for (int i = 0; i < 8; ++i) o8[i] = r0 == 0 ? o8p[i] : (r0 + i < a.k ? sl.ord[r0 + i] : 0);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
               c8[i] = cmb[o8[i]][lane];
-              w8[i] = sl.w[o8[i]];
+              w8[i] = r0 == 0 ? w8p[i] : sl.w[o8[i]];
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i)
@@ -942,10 +985,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
           }
           uint32_t o = f32_to_bf16(acc2);
           if (a.S > a.k) o = f32_to_bf16(__fadd_rn(bf16_to_f32(o), cmb[a.k][lane]));
-          if (a.residual) {
-            const uint32_t xv = (xs[row >> 1] >> (16 * (row & 1))) & 0xffffu;
-            o = f32_to_bf16(__fadd_rn(bf16_to_f32(xv), bf16_to_f32(o)));
-          }
+          if (a.residual) o = f32_to_bf16(__fadd_rn(bf16_to_f32(xres), bf16_to_f32(o)));
           const uint32_t hi = __shfl_down(o, 1, 64);
           if ((lane & 1) == 0) xband[lane >> 1] = o | (hi << 16);
           if (l + 1 == a.L) {
