@@ -3,10 +3,11 @@
 // Produces the flattened job order of build_plan (kernels/moe_grouped/planner.py:76-108):
 // assignments (token, route) sorted by expert id ascending and, inside one expert,
 // in row-major (token, route) order.  Chunks of 1,024 assignments are counted in
-// parallel; one workgroup turns the per-chunk counts into per-chunk bases; each chunk
-// then places its assignments: its 4 waves take 256 consecutive assignments each, rank
-// lanes of equal expert with ballots (64 at a time, in order) and offset by the counts
-// of the waves before, so the sort is stable without atomics on the output.
+// parallel; then each chunk's workgroup derives its own bases (the expert offsets, an
+// exclusive scan of the per-expert totals, plus the counts of the chunks before it) and
+// places its assignments: its 4 waves take 256 consecutive assignments each, rank lanes
+// of equal expert with ballots (64 at a time, in order) and offset by the counts of the
+// waves before, so the sort is stable without atomics on the output.
 #include "rmoe_internal.h"
 
 namespace rmoe {
@@ -37,49 +38,35 @@ __global__ __launch_bounds__(256) void dispatch_count_kernel(const int32_t* __re
   if ((int)threadIdx.x < E) counts[(size_t)c * E + threadIdx.x] = hist[threadIdx.x];
 }
 
-// One workgroup of 1,024 threads: counts[c][e] -> bases[c][e] in place; offsets[e]
-// (E + 1 entries).  Thread (e, p) handles the p-th quarter of the chunks of expert e.
-__global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t* __restrict__ counts, int nchunks, int E,
-                                                            int32_t* __restrict__ offsets) {
-  __shared__ int part[4][256];
-  __shared__ int tot[256];
-  const int e = threadIdx.x & 255, p = threadIdx.x >> 8;
-  const int per = (nchunks + 3) / 4, c0 = min(nchunks, p * per), c1 = min(nchunks, c0 + per);
-  int sum = 0;
-  if (e < E)
-    for (int c = c0; c < c1; ++c) sum += counts[(size_t)c * E + e];
-  part[p][e] = sum;
-  __syncthreads();
-  if (p == 0) tot[e] = e < E ? part[0][e] + part[1][e] + part[2][e] + part[3][e] : 0;
-  __syncthreads();
-  for (int d = 1; d < 256; d <<= 1) {  // inclusive scan of tot (Hillis-Steele)
-    int v = 0;
-    if (p == 0 && e >= d) v = tot[e - d];
-    __syncthreads();
-    if (p == 0) tot[e] += v;
-    __syncthreads();
-  }
-  if (e < E) {
-    int run = (e ? tot[e - 1] : 0);
-    if (p == 0) {
-      offsets[e] = run;
-      if (e == E - 1) offsets[E] = tot[e];
-    }
-    for (int q = 0; q < p; ++q) run += part[q][e];
-    for (int c = c0; c < c1; ++c) {
-      const int v = counts[(size_t)c * E + e];
-      counts[(size_t)c * E + e] = run;
-      run += v;
-    }
-  }
-}
-
+// counts[c][e]: assignments of chunk c routed to expert e.  Workgroup c also writes
+// offsets[e] (E + 1 entries) when c == 0.
 __global__ __launch_bounds__(256) void dispatch_scatter_kernel(const int32_t* __restrict__ ids, int n, int E,
-                                                               const int32_t* __restrict__ bases,
+                                                               const int32_t* __restrict__ counts, int nchunks,
+                                                               int32_t* __restrict__ offsets,
                                                                int32_t* __restrict__ order, int32_t* __restrict__ inv) {
   __shared__ int slot[4][256];  // per wave: counts, then next output slot per expert
+  __shared__ int wsum[4];
   const int c = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   for (int i = tid; i < 4 * 256; i += 256) (&slot[0][0])[i] = 0;
+  // Thread e: expert e's assignments in the chunks before this one and in all chunks;
+  // the expert's offset is the exclusive scan of the totals (wave scans, then the four
+  // wave sums).
+  int before = 0, total = 0;
+  if (tid < E) {
+#pragma unroll 8
+    for (int q = 0; q < nchunks; ++q) {
+      const int v = counts[(size_t)q * E + tid];
+      before += q < c ? v : 0;
+      total += v;
+    }
+  }
+  int incl = total;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += y;
+  }
+  if (lane == 63) wsum[wave] = incl;
   const int begin = c * kChunk + 256 * wave;
   int ev[4];
   unsigned long long same[4];
@@ -105,9 +92,16 @@ __global__ __launch_bounds__(256) void dispatch_scatter_kernel(const int32_t* __
     if (ok && (m >> lane) == 1ull) slot[wave][e] += __popcll(m);
   }
   __syncthreads();
-  // Expert e's first slot for wave w: chunk base + counts of waves 0..w-1.
+  // Expert e's first slot for wave w: offset + earlier chunks + counts of waves 0..w-1.
   if (tid < E) {
-    int run = bases[(size_t)c * E + tid];
+    int woff = 0;
+    for (int w = 0; w < wave; ++w) woff += wsum[w];
+    const int offset = woff + incl - total;
+    if (c == 0) {
+      offsets[tid] = offset;
+      if (tid == E - 1) offsets[E] = offset + total;
+    }
+    int run = offset + before;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       const int v = slot[w][tid];
@@ -140,11 +134,8 @@ hipError_t launch_dispatch(const int32_t* ids, int T, int k, int n_experts, int3
   hipLaunchKernelGGL(dispatch_count_kernel, dim3(nchunks), dim3(256), 0, st, ids, n, n_experts, s.chunk_counts, s.err);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, st, s.chunk_counts, nchunks, n_experts, offsets);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nchunks), dim3(256), 0, st, ids, n, n_experts, s.chunk_counts, order,
-                     inv);
+  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nchunks), dim3(256), 0, st, ids, n, n_experts, s.chunk_counts,
+                     nchunks, offsets, order, inv);
   return hipGetLastError();
 }
 

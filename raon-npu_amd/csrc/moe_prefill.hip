@@ -314,11 +314,13 @@ constexpr int kTileClasses = 3;
 __host__ __device__ constexpr int class_fragments(int c) { return c == 0 ? 2 : c == 1 ? 4 : 8; }
 
 // One workgroup of 512 threads; thread e owns group e (routed 0..n_routed-1, shared n_routed).
+// The per-class tile bases are an exclusive prefix over the groups: a 64-lane scan per wave
+// (shuffles), then the wave totals.
 __global__ __launch_bounds__(512) void tile_table_kernel(const int32_t* __restrict__ offsets, int n_routed,
                                                          int shared_rows, uint32_t* __restrict__ tiles,
                                                          int* __restrict__ ntiles, int cap) {
-  __shared__ int base[kTileClasses][513];
-  const int e = threadIdx.x;
+  __shared__ int wsum[kTileClasses][8];
+  const int e = threadIdx.x, lane = e & 63, wave = e >> 6;
   const int ng = n_routed + (shared_rows > 0 ? 1 : 0);
   int b = 0, full = 0, cnt[kTileClasses] = {0, 0, 0};
   if (e < ng) {
@@ -330,22 +332,40 @@ __global__ __launch_bounds__(512) void tile_table_kernel(const int32_t* __restri
     cnt[1] = (rem > 32 && rem <= 64) ? 1 : 0;
     cnt[0] = (rem > 0 && rem <= 32) ? 1 : 0;
   }
+  int incl[kTileClasses];
 #pragma unroll
   for (int c = 0; c < kTileClasses; ++c) {
-    base[c][e + 1] = cnt[c];
-    if (e == 0) base[c][0] = 0;
+    int x = cnt[c];
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(x, d, 64);
+      if (lane >= d) x += y;
+    }
+    incl[c] = x;
+    if (lane == 63) wsum[c][wave] = x;
   }
   __syncthreads();
-  if (e < kTileClasses)
-    for (int q = 1; q <= ng; ++q) base[e][q] += base[e][q - 1];
-  __syncthreads();
+  int base[kTileClasses], total[kTileClasses];
+#pragma unroll
+  for (int c = 0; c < kTileClasses; ++c) {
+    int before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      const int v = wsum[c][w];
+      before += w < wave ? v : 0;
+      all += v;
+    }
+    base[c] = before + incl[c] - cnt[c];
+    total[c] = all;
+  }
   for (int i = 0; i < cnt[2]; ++i) {
-    const int slot = base[2][e] + i;
+    const int slot = base[2] + i;
     if (slot < cap) tiles[2 * cap + slot] = (uint32_t)e | ((uint32_t)(b + i * kBM) << 9);
   }
+#pragma unroll
   for (int c = 0; c < 2; ++c)
-    if (cnt[c] && base[c][e] < cap) tiles[c * cap + base[c][e]] = (uint32_t)e | ((uint32_t)(b + full * kBM) << 9);
-  if (e < kTileClasses) ntiles[e] = min(base[e][ng], cap);
+    if (cnt[c] && base[c] < cap) tiles[c * cap + base[c]] = (uint32_t)e | ((uint32_t)(b + full * kBM) << 9);
+  if (e < kTileClasses) ntiles[e] = min(e == 0 ? total[0] : e == 1 ? total[1] : total[2], cap);
 }
 
 // ------------------------------------------------------------- grouped GEMM --
