@@ -329,7 +329,7 @@ def configs_bench(ctx, layers, geom, seed: int, stream) -> dict:
         "host_call_ms_per_layer": round(gsec * 1e3, 3)}
     out["weights_d_moe_experts"] = {
         "workload": "released-model MoE layer from weights-d bundles (q4nx moe_b1 + bfp16 moe_b2, H=2560, "
-                    "I=1088), 6 routed experts of one token (decode_gate_up_kernel + decode_down_kernel)",
+                    "I=1088), 6 routed experts of one token (decode_gate_up_band_kernel + decode_down_band_kernel)",
         "us_per_layer": round(us, 3), "bytes": b, "GBps": round(b / us / 1e3, 1),
         "frac_hbm_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
     dl.free()

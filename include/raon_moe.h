@@ -215,13 +215,14 @@ int rmoe_moe_experts_dev(rmoe_ctx* ctx, int layer, const void* x_dev, const void
                          void* out_dev, void* stream);
 
 /* rmoe_moe_experts_dev without context scratch: the same kernels and results, with their
- * working memory (arrival counters, fp32 partial sums, activations, expert outputs) in a
- * file-scope device array of 4 MiB that each GPU holds until the process ends, set up
+ * working memory (the activations of the k slots, k x Ipad bf16) in a file-scope device
+ * array of 256 KiB that each GPU holds until the process ends, its address looked up
  * once per device by rmoe_create.  It allocates nothing and needs no rmoe_reserve, for
  * callers that cannot allocate: code under HIP graph capture, tight serving loops,
- * harnesses that forbid allocation.  A layer and k whose scratch exceeds 4 MiB is
- * rejected with RMOE_EINVAL (the BASELINE shape at k=8 needs ~0.7 MiB, the reference
- * model's at k=6 ~0.9 MiB).  All calls on one GPU share the array: calls that overlap on
+ * harnesses that forbid allocation.  A layer and k whose scratch exceeds 256 KiB, or whose
+ * k slots exceed the decode kernels' shape limits, is rejected with RMOE_EINVAL (the
+ * BASELINE shape at k=8 needs 12 KiB, the reference model's at k=6 15 KiB).  All calls
+ * on one GPU share the array: calls that overlap on
  * one GPU (any context, any stream) race.  No counterpart in the reference. */
 int rmoe_moe_experts_static_dev(rmoe_ctx* ctx, int layer, const void* x_dev, const void* top_ids_dev,
                                 const void* top_weights_dev, int k, int act, float gate_beta, float value_beta,

@@ -13,6 +13,8 @@
 // Kernel A streams gate+up of all slots (one launch) and applies the activation in the
 // last workgroup of each (slot, 64-unit) band; kernel B streams down of all slots and
 // the last workgroup of each 64-row output band performs the ordered combine.
+#include <type_traits>
+
 #include "../../include/raon_moe.h"
 #include "rmoe_internal.h"
 
@@ -158,18 +160,11 @@ struct DecodeArgs {
   float gb, vb;
   int residual;
   uint16_t* h;          // [slots, Ipad]
-  float* dout;          // [slots, H] fp32 values of the bf16-rounded expert outputs
   uint16_t* out;        // [H]
   uint16_t* out_routed; // [H] or null
-  float* part_gu;       // [slots, I/64, ks1, 2, 64]
-  float* part_dn;       // [slots, H/64, ks2, 64]
-  unsigned* cnt_gu;     // [slots, I/64]
-  unsigned* cnt_dn;     // [slots, H/64]
-  unsigned* cnt_rt;     // [H/64]
-  int ks1, ks2;
-  // Tokens: blockIdx.y selects the token; every per-token buffer above is the first
-  // token's and the next token's starts the given number of elements later.
-  size_t tok_part_gu, tok_part_dn, tok_cnt_gu, tok_cnt_dn, tok_h, tok_dout;
+  // Tokens: blockIdx.y selects the token; its h starts tok_h elements after the previous
+  // token's.
+  size_t tok_h;
 };
 
 // The arguments of token blockIdx.y (a copy with every per-token pointer advanced).
@@ -181,14 +176,8 @@ __device__ __forceinline__ DecodeArgs token_args(const DecodeArgs& a0) {
   a.ids += t * a.k;
   a.wts += t * a.k;
   a.h += t * a.tok_h;
-  a.dout += t * a.tok_dout;
   if (a.out) a.out += t * a.H;
   if (a.out_routed) a.out_routed += t * a.H;
-  a.part_gu += t * a.tok_part_gu;
-  a.part_dn += t * a.tok_part_dn;
-  a.cnt_gu += t * a.tok_cnt_gu;
-  a.cnt_dn += t * a.tok_cnt_dn;
-  a.cnt_rt += t * a.tok_cnt_dn;
   return a;
 }
 
@@ -198,184 +187,234 @@ __device__ __forceinline__ int slot_expert(const DecodeArgs& a, int s) {
   return e < 0 ? 0 : (e >= a.n_routed ? a.n_routed - 1 : e);
 }
 
-constexpr int kMaxRange = 8;  // K tiles per workgroup
-
-// Stage nrange*128 bf16 of src (starting at column c0) into xs as pairs, and group sums.
-__device__ __forceinline__ void stage_vector(const uint16_t* src, int c0, int nrange, uint32_t* xs, float* ssum) {
-  const int tid = threadIdx.x;
-  const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src + c0);
-  for (int i = tid; i < nrange * 64; i += blockDim.x) xs[i] = s32[i];
-  __syncthreads();
-  for (int g = tid; g < nrange * 4; g += blockDim.x) {
-    float s = 0.f;
-    for (int c = 0; c < 16; ++c) {
-      const uint32_t v = xs[g * 16 + c];
-      s += bf16_to_f32(v & 0xffffu);
-      s += bf16_to_f32(v >> 16);
-    }
-    ssum[g] = s;
-  }
-  __syncthreads();
+// One row of a q4nx tile: its 4 code chunks and its scale|min words.
+struct Q4Row {
+  uint4 c[4], sm;
+};
+__device__ __forceinline__ void q4_row_load(const uint8_t* tile, int row, Q4Row& r) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r.c[j] = load_stream16(tile + j * 1024 + row * 16);
+  r.sm = load_stream16(tile + kCodeBytes + row * 16);
 }
-
-// Accumulate one tile row band for one lane.
-__device__ __forceinline__ float tile_accumulate(const uint8_t* tile, int lane, const uint32_t* xs, const float* ss,
-                                                 float acc) {
-  uint4 c[4];
+__device__ __forceinline__ float q4_row_dot(const Q4Row& r, const uint32_t* xs, const float* ss, float acc) {
+  const uint32_t sm[4] = {r.sm.x, r.sm.y, r.sm.z, r.sm.w};
 #pragma unroll
-  for (int j = 0; j < 4; ++j) c[j] = load_stream16(tile + j * 1024 + lane * 16);
-  const uint4 smq = load_stream16(tile + kCodeBytes + lane * 16);
-  const uint32_t sm[4] = {smq.x, smq.y, smq.z, smq.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) acc = group_apply(sm[j], group_dot(c[j], xs + j * 16), ss[j], acc);
+  for (int j = 0; j < 4; ++j) acc = group_apply(sm[j], group_dot(r.c[j], xs + j * 16), ss[j], acc);
   return acc;
 }
 
-// grid (slots*(I/64)*ks1, tokens), block 256.
-__global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeArgs a0) {
-  const DecodeArgs a = token_args(a0);
-  __shared__ uint32_t xs[kMaxRange * 64];
-  __shared__ float ssum[kMaxRange * 4];
-  __shared__ float red[4][2][64];
-  __shared__ unsigned last_flag;
-  const int nj = a.I / 64;
-  const int s = blockIdx.x / (nj * a.ks1);
-  const int rem = blockIdx.x % (nj * a.ks1);
-  const int j = rem / a.ks1, ks = rem % a.ks1;
-  const int nkt = a.H / kTileCols;
-  const int per = (nkt + a.ks1 - 1) / a.ks1;
-  const int kt0 = ks * per;
-  const int nrange = max(0, min(per, nkt - kt0));
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
-  const int e = slot_expert(a, s);
-  const uint8_t* W = a.gu + (size_t)e * a.gu_bytes;
+// ------------------------------------------------ row-band decode kernels --
+// The per-stage decode in two launches with no workgroup-to-workgroup hand-off:
+//   decode_gate_up_band_kernel<R>: one workgroup per (slot, R units of I) over all of K:
+//     lane L takes row R-slice row (L % R) of K tile (L / R) + G * (wave + W * i) of the
+//     gate and of the up band, G = 64 / R tiles per wave at a time; the lane groups' and
+//     waves' sums are added in a fixed order (shuffle tree, then waves in order), then
+//     the activation and h (bf16).
+//   decode_down_band_kernel<kFmt, R>: one workgroup per R output rows over every slot:
+//     a lane group takes one (slot, K tile) item; per slot the tiles' sums are added in K
+//     order and rounded to bf16 (the expert output), then the slots are combined in
+//     ascending expert order in fp32 (then the shared row and the residual), as the
+//     reference's moe_experts does.
+constexpr int kBandPad = 4;  // dwords of padding after each K tile's activations in LDS
 
-  stage_vector(a.x, kt0 * kTileCols, nrange, xs, ssum);
-
-  float acc[2] = {0.f, 0.f};
-  for (int it = wave; it < 2 * nrange; it += nwaves) {
-    const int sel = it & 1, kk = it >> 1;
-    const int rt = sel ? nj + j : j;  // gate band j, up band I/64 + j
-    const uint8_t* tile = W + ((size_t)rt * nkt + kt0 + kk) * kTileBytes;
-    acc[sel] = tile_accumulate(tile, lane, xs + kk * 64, ssum + kk * 4, acc[sel]);
-  }
-  red[wave][0][lane] = acc[0];
-  red[wave][1][lane] = acc[1];
-  __syncthreads();
-  float g = 0.f, u = 0.f;
-  if (wave == 0) {
-    for (int w = 0; w < nwaves; ++w) {
-      g += red[w][0][lane];
-      u += red[w][1][lane];
+// Stage nvec vectors of n bf16 (vector v at src + v * stride) into LDS as pairs, one K
+// tile (64 dwords) per kBandPad-padded row, vectors one after another; with
+// sums != nullptr also the group sums (32 values each, n / 32 per vector).  Every thread
+// requests its (up to 4) 16-byte units before it stores any, so the vectors' loads are in
+// flight together.
+__device__ __forceinline__ void stage_band(const uint16_t* src, size_t stride, int nvec, int n, uint32_t* xs,
+                                           float* sums) {
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int units = n / 8, total = nvec * units;  // 16-byte units; units % 16 == 0
+  for (int i0 = tid; i0 < total; i0 += 4 * nthr) {
+    uint4 v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = i0 + q * nthr;
+      if (i < total) v[q] = reinterpret_cast<const uint4*>(src + (size_t)(i / units) * stride)[i % units];
     }
-  }
-  const size_t band = (size_t)s * nj + j;
-  if (a.ks1 > 1) {
-    float* part = a.part_gu + (band * a.ks1 + ks) * 128;
-    if (wave == 0) {
-      st_dev(&part[lane], g);
-      st_dev(&part[64 + lane], u);
-    }
-    if (!arrive_last(&a.cnt_gu[band], (unsigned)a.ks1, &last_flag)) return;
-    if (wave == 0) {
-      const float* pb = a.part_gu + band * a.ks1 * 128;
-      g = 0.f;
-      u = 0.f;
-      for (int q = 0; q < a.ks1; ++q) {
-        g += ld_dev(&pb[q * 128 + lane]);
-        u += ld_dev(&pb[q * 128 + 64 + lane]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = i0 + q * nthr;
+      if (i >= total) break;
+      const int vec = i / units, u = i % units;
+      *reinterpret_cast<uint4*>(xs + (size_t)vec * (units / 16) * (64 + kBandPad) + (u >> 4) * (64 + kBandPad) +
+                                (u & 15) * 4) = v[q];
+      if (sums) {
+        float sv = ((bf16_to_f32(v[q].x & 0xffffu) + bf16_to_f32(v[q].x >> 16)) +
+                    (bf16_to_f32(v[q].y & 0xffffu) + bf16_to_f32(v[q].y >> 16))) +
+                   ((bf16_to_f32(v[q].z & 0xffffu) + bf16_to_f32(v[q].z >> 16)) +
+                    (bf16_to_f32(v[q].w & 0xffffu) + bf16_to_f32(v[q].w >> 16)));
+        // units 4j..4j+3 (one group) are held by neighbouring lanes (nthr % 64 == 0)
+        sv += __shfl_xor(sv, 1, 64);
+        sv += __shfl_xor(sv, 2, 64);
+        if ((u & 3) == 0) sums[(size_t)vec * (units / 4) + (u >> 2)] = sv;
       }
     }
-  }
-  if (wave == 0) {
-    const float gb = bf16_round(g), ub = bf16_round(u);
-    a.h[(size_t)s * a.Ipad + j * 64 + lane] = (uint16_t)f32_to_bf16(act_apply(a.act, gb, ub, a.gb, a.vb));
-    // The down input's padding columns [I, Ipad) are zero: the scratch is shared with
-    // other layers and launches, and padded weights need not be zero (bfp16 moe_b2).
-    if (j == nj - 1)
-      for (int c = a.I + lane; c < a.Ipad; c += 64) a.h[(size_t)s * a.Ipad + c] = 0;
   }
 }
 
-// grid slots*(H/64)*ks2, block 64*waves.  kFmt: format of the down weights (q4nx, or
-// bfp16 for a weights-d layer whose moe_b2 holds bfp16ebs8 experts).
-template <int kFmt>
-__global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a0) {
+// grid (slots * I / R, tokens), block 64 * W.  Dynamic LDS: x [nkt][64 + pad] pairs,
+// group sums [nkt * 4], wave sums [W][2][R].
+template <int R>
+__global__ __launch_bounds__(1024) void decode_gate_up_band_kernel(DecodeArgs a0) {
+  constexpr int G = 64 / R;
   const DecodeArgs a = token_args(a0);
-  __shared__ uint32_t xs[kMaxRange * 64];
-  __shared__ float ssum[kMaxRange * 4];
-  __shared__ float red[4][64];
-  __shared__ unsigned last_flag;
-  const int nrt = a.H / 64;
-  const int s = blockIdx.x / (nrt * a.ks2);
-  const int rem = blockIdx.x % (nrt * a.ks2);
-  const int rt = rem / a.ks2, ks = rem % a.ks2;
-  const int nkt = a.Ipad / kTileCols;
-  const int per = (nkt + a.ks2 - 1) / a.ks2;
-  const int kt0 = ks * per;
-  const int nrange = max(0, min(per, nkt - kt0));
+  extern __shared__ __attribute__((aligned(16))) uint32_t band_lds[];
+  const int nkt = a.H / kTileCols, tstride = 64 + kBandPad;
+  uint32_t* xs = band_lds;
+  float* ssum = reinterpret_cast<float*>(band_lds + nkt * tstride);
+  float* red = ssum + nkt * 4;
+  const int groups = a.I / R;
+  const int s = blockIdx.x / groups, u0 = (blockIdx.x % groups) * R;
+  const int band = u0 / kTileRows, rsub = u0 % kTileRows;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+  const int g = lane / R, r = lane % R;
   const int e = slot_expert(a, s);
-  const uint8_t* W = a.dn + (size_t)e * a.dn_bytes;
-
-  stage_vector(a.h + (size_t)s * a.Ipad, kt0 * kTileCols, nrange, xs, ssum);
-
-  float acc = 0.f;
-  for (int it = wave; it < nrange; it += nwaves) {
-    if constexpr (kFmt == RMOE_FMT_BFP16) {
-      const uint8_t* tile = W + ((size_t)rt * nkt + kt0 + it) * kB16TileBytes;
-      acc = b16_tile_accumulate(tile, lane, xs + it * 64, acc);
-    } else {
-      const uint8_t* tile = W + ((size_t)rt * nkt + kt0 + it) * kTileBytes;
-      acc = tile_accumulate(tile, lane, xs + it * 64, ssum + it * 4, acc);
-    }
+  const uint8_t* W = a.gu + (size_t)e * a.gu_bytes;
+  const uint8_t* gate = W + (size_t)band * nkt * kTileBytes + (size_t)(rsub + r) * 16;
+  const uint8_t* up = W + (size_t)(a.I / kTileRows + band) * nkt * kTileBytes + (size_t)(rsub + r) * 16;
+  const int kt0 = wave * G + g;
+  // The first tiles are requested before x is staged: loads complete in order.
+  uint4 cg[4], cu[4], sg, su;
+  {
+    const size_t o = (size_t)(kt0 < nkt ? kt0 : 0) * kTileBytes;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) cg[j] = load_stream16(gate + o + j * 1024);
+    sg = load_stream16(gate + o + kCodeBytes);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) cu[j] = load_stream16(up + o + j * 1024);
+    su = load_stream16(up + o + kCodeBytes);
   }
-  red[wave][lane] = acc;
+  stage_band(a.x, 0, 1, a.H, xs, ssum);
   __syncthreads();
-  float d = 0.f;
-  if (wave == 0)
-    for (int w = 0; w < nwaves; ++w) d += red[w][lane];
-  const size_t band = (size_t)s * nrt + rt;
-  if (a.ks2 > 1) {
-    float* part = a.part_dn + (band * a.ks2 + ks) * 64;
-    if (wave == 0) st_dev(&part[lane], d);
-    if (!arrive_last(&a.cnt_dn[band], (unsigned)a.ks2, &last_flag)) return;
-    if (wave == 0) {
-      const float* pb = a.part_dn + band * a.ks2 * 64;
-      d = 0.f;
-      for (int q = 0; q < a.ks2; ++q) d += ld_dev(&pb[q * 64 + lane]);
+  float ag = 0.f, au = 0.f;
+  for (int kt = kt0; kt < nkt; kt += nwaves * G) {
+    if (kt != kt0) {
+      const size_t o = (size_t)kt * kTileBytes;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cg[j] = load_stream16(gate + o + j * 1024);
+      sg = load_stream16(gate + o + kCodeBytes);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cu[j] = load_stream16(up + o + j * 1024);
+      su = load_stream16(up + o + kCodeBytes);
+    }
+    const uint32_t smg[4] = {sg.x, sg.y, sg.z, sg.w}, smu[4] = {su.x, su.y, su.z, su.w};
+    const uint32_t* xt = xs + kt * tstride;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      ag = group_apply(smg[j], group_dot(cg[j], xt + j * 16), ssum[kt * 4 + j], ag);
+      au = group_apply(smu[j], group_dot(cu[j], xt + j * 16), ssum[kt * 4 + j], au);
     }
   }
-  const int row = rt * 64 + lane;
-  // Expert outputs are handed to the combining workgroup as the fp32 value of the
-  // bf16-rounded result.
-  if (wave == 0) st_dev(&a.dout[(size_t)s * a.H + row], bf16_round(d));
-  // Second level: the last slot to finish this 64-row band combines all slots.
-  if (!arrive_last(&a.cnt_rt[rt], (unsigned)a.slots, &last_flag)) return;
+#pragma unroll
+  for (int m = R; m < 64; m *= 2) {
+    ag += __shfl_xor(ag, m, 64);
+    au += __shfl_xor(au, m, 64);
+  }
+  if (g == 0) {
+    red[(wave * 2 + 0) * R + r] = ag;
+    red[(wave * 2 + 1) * R + r] = au;
+  }
+  __syncthreads();
+  if (wave == 0 && lane < R) {
+    float gs = 0.f, us = 0.f;
+    for (int w = 0; w < nwaves; ++w) {
+      gs += red[(w * 2 + 0) * R + lane];
+      us += red[(w * 2 + 1) * R + lane];
+    }
+    a.h[(size_t)s * a.Ipad + u0 + lane] =
+        (uint16_t)f32_to_bf16(act_apply(a.act, bf16_round(gs), bf16_round(us), a.gb, a.vb));
+  }
+  // The down input's padding columns [I, Ipad) are zero: the scratch is shared with other
+  // layers and launches, and padded weights need not be zero (bfp16 moe_b2).
+  if (wave == 0 && u0 + R == a.I)
+    for (int c = a.I + lane; c < a.Ipad; c += 64) a.h[(size_t)s * a.Ipad + c] = 0;
+}
+
+// grid (H / R, tokens), block 64 * W.  Dynamic LDS: h of every slot [slots][nkt][64 + pad]
+// pairs, group sums [slots][nkt * 4] (q4nx), item sums [slots][nkt][R].
+template <int kFmt, int R>
+__global__ __launch_bounds__(1024) void decode_down_band_kernel(DecodeArgs a0) {
+  constexpr int G = 64 / R;
+  const DecodeArgs a = token_args(a0);
+  extern __shared__ __attribute__((aligned(16))) uint32_t band_lds[];
+  const int nkt = a.Ipad / kTileCols, tstride = 64 + kBandPad;
+  const int items = a.slots * nkt;
+  uint32_t* hs = band_lds;
+  float* ssum = reinterpret_cast<float*>(band_lds + items * tstride);
+  float* isum = ssum + items * 4;
+  const int row0 = blockIdx.x * R, band = row0 / kTileRows, rsub = row0 % kTileRows;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+  const int g = lane / R, r = lane % R;
+  constexpr int kTB = kFmt == RMOE_FMT_BFP16 ? kB16TileBytes : kTileBytes;
+  using Row = typename std::conditional<kFmt == RMOE_FMT_BFP16, B16Row, Q4Row>::type;
+  __shared__ int s_ord[32];
+  __shared__ float s_w[32];
+  __shared__ int s_n;
+  auto tile_of = [&](int it) {
+    const int s = it / nkt, kt = it % nkt;
+    return a.dn + (size_t)slot_expert(a, s) * a.dn_bytes + ((size_t)band * nkt + kt) * kTB;
+  };
+  auto load_row = [&](int it, Row& w) {
+    if constexpr (kFmt == RMOE_FMT_BFP16)
+      b16_row_load(tile_of(it), rsub + r, w);
+    else
+      q4_row_load(tile_of(it), rsub + r, w);
+  };
+  // The first item's weight row is requested before h is staged.
+  const int it0 = wave * G + g;
+  Row wr;
+  if (it0 < items) load_row(it0, wr);
+  // Combine order: the routed slots by ascending expert id, as a scan for the next
+  // larger id from -1 takes them (a repeated id counts once, at its first slot; negative
+  // ids are skipped).
   if (wave == 0) {
-    // Ascending expert id over the routed slots (ids are distinct per token).
-    float acc2 = 0.f;
-    int prev = -1;
-    for (int r = 0; r < a.k; ++r) {
-      int best = 0x7fffffff, bs = -1;
-      for (int q = 0; q < a.k; ++q) {
-        const int eq = a.ids[q];
-        if (eq > prev && eq < best) {
-          best = eq;
-          bs = q;
-        }
-      }
-      if (bs < 0) break;
-      prev = best;
-      const float dv = ld_dev(&a.dout[(size_t)bs * a.H + row]);
-      acc2 = __fadd_rn(acc2, __fmul_rn(dv, a.wts[bs]));
+    const int eq = lane < a.k ? a.ids[lane] : 0x7fffffff;
+    const float wq = lane < a.k ? a.wts[lane] : 0.f;
+    int rank = 0, n = 0;
+    bool first = eq >= 0;
+    for (int q2 = 0; q2 < a.k; ++q2) {
+      const int e2 = __shfl(eq, q2, 64);
+      bool f2 = e2 >= 0;
+      for (int q3 = 0; q3 < q2; ++q3) f2 = f2 && __shfl(eq, q3, 64) != e2;
+      n += f2 ? 1 : 0;
+      if (q2 < lane && e2 == eq) first = false;
+      rank += (f2 && e2 < eq) ? 1 : 0;
     }
-    uint32_t o = f32_to_bf16(acc2);
-    if (a.out_routed) a.out_routed[row] = (uint16_t)o;
-    if (a.slots > a.k) o = f32_to_bf16(__fadd_rn(bf16_to_f32(o), ld_dev(&a.dout[(size_t)a.k * a.H + row])));
-    if (a.residual) o = f32_to_bf16(__fadd_rn(bf16_to_f32(a.x[row]), bf16_to_f32(o)));
-    if (a.out) a.out[row] = (uint16_t)o;
+    if (lane < a.k && first) {
+      s_ord[rank] = lane;
+      s_w[rank] = wq;
+    }
+    if (lane == 0) s_n = n;
   }
+  stage_band(a.h, a.Ipad, a.slots, a.Ipad, hs, kFmt == RMOE_FMT_BFP16 ? nullptr : ssum);
+  __syncthreads();
+  for (int it = it0; it < items; it += nwaves * G) {
+    if (it != it0) load_row(it, wr);
+    float acc;
+    if constexpr (kFmt == RMOE_FMT_BFP16)
+      acc = b16_row_dot(wr, hs + (size_t)it * tstride, 0.f);
+    else
+      acc = q4_row_dot(wr, hs + (size_t)it * tstride, ssum + (size_t)it * 4, 0.f);
+    isum[(size_t)it * R + r] = acc;
+  }
+  __syncthreads();
+  if (wave != 0 || lane >= R) return;
+  const int row = row0 + lane;
+  // Expert outputs (bf16-rounded), combined in ascending expert id over the routed slots.
+  auto slot_out = [&](int s) {
+    float d = 0.f;
+    for (int kt = 0; kt < nkt; ++kt) d += isum[(size_t)(s * nkt + kt) * R + lane];
+    return bf16_round(d);
+  };
+  float acc2 = 0.f;
+  for (int q = 0; q < s_n; ++q) acc2 = __fadd_rn(acc2, __fmul_rn(slot_out(s_ord[q]), s_w[q]));
+  uint32_t o = f32_to_bf16(acc2);
+  if (a.out_routed) a.out_routed[row] = (uint16_t)o;
+  if (a.slots > a.k) o = f32_to_bf16(__fadd_rn(bf16_to_f32(o), slot_out(a.k)));
+  if (a.residual) o = f32_to_bf16(__fadd_rn(bf16_to_f32(a.x[row]), bf16_to_f32(o)));
+  if (a.out) a.out[row] = (uint16_t)o;
 }
 
 }  // namespace
@@ -391,41 +430,37 @@ hipError_t launch_route(const RmoeLayer& L, const uint16_t* x, int T, int32_t* i
   return hipGetLastError();
 }
 
-static void decode_splits(const RmoeLayer& L, int& ks1, int& ks2) {
-  const int nkt1 = L.H / kTileCols, nkt2 = L.Ipad / kTileCols;
-  ks1 = (nkt1 + 1) / 2;           // two K tiles per band-pair per workgroup -> 4 waves
-  if (ks1 < 1) ks1 = 1;
-  ks2 = (nkt2 + 1) / 2;
-  if (ks2 < 1) ks2 = 1;
-  while ((nkt1 + ks1 - 1) / ks1 > kMaxRange) ++ks1;
-  while ((nkt2 + ks2 - 1) / ks2 > kMaxRange) ++ks2;
+// Launch shape of the row-band decode kernels: 16 units of I per gate/up workgroup (4 K
+// tiles per wave at a time), 8 output rows per down workgroup (8 (slot, K tile) items per
+// wave at a time); dynamic LDS of each.
+constexpr int kRGU = 16, kRDN = 8;
+struct BandShape {
+  int w1, w2;
+  size_t lds1, lds2;
+};
+static BandShape band_shape(const RmoeLayer& L, int slots) {
+  BandShape b;
+  const int nkt1 = L.H / kTileCols, nkt2 = L.Ipad / kTileCols, items = slots * nkt2;
+  b.w1 = min(16, (nkt1 + (64 / kRGU) - 1) / (64 / kRGU));
+  b.w2 = min(16, (items + (64 / kRDN) - 1) / (64 / kRDN));
+  b.lds1 = ((size_t)nkt1 * (64 + kBandPad) + (size_t)nkt1 * 4 + (size_t)b.w1 * 2 * kRGU) * 4;
+  b.lds2 = ((size_t)items * (64 + kBandPad) + (size_t)items * 4 + (size_t)items * kRDN) * 4;
+  return b;
 }
-
-size_t decode_scratch_floats(const RmoeLayer& L) {
-  int ks1, ks2;
-  decode_splits(L, ks1, ks2);
-  const size_t slots = (size_t)L.top_k + L.n_shared;
-  return slots * (L.I / 64) * ks1 * 128 + slots * (L.H / 64) * ks2 * 64;
-}
-
-size_t decode_scratch_counters(const RmoeLayer& L) {
-  const size_t slots = (size_t)L.top_k + L.n_shared;
-  return slots * (L.I / 64) + slots * (L.H / 64) + (L.H / 64);
+hipError_t decode_band_check(const RmoeLayer& L, int slots) {
+  const BandShape b = band_shape(L, slots);
+  if (L.I % kRGU || L.H % kRDN || b.lds1 > kDecodeMaxLds || b.lds2 > kDecodeMaxLds) return hipErrorInvalidValue;
+  return hipSuccess;
 }
 
 hipError_t launch_moe_decode(const RmoeLayer& L, const uint16_t* x, const int32_t* ids, const float* wts, int k,
                              bool with_shared, int act, float gb, float vb, bool residual, uint16_t* out,
                              uint16_t* out_routed, RmoeScratch& s, hipStream_t st, int stages, int ntok) {
-  int ks1, ks2;
-  decode_splits(L, ks1, ks2);
   const int slots = k + (with_shared ? 1 : 0);
   // A weights-d layer keeps the shared gate/up outside the layer: routed slots only.
   if (with_shared && (L.n_shared < 1 || L.d_layout)) return hipErrorInvalidValue;
   if (ntok < 1) return hipErrorInvalidValue;
-  const size_t nf = (size_t)slots * (L.I / 64) * ks1 * 128 + (size_t)slots * (L.H / 64) * ks2 * 64;
-  const size_t nc = (size_t)slots * (L.I / 64) + (size_t)slots * (L.H / 64) + (L.H / 64);
-  if (nf * ntok > s.part_floats || nc * ntok > s.n_counters || (size_t)slots * L.Ipad * ntok > s.h_elems ||
-      (size_t)slots * L.H * ntok > s.dout_elems)
+  if ((size_t)slots * L.Ipad * ntok > s.h_elems || decode_band_check(L, slots) != hipSuccess)
     return hipErrorInvalidValue;
   DecodeArgs a{};
   a.gu = L.gu;
@@ -446,39 +481,23 @@ hipError_t launch_moe_decode(const RmoeLayer& L, const uint16_t* x, const int32_
   a.vb = vb;
   a.residual = residual ? 1 : 0;
   a.h = s.h;
-  a.dout = s.dout;
   a.out = out;
   a.out_routed = out_routed;
-  a.part_gu = s.part;
-  a.part_dn = s.part + (size_t)slots * (L.I / 64) * ks1 * 128;
-  a.cnt_gu = s.counters;
-  a.cnt_dn = s.counters + (size_t)slots * (L.I / 64);
-  a.cnt_rt = a.cnt_dn + (size_t)slots * (L.H / 64);
-  a.ks1 = ks1;
-  a.ks2 = ks2;
-  // Token t's scratch: its partials and counters follow token t-1's (the layout of one
-  // token repeated), its h and expert outputs likewise.
-  a.tok_part_gu = nf;
-  a.tok_part_dn = nf;
-  a.tok_cnt_gu = nc;
-  a.tok_cnt_dn = nc;
-  a.tok_h = (size_t)slots * L.Ipad;
-  a.tok_dout = (size_t)slots * L.H;
-  const int nkt1 = L.H / kTileCols, nkt2 = L.Ipad / kTileCols;
-  const int per1 = (nkt1 + ks1 - 1) / ks1, per2 = (nkt2 + ks2 - 1) / ks2;
-  const int w1 = min(4, 2 * per1), w2 = min(4, per2);
+  a.tok_h = (size_t)slots * L.Ipad;  // token t's h follows token t-1's
+  const BandShape b = band_shape(L, slots);
   if (stages & 1) {
-    hipLaunchKernelGGL(decode_gate_up_kernel, dim3(slots * (L.I / 64) * ks1, ntok), dim3(64 * w1), 0, st, a);
+    hipLaunchKernelGGL(decode_gate_up_band_kernel<kRGU>, dim3(slots * (L.I / kRGU), ntok), dim3(64 * b.w1), b.lds1,
+                       st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (stages & 2) {
     if (L.dn_fmt == RMOE_FMT_BFP16)
-      hipLaunchKernelGGL(decode_down_kernel<RMOE_FMT_BFP16>, dim3(slots * (L.H / 64) * ks2, ntok), dim3(64 * w2), 0,
-                         st, a);
+      hipLaunchKernelGGL((decode_down_band_kernel<RMOE_FMT_BFP16, kRDN>), dim3(L.H / kRDN, ntok), dim3(64 * b.w2),
+                         b.lds2, st, a);
     else
-      hipLaunchKernelGGL(decode_down_kernel<RMOE_FMT_Q4NX>, dim3(slots * (L.H / 64) * ks2, ntok), dim3(64 * w2), 0,
-                         st, a);
+      hipLaunchKernelGGL((decode_down_band_kernel<RMOE_FMT_Q4NX, kRDN>), dim3(L.H / kRDN, ntok), dim3(64 * b.w2),
+                         b.lds2, st, a);
     return hipGetLastError();
   }
   return hipSuccess;

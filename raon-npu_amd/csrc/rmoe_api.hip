@@ -100,19 +100,15 @@ int reserve_stack(rmoe_ctx* ctx, const RmoeLayer& L, int n_layers);
 // Size every scratch buffer for `layer` with up to T tokens and k routes.
 int reserve_layer(rmoe_ctx* ctx, const RmoeLayer& L, int T, int k) {
   RmoeScratch& s = ctx->s;
-  RmoeLayer Lk = L;
-  Lk.top_k = std::max(k, L.top_k);
-  const int kk = Lk.top_k;
+  const int kk = std::max(k, L.top_k);
   size_t f1, c1, f2, c2;
   linear_needs(2 * L.I, L.H, T, f1, c1);
   linear_needs(L.H, L.Ipad, T, f2, c2);
-  Lk.n_shared = 1;
-  const size_t floats = std::max({rmoe::decode_scratch_floats(Lk), f1, f2});
-  const size_t counters = std::max({rmoe::decode_scratch_counters(Lk), c1, c2, (size_t)T});
+  const size_t floats = std::max(f1, f2);
+  const size_t counters = std::max({c1, c2, (size_t)T});  // K-split linear; one per routed token
   TRY(grow(s.part, s.part_floats, floats, ctx));
   TRY(grow(s.counters, s.n_counters, counters, ctx));
   TRY(grow(s.h, s.h_elems, (size_t)(kk + 1) * L.Ipad, ctx));
-  TRY(grow(s.dout, s.dout_elems, (size_t)(kk + 1) * L.H, ctx));
   size_t re = s.route_elems;
   TRY(grow(s.ids, re, (size_t)T * kk, ctx));
   re = s.route_elems;
@@ -127,6 +123,8 @@ int reserve_layer(rmoe_ctx* ctx, const RmoeLayer& L, int T, int k) {
   TRY(grow(s.inv, oe, (size_t)T * kk, ctx));
   s.order_elems = oe;
   TRY(grow(s.offsets, s.offset_elems, 257, ctx));
+  RmoeLayer Lk = L;
+  Lk.top_k = kk;
   if (L.n_shared > 0) TRY(grow(s.pf, s.pf_bytes, rmoe::prefill_scratch_bytes(Lk, T), ctx));
   if (L.n_shared > 0 && !L.d_layout) TRY(reserve_stack(ctx, L, 1));
   s.max_tokens = std::max(s.max_tokens, T);
@@ -222,11 +220,10 @@ int check_ids(const int32_t* ids, int T, int k, int n_routed) {
 // ------------------------------------------------------- static decode scratch --
 // rmoe_moe_experts_static_dev runs the routed-expert decode kernels on this file-scope
 // device array instead of context scratch, so it never allocates.  Each GPU holds its
-// own copy until the process ends.  Layout: the kernels' arrival counters (which must
-// be zero when a launch starts, and which every complete launch leaves at zero), then
-// the fp32 partial sums, the activations h and the expert outputs.
-constexpr size_t kStaticScratchBytes = 4u << 20;
-constexpr size_t kStaticCounterBytes = 64u << 10;
+// own copy until the process ends.  It holds the activations h of the call's slots
+// ([k][Ipad] bf16), which the gate/up kernel writes in full (padding columns included)
+// before the down kernel reads them, so nothing in it must start at zero.
+constexpr size_t kStaticScratchBytes = 256u << 10;
 
 }  // namespace
 
@@ -240,15 +237,13 @@ std::mutex g_scratch_mu;
 std::map<int, uint8_t*> g_scratch_ptr;
 
 // Called by rmoe_create with the context's device current: the first context on a
-// device looks up the array's address and zeroes it (its counters must start at zero).
+// device looks up the array's address.
 int init_static_scratch(rmoe_ctx* ctx) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr.count(ctx->device)) return RMOE_OK;
   void* p = nullptr;
   hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
   if (e != hipSuccess || !p) return fail(RMOE_EDEVICE, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
-  HIP_TRY(hipMemsetAsync(p, 0, kStaticScratchBytes, ctx->stream));
-  HIP_TRY(hipStreamSynchronize(ctx->stream));
   g_scratch_ptr[ctx->device] = static_cast<uint8_t*>(p);
   return RMOE_OK;
 }
@@ -317,7 +312,7 @@ int rmoe_destroy(rmoe_ctx* ctx) {
     hipFree(kv.second.router_bias);
   }
   RmoeScratch& s = ctx->s;
-  void* bufs[] = {s.part, s.counters, s.h, s.dout, s.ids, s.wts, s.logits, s.order, s.inv, s.offsets,
+  void* bufs[] = {s.part, s.counters, s.h, s.ids, s.wts, s.logits, s.order, s.inv, s.offsets,
                   s.chunk_counts, s.err, s.staging, s.pf, s.stack, s.stack_cnt};
   for (void* b : bufs)
     if (b) hipFree(b);
@@ -853,6 +848,17 @@ int rmoe_route(rmoe_ctx* ctx, int layer, const uint16_t* x, int T, int32_t* top_
   return RMOE_OK;
 }
 
+// The per-stage decode kernels' shape limits (rows per workgroup, activations of every
+// slot in one workgroup's LDS).
+static int check_decode_shape(const RmoeLayer& L, int slots, int layer) {
+  if (rmoe::decode_band_check(L, slots) != hipSuccess)
+    return fail(RMOE_EINVAL,
+                "layer %d with %d expert slots exceeds the decode kernels' shape limits (I %% 16, H %% 8, %zu bytes "
+                "of LDS)",
+                layer, slots, rmoe::kDecodeMaxLds);
+  return RMOE_OK;
+}
+
 int rmoe_moe_experts(rmoe_ctx* ctx, int layer, const uint16_t* x, const int32_t* top_ids, const float* top_weights,
                      int k, int act, float gate_beta, float value_beta, uint16_t* out) {
   RmoeLayer* L;
@@ -861,6 +867,7 @@ int rmoe_moe_experts(rmoe_ctx* ctx, int layer, const uint16_t* x, const int32_t*
   if (k < 1 || k > 16) return fail(RMOE_EINVAL, "k (%d) must be in 1..16", k);
   if (act != RMOE_ACT_SITU && act != RMOE_ACT_SWIGLU) return fail(RMOE_EINVAL, "unknown activation %d", act);
   TRY(check_ids(top_ids, 1, k, L->n_routed));
+  TRY(check_decode_shape(*L, k, layer));
   HIP_TRY(hipSetDevice(ctx->device));
   TRY(reserve_layer(ctx, *L, 1, k));
   const size_t xb = align_up((size_t)L->H * 2, 256);
@@ -886,6 +893,7 @@ int rmoe_moe_experts_dev(rmoe_ctx* ctx, int layer, const void* x_dev, const void
   if (!x_dev || !top_ids_dev || !top_weights_dev || !out_dev) return fail(RMOE_EINVAL, "null argument");
   if (k < 1 || k > 16 || k > L->n_routed) return fail(RMOE_EINVAL, "k (%d) must be in 1..min(16, n_routed)", k);
   if (act != RMOE_ACT_SITU && act != RMOE_ACT_SWIGLU) return fail(RMOE_EINVAL, "unknown activation %d", act);
+  TRY(check_decode_shape(*L, k, layer));
   hipError_t e = rmoe::launch_moe_decode(*L, (const uint16_t*)x_dev, (const int32_t*)top_ids_dev,
                                          (const float*)top_weights_dev, k, false, act, gate_beta, value_beta, false,
                                          nullptr, (uint16_t*)out_dev, ctx->s, pick_stream(ctx, stream));
@@ -905,27 +913,16 @@ int rmoe_moe_experts_static_dev(rmoe_ctx* ctx, int layer, const void* x_dev, con
   if (act != RMOE_ACT_SITU && act != RMOE_ACT_SWIGLU) return fail(RMOE_EINVAL, "unknown activation %d", act);
   uint8_t* base = static_scratch(ctx->device);
   if (!base) return fail(RMOE_EDEVICE, "static scratch of device %d was not set up", ctx->device);
-  // The same scratch the routed-expert decode kernels take from a context (k slots, no
-  // shared slot), carved out of the static array.
-  RmoeLayer Lk = *L;
-  Lk.top_k = k;
-  Lk.n_shared = 0;
-  const size_t nc = rmoe::decode_scratch_counters(Lk), nf = rmoe::decode_scratch_floats(Lk);
-  const size_t nh = (size_t)k * L->Ipad, nd = (size_t)k * L->H;
-  const size_t off_f = kStaticCounterBytes, off_h = align_up(off_f + nf * 4, 256);
-  const size_t off_d = align_up(off_h + nh * 2, 256), need = off_d + nd * 4;
-  if (nc * 4 > kStaticCounterBytes || need > kStaticScratchBytes)
+  // The scratch the routed-expert decode kernels take from a context -- the activations h
+  // of k slots (no shared slot) -- in the static array.
+  const size_t nh = (size_t)k * L->Ipad, need = nh * 2;
+  if (need > kStaticScratchBytes)
     return fail(RMOE_EINVAL, "layer %d with k=%d needs %zu bytes of static decode scratch, more than its %zu",
                 layer, k, need, kStaticScratchBytes);
+  TRY(check_decode_shape(*L, k, layer));
   RmoeScratch s{};
-  s.counters = reinterpret_cast<unsigned*>(base);
-  s.n_counters = kStaticCounterBytes / 4;
-  s.part = reinterpret_cast<float*>(base + off_f);
-  s.part_floats = nf;
-  s.h = reinterpret_cast<uint16_t*>(base + off_h);
+  s.h = reinterpret_cast<uint16_t*>(base);
   s.h_elems = nh;
-  s.dout = reinterpret_cast<float*>(base + off_d);
-  s.dout_elems = nd;
   s.err = ctx->s.err;
   hipError_t e = rmoe::launch_moe_decode(*L, (const uint16_t*)x_dev, (const int32_t*)top_ids_dev,
                                          (const float*)top_weights_dev, k, false, act, gate_beta, value_beta, false,
@@ -1026,6 +1023,7 @@ int rmoe_moe_decode_stage_dev(rmoe_ctx* ctx, int layer, int stage, const void* x
   if (act != RMOE_ACT_SITU && act != RMOE_ACT_SWIGLU) return fail(RMOE_EINVAL, "unknown activation %d", act);
   if ((size_t)L->top_k > ctx->s.route_elems || (size_t)L->n_routed > ctx->s.logit_elems)
     return fail(RMOE_EINVAL, "scratch not reserved for layer %d", layer);
+  if (stage > 0) TRY(check_decode_shape(*L, L->top_k + 1, layer));
   hipStream_t st = pick_stream(ctx, stream);
   hipError_t e;
   if (stage == 0) {

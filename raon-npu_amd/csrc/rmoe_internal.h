@@ -121,16 +121,22 @@ __device__ __forceinline__ void mant_pairs(uint32_t w, uint32_t& p0, uint32_t& p
 // Kernel scale of an exponent byte: 2^(max(e, 7) - 133), built as fp32 bits.
 __device__ __forceinline__ float exp_scale(uint32_t e) { return __uint_as_float((max(e, 7u) - 6u) << 23); }
 
-// One lane's row of a bfp16 tile (64 rows x 128 columns) against x of those 128 columns
-// (64 bf16-pair dwords): per 8-column group d = dot(mantissas, x) from 0, then
-// acc = fma(2^(e-133), d, acc), in column order -- the order of the dense bfp16 GEMV.
-__device__ __forceinline__ float b16_tile_accumulate(const uint8_t* tile, int lane, const uint32_t* __restrict__ xs,
-                                                     float acc) {
-  const uint8_t* p = tile + lane * 16;
-  uint4 mc[8];
+// One row of a bfp16 tile (64 rows x 128 columns): 8 mantissa chunks and the exponents.
+struct B16Row {
+  uint4 mc[8], eq;
+};
+__device__ __forceinline__ void b16_row_load(const uint8_t* tile, int row, B16Row& r) {
+  const uint8_t* p = tile + row * 16;
 #pragma unroll
-  for (int c = 0; c < 8; ++c) mc[c] = load_stream16(p + c * 1024);
-  const uint4 eq = load_stream16(p + kB16MantBytes);
+  for (int c = 0; c < 8; ++c) r.mc[c] = load_stream16(p + c * 1024);
+  r.eq = load_stream16(p + kB16MantBytes);
+}
+// A bfp16 tile row against x of its 128 columns (64 bf16-pair dwords): per 8-column
+// group d = dot(mantissas, x) from 0, then acc = fma(2^(e-133), d, acc), in column order
+// -- the order of the dense bfp16 GEMV.
+__device__ __forceinline__ float b16_row_dot(const B16Row& r, const uint32_t* __restrict__ xs, float acc) {
+  const uint4* mc = r.mc;
+  const uint4 eq = r.eq;
   const uint32_t ew[4] = {eq.x, eq.y, eq.z, eq.w};
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
@@ -151,6 +157,13 @@ __device__ __forceinline__ float b16_tile_accumulate(const uint8_t* tile, int la
     }
   }
   return acc;
+}
+// One lane's row (lane = row) of a bfp16 tile: b16_row_load, then b16_row_dot.
+__device__ __forceinline__ float b16_tile_accumulate(const uint8_t* tile, int lane, const uint32_t* __restrict__ xs,
+                                                     float acc) {
+  B16Row r;
+  b16_row_load(tile, lane, r);
+  return b16_row_dot(r, xs, acc);
 }
 
 // Activations, in the operation order of the oracle (fp32).
@@ -268,8 +281,6 @@ struct RmoeScratch {
   size_t n_counters = 0;
   uint16_t* h = nullptr;         // activations [slots, Ipad] / [A, Ipad]
   size_t h_elems = 0;
-  float* dout = nullptr;         // expert outputs [slots, H] (fp32 of the bf16-rounded value)
-  size_t dout_elems = 0;
   int32_t* ids = nullptr;        // routing ids
   float* wts = nullptr;          // routing weights
   float* logits = nullptr;
@@ -370,7 +381,9 @@ hipError_t launch_decode_stack(const RmoeLayer* const* layers, int n_layers, con
                                RmoeScratch& s, int n_cu, hipStream_t st);
 
 // Scratch requirements (bytes) for the launch wrappers above.
-size_t decode_scratch_floats(const RmoeLayer& L);
-size_t decode_scratch_counters(const RmoeLayer& L);
+// The per-stage decode kernels' shape limit: hipSuccess if `slots` slots of layer L fit
+// their LDS (kDecodeMaxLds bytes of dynamic LDS per workgroup).
+constexpr size_t kDecodeMaxLds = 65536;
+hipError_t decode_band_check(const RmoeLayer& L, int slots);
 
 }  // namespace rmoe

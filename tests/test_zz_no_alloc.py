@@ -5,7 +5,7 @@ Called through the C ABI and compared with rmoe_moe_experts_dev (context scratch
 calls in a row, the second on a smaller layer; both share the decode kernels, so the
 outputs are bit-identical, and they match the oracle within the BASELINE bar.  Also:
 replays of a HIP graph that captured it, and the rejection of a layer whose scratch
-exceeds the static array.
+exceeds the static array or whose slots exceed the decode kernels' shape limits.
 """
 
 from __future__ import annotations
@@ -96,15 +96,24 @@ def test_static_scratch_entry_point(gpu_ctx):
 
 
 def test_static_scratch_rejects_oversize(gpu_ctx):
-    """A layer whose decode scratch exceeds the static array is refused before any launch."""
+    """A layer whose decode scratch (the activations of its k slots, 16 x 8448 bf16 here)
+    exceeds the 256 KiB static array is refused before any launch; so is one within the
+    array whose k slots exceed the decode kernels' shape limits (LDS)."""
     import torch
 
-    geom = G.MoeGeometry(hidden=4096, inter=2048, n_routed=16, n_shared=1, top_k=16)
-    lyr = gpu_ctx.create_layer(5104, geom)
-    x = torch.zeros(geom.hidden, dtype=torch.int16, device="cuda")
     ids = torch.arange(16, dtype=torch.int32, device="cuda")
     wts = torch.ones(16, dtype=torch.float32, device="cuda")
+    geom = G.MoeGeometry(hidden=256, inter=8448, n_routed=16, n_shared=1, top_k=16)
+    lyr = gpu_ctx.create_layer(5104, geom)
+    x = torch.zeros(geom.hidden, dtype=torch.int16, device="cuda")
     out = torch.empty_like(x)
     with pytest.raises(ValueError, match="static decode scratch"):
+        _static(lyr, x, ids, wts, out)
+    lyr.free()
+    geom = G.MoeGeometry(hidden=4096, inter=2048, n_routed=16, n_shared=1, top_k=16)
+    lyr = gpu_ctx.create_layer(5105, geom)
+    x = torch.zeros(geom.hidden, dtype=torch.int16, device="cuda")
+    out = torch.empty_like(x)
+    with pytest.raises(ValueError, match="shape limits"):
         _static(lyr, x, ids, wts, out)
     lyr.free()
