@@ -119,15 +119,19 @@ __device__ __forceinline__ void store_split3_planar(uint16_t* dst, int Gp, float
 constexpr int kMaxEFrags = 16;  // E <= 256
 constexpr int kRouterTok = 32;
 
+// Grid (ceil(T / 32), 4): workgroup (b, q) takes tokens 32b.. and the K quarter q; its
+// wave w the sixteenth 4q + w, whose sum runs over 32-column steps in order.  The
+// workgroup adds its waves' sums in wave order and writes the quarter's partial logits
+// plogits[q][t][e]; topk_kernel adds the quarters in order.
 template <int NFR>
 __global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __restrict__ x, int T, int H,
                                                           const uint16_t* __restrict__ w, int E,
-                                                          float* __restrict__ logits) {
+                                                          float* __restrict__ plogits) {
   __shared__ float part[4][kRouterTok][NFR * 16 + 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lq = lane >> 4;
-  const int t0 = blockIdx.x * kRouterTok;
-  const int kq = H / 4, k0 = wave * kq;
+  const int t0 = blockIdx.x * kRouterTok, q = blockIdx.y;
+  const int kq = H / 16, k0 = (4 * q + wave) * kq;
   f32x4_t acc[2][NFR];
 #pragma unroll
   for (int m = 0; m < 2; ++m)
@@ -159,7 +163,8 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __rest
   for (int idx = tid; idx < kRouterTok * E; idx += 256) {
     const int r = idx / E, c = idx % E;
     const int t = t0 + r;
-    if (t < T) logits[(size_t)t * E + c] = ((part[0][r][c] + part[1][r][c]) + part[2][r][c]) + part[3][r][c];
+    if (t < T)
+      plogits[((size_t)q * T + t) * E + c] = ((part[0][r][c] + part[1][r][c]) + part[2][r][c]) + part[3][r][c];
   }
 }
 
@@ -181,7 +186,8 @@ __device__ float np_sum_f32_lds(const float* v, int n) {
   return res;
 }
 
-// One wave per token: scores, selection (score + bias, ties to the lower id), renorm.
+// One wave per token: logits (the four K-quarter partials of router_gemm_kernel, [4][T][E],
+// added in order), scores, selection (score + bias, ties to the lower id), renorm.
 __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int T, int E, int k, int score,
                                                    const float* __restrict__ bias, int renorm, float scaling,
                                                    int32_t* __restrict__ ids, float* __restrict__ wts) {
@@ -190,16 +196,30 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;
-  const float* lg = logits + (size_t)t * E;
+  // Logits: the router GEMM's four K-quarter partials, added in order.
+  const size_t qs = (size_t)T * E;
+  const float* lq0 = logits + (size_t)t * E;
+  float lg[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    lg[i] = e < E ? ((lq0[e] + lq0[qs + e]) + lq0[2 * qs + e]) + lq0[3 * qs + e] : 0.f;
+  }
   float* s = sc[wave];
   if (score == 0) {
-    for (int e = lane; e < E; e += 64) s[e] = 1.0f / (1.0f + expf(-lg[e]));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (lane + 64 * i < E) s[lane + 64 * i] = 1.0f / (1.0f + expf(-lg[i]));
   } else {
     float m = -__builtin_inff();
-    for (int e = lane; e < E; e += 64) m = fmaxf(m, lg[e]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (lane + 64 * i < E) m = fmaxf(m, lg[i]);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    for (int e = lane; e < E; e += 64) s[e] = expf(lg[e] - m);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (lane + 64 * i < E) s[lane + 64 * i] = expf(lg[i] - m);
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     float total = 0.f;
@@ -1345,8 +1365,8 @@ __global__ void h_unify_kernel(uint16_t* __restrict__ h, const int8_t* __restric
 
 // ------------------------------------------------------------------ launchers --
 hipError_t launch_router_gemm(const uint16_t* x, int T, int H, const uint16_t* w, int E, float* logits, hipStream_t st) {
-  if (E % 16 || E > 16 * kMaxEFrags || H % 128) return hipErrorInvalidValue;
-  const dim3 grid((T + kRouterTok - 1) / kRouterTok), block(256);
+  if (E % 16 || E > 16 * kMaxEFrags || H % 512) return hipErrorInvalidValue;
+  const dim3 grid((T + kRouterTok - 1) / kRouterTok, 4), block(256);
   switch (E / 16) {
 #define RMOE_ROUTER_CASE(n) \
   case n:                   \
@@ -1397,7 +1417,7 @@ size_t prefill_scratch_bytes(const RmoeLayer& L, int T) {
          + (size_t)T * L.H * 2                           // xh (fp16 operand)
          + (size_t)T                                     // x exponents
          + (size_t)T * 3 * sum_planes_gp(L.H / 32) * 2   // x group sums
-         + (size_t)T * L.n_routed * 4                    // logits
+         + (size_t)T * L.n_routed * 16                   // router logits, four K-quarter partials
          + kTileClasses * tiles * 4 + 256 * 12;          // tile table, counts, carve rounding
 }
 
@@ -1428,7 +1448,7 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   uint16_t* xh = (uint16_t*)carve((size_t)T * L.H * 2);
   int8_t* xexp = (int8_t*)carve((size_t)T);
   uint16_t* xsum = (uint16_t*)carve((size_t)T * 3 * Gpx * 2);
-  float* logits = (float*)carve((size_t)T * E * 4);
+  float* logits = (float*)carve((size_t)T * E * 16);
   const int tile_cap = (int)(A / kBM + E + T / kBM + 4);
   uint32_t* tiles = (uint32_t*)carve((size_t)kTileClasses * tile_cap * 4);
   int* ntiles = (int*)carve(256);
