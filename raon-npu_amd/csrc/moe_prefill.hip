@@ -185,13 +185,47 @@ __device__ float np_sum_f32_lds(const float* v, int n) {
   for (; i < n; ++i) res = __fadd_rn(res, v[i]);
   return res;
 }
+// The same sum with its 8 partial sums taken by lanes 0..7 of the wave at once (every
+// lane of the wave calls it and gets the result).
+__device__ float np_sum_f32_lds_wave(const float* v, int n) {
+  const int lane = threadIdx.x & 63;
+  if (n < 8) {
+    float r = 0.f;
+    if (lane == 0)
+      for (int i = 0; i < n; ++i) r = __fadd_rn(r, v[i]);
+    return __shfl(r, 0, 64);
+  }
+  const int full = n & ~7;  // elements in whole rows of 8
+  float r = 0.f;
+  if (lane < 8) {
+    r = v[lane];
+    for (int i = 8 + lane; i < full; i += 8) r = __fadd_rn(r, v[i]);
+  }
+  const float r0 = __shfl(r, 0, 64), r1 = __shfl(r, 1, 64), r2 = __shfl(r, 2, 64), r3 = __shfl(r, 3, 64);
+  const float r4 = __shfl(r, 4, 64), r5 = __shfl(r, 5, 64), r6 = __shfl(r, 6, 64), r7 = __shfl(r, 7, 64);
+  float res = __fadd_rn(__fadd_rn(__fadd_rn(r0, r1), __fadd_rn(r2, r3)), __fadd_rn(__fadd_rn(r4, r5), __fadd_rn(r6, r7)));
+  for (int i = full; i < n; ++i) res = __fadd_rn(res, v[i]);
+  return res;
+}
+
+// Order-preserving bits of a float (larger float, larger key); NaN is given the lowest
+// key, so it is never selected ahead of a number (numpy's argsort puts NaN last).
+__device__ __forceinline__ uint32_t float_order_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if (f != f) return 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
 
 // One wave per token: logits (the four K-quarter partials of router_gemm_kernel, [4][T][E],
 // added in order), scores, selection (score + bias, ties to the lower id), renorm.
+// Selection by rank: expert e has key (order bits of its selection score << 8) | (255 - e)
+// and rank #{keys larger than its own}; the experts of rank < k are the top k, in rank
+// order -- the order of repeated arg-max with ties to the lower id.
 __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int T, int E, int k, int score,
                                                    const float* __restrict__ bias, int renorm, float scaling,
                                                    int32_t* __restrict__ ids, float* __restrict__ wts) {
   __shared__ float sc[4][256];
+  __shared__ __attribute__((aligned(16))) uint64_t keys[4][256];
   __shared__ float ch[4][16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
@@ -222,42 +256,39 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
       if (lane + 64 * i < E) s[lane + 64 * i] = expf(lg[i] - m);
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    float total = 0.f;
-    if (lane == 0) total = np_sum_f32_lds(s, E);
-    total = __shfl(total, 0, 64);
+    const float total = np_sum_f32_lds_wave(s, E);
     __builtin_amdgcn_wave_barrier();
-    for (int e = lane; e < E; e += 64) s[e] = s[e] / total;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (lane + 64 * i < E) s[lane + 64 * i] = s[lane + 64 * i] / total;
+  }
+  // Selection keys; keys past E (up to the next even count) are 0 and rank below all.
+  uint64_t key[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    float c = 0.f;
+    if (e < E) c = bias ? __fadd_rn(s[e], bias[e]) : s[e];
+    key[i] = e < E ? ((uint64_t)float_order_key(c) << 8) | (uint64_t)(255 - e) : 0ull;
+    if (e < ((E + 1) & ~1)) keys[wave][e] = key[i];
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  // Candidates of this lane: e = lane + 64*i; taken flags in a lane mask.
-  uint32_t taken = 0u;
-  int chosen_id = 0;
-  for (int r = 0; r < k; ++r) {
-    float best = 0.f;
-    int bid = 0x7fffffff;
-    for (int i = 0; i < 4; ++i) {
-      const int e = lane + 64 * i;
-      if (e < E && !((taken >> i) & 1u)) {
-        const float c = bias ? __fadd_rn(s[e], bias[e]) : s[e];
-        if (bid == 0x7fffffff || c > best) {
-          best = c;
-          bid = e;
-        }
-      }
-    }
+  int rank[4] = {0, 0, 0, 0};
+  const uint4* kv = reinterpret_cast<const uint4*>(keys[wave]);
+  for (int j = 0; j < (E + 1) / 2; ++j) {
+    const uint4 v = kv[j];
+    const uint64_t k0 = (uint64_t)v.x | ((uint64_t)v.y << 32), k1 = (uint64_t)v.z | ((uint64_t)v.w << 32);
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ob = __shfl_xor(best, off, 64);
-      const int oi = __shfl_xor(bid, off, 64);
-      if (oi != 0x7fffffff && (bid == 0x7fffffff || ob > best || (ob == best && oi < bid))) {
-        best = ob;
-        bid = oi;
-      }
+    for (int i = 0; i < 4; ++i) rank[i] += (k0 > key[i] ? 1 : 0) + (k1 > key[i] ? 1 : 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    if (e < E && rank[i] < k) {
+      ids[(size_t)t * k + rank[i]] = e;
+      ch[wave][rank[i]] = s[e];
     }
-    if ((bid & 63) == lane) taken |= 1u << (bid >> 6);
-    if (lane == r) chosen_id = bid;
-    if (lane == 0) ch[wave][r] = s[bid];
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -266,7 +297,6 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
   denom = __shfl(denom, 0, 64);
   if (lane < k) {
     float v = renorm ? ch[wave][lane] / denom : ch[wave][lane];
-    ids[(size_t)t * k + lane] = chosen_id;
     wts[(size_t)t * k + lane] = __fmul_rn(v, scaling);
   }
 }
