@@ -527,6 +527,18 @@ __device__ __forceinline__ void wait_tied(int pending, u32x4v (&c)[2][2]) {
     default: RMOE_WAIT_TIED(0, c); break;
   }
 }
+// Largest of v over the 16 lanes of a DPP row, in every lane of the row: quad swaps, then
+// the half-row and row mirrors (VALU moves, no LDS permute).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_mov<0x141>(v));  // row_half_mirror
+  return fmaxf(v, dpp_mov<0x140>(v));  // row_mirror
+}
 // (x & m) | o in one instruction (the compiler keeps the two-instruction form).
 __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
   uint32_t r;
@@ -978,9 +990,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint32_t* __r
       const int cid = tid + 512 * q, r = cid >> 4, c = cid & 15;
       const bool live = 128 * nt + 8 * c < a.inter;
       const uint4 v = *reinterpret_cast<const uint4*>(stage0 + r * kOutStride + 8 * c);
-      float mx = live ? max_abs_bf16x8(v) : 0.f;
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      const float mx = row16_max(live ? max_abs_bf16x8(v) : 0.f);
       const int ex = f16_exp_chunk(mx);
       if (r < nrows && live)
         *reinterpret_cast<uint4*>(a.out + (size_t)(row0 + r) * a.out_ld + 128 * nt + 8 * c) =
