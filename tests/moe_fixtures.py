@@ -86,27 +86,24 @@ TOL_ABS, TOL_REL = 1e-2, 1e-3
 
 
 def check_bf16(out: np.ndarray, ref: np.ndarray, label: str, same_min: float | None = None) -> dict:
-    """The BASELINE bar, max-abs 1e-2 and rel-L2 1e-3, asserted on every element whose
-    reference value has |ref| < 2.  From |ref| = 2 on, one bf16 ulp (2^-6) exceeds 1e-2,
-    so a single rounding tie that fp32 summation order decides differently moves an
-    element past 1e-2; there the bound is two ulps of the reference value, and such
-    elements are counted and reported separately (``ulp_bounded``).  Returns the figures."""
+    """The BASELINE bar on every element: max-abs 1e-2 and rel-L2 1e-3 against the
+    oracle, and optionally a floor on the fraction of bit-identical bf16 outputs.  Also
+    reports, for elements with |ref| >= 2 (where one bf16 ulp, 2^-6 or more, alone exceeds
+    1e-2), the largest difference in ulps of the reference value.  Returns the figures."""
     from oracle.bf16 import bf16_to_f32
 
     a = bf16_to_f32(out).astype(np.float64)
     b = bf16_to_f32(ref).astype(np.float64)
     d = np.abs(a - b)
-    small = np.abs(b) < 2.0
+    big = np.abs(b) >= 2.0
     rel = float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
     ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(b), 1e-30))) - 7)
-    big_bad = (~small) & (d > TOL_ABS)
-    res = {"max_abs_small": float(d[small].max()) if small.any() else 0.0, "rel_l2": rel,
-           "bit_identical": float(np.mean(out == ref)), "ulp_bounded": int(big_bad.sum()),
-           "n_big": int((~small).sum())}
-    print(f"{label}: max-abs(|ref|<2) {res['max_abs_small']:.3e} rel-L2 {rel:.3e} "
-          f"bit-identical {res['bit_identical']:.4f} ulp-bounded {res['ulp_bounded']}/{res['n_big']}")
-    assert res["max_abs_small"] <= TOL_ABS, (label, res)
-    assert np.all(d[~small] <= 2 * ulp[~small]), (label, res)
+    res = {"max_abs": float(d.max()) if d.size else 0.0, "rel_l2": rel,
+           "bit_identical": float(np.mean(out == ref)), "n_big": int(big.sum()),
+           "max_ulps_big": float((d[big] / ulp[big]).max()) if big.any() else 0.0}
+    print(f"{label}: max-abs {res['max_abs']:.3e} rel-L2 {rel:.3e} bit-identical {res['bit_identical']:.4f} "
+          f"max ulps(|ref|>=2, {res['n_big']} elements) {res['max_ulps_big']:.1f}")
+    assert res["max_abs"] <= TOL_ABS, (label, res)
     assert rel <= TOL_REL, (label, res)
     if same_min is not None:
         assert res["bit_identical"] >= same_min, (label, res)

@@ -26,8 +26,8 @@ MARGIN = 1e-6
 
 
 def _check(out, ref, label, same_min=0.95):
-    """BASELINE bar via check_bf16: max-abs 1e-2 wherever |ref| < 2, two bf16 ulps above
-    (those elements are counted and reported), rel-L2 1e-3, and a floor on bit-identity."""
+    """BASELINE bar via check_bf16: max-abs 1e-2 and rel-L2 1e-3 on every element, and a
+    floor on bit-identity."""
     check_bf16(out, ref, label, same_min)
 
 
@@ -390,7 +390,8 @@ def test_prefill_config5_full_size_properties(baseline):
     (a hot expert takes every token, cold ones a handful).  Size-independent properties:
     a token's output does not depend on the rest of the batch -- a 445-token subset,
     whose groups fall into other tile classes, reproduces the full run's rows bit for bit
-    (routing included) -- and sampled tokens (hot- and cold-expert ones) match the oracle."""
+    (routing included) -- and 40 sampled tokens (the 8 of the coldest experts, the first and
+    last ones and 29 spread over the batch) match the oracle."""
     import torch
 
     import bench
@@ -423,13 +424,18 @@ def test_prefill_config5_full_size_properties(baseline):
         np.testing.assert_array_equal(w2, wts[sub])
         np.testing.assert_array_equal(o2, out[sub])
         zspec = om.RouterSpec(spec.weight_bf16, geom.top_k, score="softmax", bias=bias)
-        rarest = np.argsort(hist[ids].min(axis=1), kind="stable")[:3]  # tokens of the coldest experts
+        rarest = np.argsort(hist[ids].min(axis=1), kind="stable")[:8]  # tokens of the coldest experts
         cold = [int(t) for t in rarest]
-        for t in cold + [0, 1, 2]:
+        spread = [int(t) for t in np.random.default_rng(632).choice(T, 29, replace=False)]
+        checked = []
+        for t in dict.fromkeys(cold + [0, 1, 2, T - 1] + spread):
             if routing_margin(xs[t], zspec) <= MARGIN:
                 continue
             ref, top, _, _ = om.moe_token(bank, zspec, xs[t], None, None, shared_id=geom.shared_id)
             assert sorted(ids[t].tolist()) == sorted(top.tolist()), t
-            _check(out[t:t + 1], ref[None], f"config 5 token {t}")
+            checked.append((t, ref))
+        assert len(checked) >= 30
+        rows = [t for t, _ in checked]
+        _check(out[rows], np.stack([r for _, r in checked]), f"config 5, {len(rows)} sampled tokens")
     finally:
         lyr.set_router(spec.weight_bf16, score="softmax")
