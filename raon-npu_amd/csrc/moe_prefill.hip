@@ -221,6 +221,8 @@ __device__ __forceinline__ uint32_t float_order_key(float f) {
 // Selection by rank: expert e has key (order bits of its selection score << 8) | (255 - e)
 // and rank #{keys larger than its own}; the experts of rank < k are the top k, in rank
 // order -- the order of repeated arg-max with ties to the lower id.
+// NE: experts per lane (E <= 64 * NE).
+template <int NE>
 __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int T, int E, int k, int score,
                                                    const float* __restrict__ bias, int renorm, float scaling,
                                                    int32_t* __restrict__ ids, float* __restrict__ wts) {
@@ -233,39 +235,39 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
   // Logits: the router GEMM's four K-quarter partials, added in order.
   const size_t qs = (size_t)T * E;
   const float* lq0 = logits + (size_t)t * E;
-  float lg[4];
+  float lg[NE];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NE; ++i) {
     const int e = lane + 64 * i;
     lg[i] = e < E ? ((lq0[e] + lq0[qs + e]) + lq0[2 * qs + e]) + lq0[3 * qs + e] : 0.f;
   }
   float* s = sc[wave];
   if (score == 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NE; ++i)
       if (lane + 64 * i < E) s[lane + 64 * i] = 1.0f / (1.0f + expf(-lg[i]));
   } else {
     float m = -__builtin_inff();
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NE; ++i)
       if (lane + 64 * i < E) m = fmaxf(m, lg[i]);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NE; ++i)
       if (lane + 64 * i < E) s[lane + 64 * i] = expf(lg[i] - m);
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     const float total = np_sum_f32_lds_wave(s, E);
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NE; ++i)
       if (lane + 64 * i < E) s[lane + 64 * i] = s[lane + 64 * i] / total;
   }
   // Selection keys; keys past E (up to the next even count) are 0 and rank below all.
-  uint64_t key[4];
+  uint64_t key[NE];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NE; ++i) {
     const int e = lane + 64 * i;
     float c = 0.f;
     if (e < E) c = bias ? __fadd_rn(s[e], bias[e]) : s[e];
@@ -274,16 +276,16 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  int rank[4] = {0, 0, 0, 0};
+  int rank[NE] = {};
   const uint4* kv = reinterpret_cast<const uint4*>(keys[wave]);
   for (int j = 0; j < (E + 1) / 2; ++j) {
     const uint4 v = kv[j];
     const uint64_t k0 = (uint64_t)v.x | ((uint64_t)v.y << 32), k1 = (uint64_t)v.z | ((uint64_t)v.w << 32);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) rank[i] += (k0 > key[i] ? 1 : 0) + (k1 > key[i] ? 1 : 0);
+    for (int i = 0; i < NE; ++i) rank[i] += (k0 > key[i] ? 1 : 0) + (k1 > key[i] ? 1 : 0);
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NE; ++i) {
     const int e = lane + 64 * i;
     if (e < E && rank[i] < k) {
       ids[(size_t)t * k + rank[i]] = e;
@@ -1426,8 +1428,13 @@ hipError_t launch_router_gemm(const uint16_t* x, int T, int H, const uint16_t* w
 hipError_t launch_topk(const float* logits, int T, int E, int k, int score, const float* bias, int renorm,
                        float scaling, int32_t* ids, float* wts, hipStream_t st) {
   if (E > 256 || k > 16 || k > 64) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(topk_kernel, dim3((T + 3) / 4), dim3(256), 0, st, logits, T, E, k, score, bias, renorm, scaling,
-                     ids, wts);
+  const dim3 grid((T + 3) / 4), block(256);
+  if (E <= 64)
+    hipLaunchKernelGGL(topk_kernel<1>, grid, block, 0, st, logits, T, E, k, score, bias, renorm, scaling, ids, wts);
+  else if (E <= 128)
+    hipLaunchKernelGGL(topk_kernel<2>, grid, block, 0, st, logits, T, E, k, score, bias, renorm, scaling, ids, wts);
+  else
+    hipLaunchKernelGGL(topk_kernel<4>, grid, block, 0, st, logits, T, E, k, score, bias, renorm, scaling, ids, wts);
   return hipGetLastError();
 }
 
