@@ -43,7 +43,9 @@ __global__ __launch_bounds__(256) void dispatch_count_kernel(const int32_t* __re
 __global__ __launch_bounds__(256) void dispatch_scatter_kernel(const int32_t* __restrict__ ids, int n, int E,
                                                                const int32_t* __restrict__ counts, int nchunks,
                                                                int32_t* __restrict__ offsets,
-                                                               int32_t* __restrict__ order, int32_t* __restrict__ inv) {
+                                                               int32_t* __restrict__ order, int32_t* __restrict__ inv,
+                                                               uint32_t* __restrict__ tiles, int* __restrict__ ntiles,
+                                                               int cap, int shared_rows) {
   __shared__ int slot[4][256];  // per wave: counts, then next output slot per expert
   __shared__ int wsum[4];
   const int c = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -93,10 +95,11 @@ __global__ __launch_bounds__(256) void dispatch_scatter_kernel(const int32_t* __
   }
   __syncthreads();
   // Expert e's first slot for wave w: offset + earlier chunks + counts of waves 0..w-1.
+  // (Thread E's exclusive prefix is the number of routed rows.)
+  int woff = 0;
+  for (int w = 0; w < wave; ++w) woff += wsum[w];
+  const int offset = woff + incl - total;
   if (tid < E) {
-    int woff = 0;
-    for (int w = 0; w < wave; ++w) woff += wsum[w];
-    const int offset = woff + incl - total;
     if (c == 0) {
       offsets[tid] = offset;
       if (tid == E - 1) offsets[E] = offset + total;
@@ -121,21 +124,30 @@ __global__ __launch_bounds__(256) void dispatch_scatter_kernel(const int32_t* __
     }
     if (same[j] && (same[j] >> lane) == 1ull) slot[wave][e] += __popcll(same[j]);
   }
+  // The grouped GEMM's tile table (when asked for): routed group e holds sorted rows
+  // [offset, offset + total); the shared group (shared_rows > 0) follows them.
+  if (c == 0 && tiles) {
+    __shared__ int tsum[kTileClasses][4];
+    const int ng = E + (shared_rows > 0 ? 1 : 0);
+    tile_table_block<4>(tid, ng, offset, offset + (tid < E ? total : shared_rows), tiles, ntiles, cap, tsum);
+  }
 }
 
 }  // namespace
 
 hipError_t launch_dispatch(const int32_t* ids, int T, int k, int n_experts, int32_t* order, int32_t* inv,
-                           int32_t* offsets, RmoeScratch& s, hipStream_t st) {
+                           int32_t* offsets, RmoeScratch& s, hipStream_t st, uint32_t* tiles, int* ntiles, int cap,
+                           int shared_rows) {
   const int n = T * k;
   const int nchunks = (n + kChunk - 1) / kChunk;
   if (n_experts < 1 || n_experts > 256) return hipErrorInvalidValue;
+  if (tiles && n_experts + (shared_rows > 0 ? 1 : 0) > 256) return hipErrorInvalidValue;
   if ((size_t)nchunks * n_experts > s.chunk_elems) return hipErrorInvalidValue;
   hipLaunchKernelGGL(dispatch_count_kernel, dim3(nchunks), dim3(256), 0, st, ids, n, n_experts, s.chunk_counts, s.err);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nchunks), dim3(256), 0, st, ids, n, n_experts, s.chunk_counts,
-                     nchunks, offsets, order, inv);
+                     nchunks, offsets, order, inv, tiles, ntiles, cap, shared_rows);
   return hipGetLastError();
 }
 

@@ -353,71 +353,22 @@ __global__ __launch_bounds__(256) void prep_x_kernel(const uint16_t* __restrict_
 }
 
 // ----------------------------------------------------------------- tile table --
-// The m-tiles of every group, 128 sorted rows each; group e covers sorted rows
-// [offsets[e], offsets[e+1]) and the extra group n_routed (shared expert) rows
-// [offsets[n_routed], offsets[n_routed] + shared_rows).  A tile is
-// expert | (row_start << 9).  Tiles are listed by class, the number of 16-row fragments
-// that hold rows: class 0 (up to 32 rows: 2 fragments), 1 (up to 64: 4), 2 (8); the
-// grouped GEMM runs each class with that many fragments, so a group's short last tile
-// does no MFMA work on absent rows.  Class c's tiles sit at tiles[c * cap ...] in group
-// order, their count in ntiles[c].
-constexpr int kBM = 128;
-constexpr int kTileClasses = 3;
-__host__ __device__ constexpr int class_fragments(int c) { return c == 0 ? 2 : c == 1 ? 4 : 8; }
-
-// One workgroup of 512 threads; thread e owns group e (routed 0..n_routed-1, shared n_routed).
-// The per-class tile bases are an exclusive prefix over the groups: a 64-lane scan per wave
-// (shuffles), then the wave totals.
+// One workgroup of 512 threads; thread e owns group e (routed 0..n_routed-1, shared
+// n_routed).  (The dispatch scatter builds the same table in its first workgroup when
+// the groups fit its 256 threads; this kernel serves the other cases and the table for
+// a second GEMM with other shared rows.)
 __global__ __launch_bounds__(512) void tile_table_kernel(const int32_t* __restrict__ offsets, int n_routed,
                                                          int shared_rows, uint32_t* __restrict__ tiles,
                                                          int* __restrict__ ntiles, int cap) {
   __shared__ int wsum[kTileClasses][8];
-  const int e = threadIdx.x, lane = e & 63, wave = e >> 6;
+  const int e = threadIdx.x;
   const int ng = n_routed + (shared_rows > 0 ? 1 : 0);
-  int b = 0, full = 0, cnt[kTileClasses] = {0, 0, 0};
+  int b = 0, end = 0;
   if (e < ng) {
     b = offsets[min(e, n_routed)];
-    const int end = e < n_routed ? offsets[e + 1] : b + shared_rows;
-    full = (end - b) / kBM;
-    const int rem = (end - b) % kBM;
-    cnt[2] = full + (rem > 64 ? 1 : 0);
-    cnt[1] = (rem > 32 && rem <= 64) ? 1 : 0;
-    cnt[0] = (rem > 0 && rem <= 32) ? 1 : 0;
+    end = e < n_routed ? offsets[e + 1] : b + shared_rows;
   }
-  int incl[kTileClasses];
-#pragma unroll
-  for (int c = 0; c < kTileClasses; ++c) {
-    int x = cnt[c];
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int y = __shfl_up(x, d, 64);
-      if (lane >= d) x += y;
-    }
-    incl[c] = x;
-    if (lane == 63) wsum[c][wave] = x;
-  }
-  __syncthreads();
-  int base[kTileClasses], total[kTileClasses];
-#pragma unroll
-  for (int c = 0; c < kTileClasses; ++c) {
-    int before = 0, all = 0;
-#pragma unroll
-    for (int w = 0; w < 8; ++w) {
-      const int v = wsum[c][w];
-      before += w < wave ? v : 0;
-      all += v;
-    }
-    base[c] = before + incl[c] - cnt[c];
-    total[c] = all;
-  }
-  for (int i = 0; i < cnt[2]; ++i) {
-    const int slot = base[2] + i;
-    if (slot < cap) tiles[2 * cap + slot] = (uint32_t)e | ((uint32_t)(b + i * kBM) << 9);
-  }
-#pragma unroll
-  for (int c = 0; c < 2; ++c)
-    if (cnt[c] && base[c] < cap) tiles[c * cap + base[c]] = (uint32_t)e | ((uint32_t)(b + full * kBM) << 9);
-  if (e < kTileClasses) ntiles[e] = min(e == 0 ? total[0] : e == 1 ? total[1] : total[2], cap);
+  tile_table_block<8>(e, ng, b, end, tiles, ntiles, cap, wsum);
 }
 
 // ------------------------------------------------------------- grouped GEMM --
@@ -1510,7 +1461,12 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
     ids = ids_out;
     wts = wts_out;
   }
-  err = launch_dispatch(ids, T, k, E, s.order, s.inv, s.offsets, s, st);
+  // The gate/up GEMM's groups: routed, and the shared expert unless its gate/up is given.
+  const int gu_shared_rows = shared_gu ? 0 : T;
+  const bool fused_table = E + (gu_shared_rows > 0 ? 1 : 0) <= 256;
+  err = fused_table ? launch_dispatch(ids, T, k, E, s.order, s.inv, s.offsets, s, st, tiles, ntiles, tile_cap,
+                                      gu_shared_rows)
+                    : launch_dispatch(ids, T, k, E, s.order, s.inv, s.offsets, s, st);
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL(prep_x_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, x, T, L.H, xh, xexp, xsum);
   if ((err = hipGetLastError()) != hipSuccess) return err;
@@ -1540,7 +1496,7 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   g.tiles = tiles;
   g.ntiles = ntiles;
   g.offsets = s.offsets;
-  g.shared_rows = shared_gu ? 0 : T;
+  g.shared_rows = gu_shared_rows;
   g.out = h;
   g.out_ld = L.Ipad;
   g.out_ssum = hsum;
@@ -1548,8 +1504,11 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   g.act = act;
   g.gb = gb;
   g.vb = vb;
-  hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(512), 0, st, s.offsets, E, g.shared_rows, tiles, ntiles, tile_cap);
-  if ((err = hipGetLastError()) != hipSuccess) return err;
+  if (!fused_table) {
+    hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(512), 0, st, s.offsets, E, g.shared_rows, tiles, ntiles,
+                       tile_cap);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+  }
   if (shared_gu) {
     const size_t n = (size_t)T * (L.Ipad / 128);  // waves, 4 per block
     hipLaunchKernelGGL(shared_act_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, shared_gu, T, L.I,

@@ -227,6 +227,69 @@ __device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned n, unsig
   return last;
 }
 
+// ---- grouped GEMM tile table ----
+// The m-tiles of every group of expert-sorted rows, 128 rows each; a tile is
+// group | (row_start << 9).  Tiles are listed by class, the number of 16-row fragments
+// that hold rows: class 0 (up to 32 rows: 2 fragments), 1 (up to 64: 4), 2 (8); the
+// grouped GEMM runs each class with that many fragments, so a group's short last tile
+// does no MFMA work on absent rows.  Class c's tiles sit at tiles[c * cap ...] in group
+// order, their count in ntiles[c].
+constexpr int kBM = 128;
+constexpr int kTileClasses = 3;
+__host__ __device__ constexpr int class_fragments(int c) { return c == 0 ? 2 : c == 1 ? 4 : 8; }
+
+// The tile table built by one workgroup of 64 * NW threads; thread e (e < ng) brings group
+// e's sorted rows [b, end).  The per-class bases are an exclusive prefix over the groups:
+// a 64-lane scan per wave (shuffles), then the wave totals (wsum: kTileClasses x NW ints
+// of LDS).  Every thread of the workgroup calls it (it meets the workgroup once).
+template <int NW>
+__device__ __forceinline__ void tile_table_block(int e, int ng, int b, int end, uint32_t* __restrict__ tiles,
+                                                 int* __restrict__ ntiles, int cap, int (*wsum)[NW]) {
+  const int lane = e & 63, wave = e >> 6;
+  int full = 0, cnt[kTileClasses] = {0, 0, 0};
+  if (e < ng) {
+    full = (end - b) / kBM;
+    const int rem = (end - b) % kBM;
+    cnt[2] = full + (rem > 64 ? 1 : 0);
+    cnt[1] = (rem > 32 && rem <= 64) ? 1 : 0;
+    cnt[0] = (rem > 0 && rem <= 32) ? 1 : 0;
+  }
+  int incl[kTileClasses];
+#pragma unroll
+  for (int c = 0; c < kTileClasses; ++c) {
+    int x = cnt[c];
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(x, d, 64);
+      if (lane >= d) x += y;
+    }
+    incl[c] = x;
+    if (lane == 63) wsum[c][wave] = x;
+  }
+  __syncthreads();
+  int base[kTileClasses], total[kTileClasses];
+#pragma unroll
+  for (int c = 0; c < kTileClasses; ++c) {
+    int before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const int v = wsum[c][w];
+      before += w < wave ? v : 0;
+      all += v;
+    }
+    base[c] = before + incl[c] - cnt[c];
+    total[c] = all;
+  }
+  for (int i = 0; i < cnt[2]; ++i) {
+    const int slot = base[2] + i;
+    if (slot < cap) tiles[2 * cap + slot] = (uint32_t)e | ((uint32_t)(b + i * kBM) << 9);
+  }
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+    if (cnt[c] && base[c] < cap) tiles[c * cap + base[c]] = (uint32_t)e | ((uint32_t)(b + full * kBM) << 9);
+  if (e < kTileClasses) ntiles[e] = min(e == 0 ? total[0] : e == 1 ? total[1] : total[2], cap);
+}
+
 // Wave-wide (64 lanes) sum.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -352,8 +415,12 @@ hipError_t launch_moe_decode(const RmoeLayer& L, const uint16_t* x, const int32_
                              uint16_t* out_routed, RmoeScratch& s, hipStream_t st, int stages = 3, int ntok = 1);
 
 // h[T, Ipad] = RTNE(act(gu[t, :I], gu[t, I:2I])) with zero columns [I, Ipad).
+// With tiles != nullptr the first scatter workgroup also writes the grouped GEMM's tile
+// table for the routed groups plus, when shared_rows > 0, a shared group of that many rows
+// (n_experts + 1 <= 256 groups then).
 hipError_t launch_dispatch(const int32_t* ids, int T, int k, int n_experts, int32_t* order, int32_t* inv,
-                           int32_t* offsets, RmoeScratch& s, hipStream_t st);
+                           int32_t* offsets, RmoeScratch& s, hipStream_t st, uint32_t* tiles = nullptr,
+                           int* ntiles = nullptr, int cap = 0, int shared_rows = 0);
 
 // Prefill MoE (moe_prefill.hip).  With ids_in == nullptr the router runs on the device
 // and writes ids_out/wts_out; otherwise ids_in/wts_in are used.  With shared_gu the
