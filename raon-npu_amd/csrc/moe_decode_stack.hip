@@ -73,7 +73,8 @@ __device__ unsigned long long g_stack_timeline[kTimelineLayers][kTimelineGroups]
 // Stamp points (event index): ready seen 0, x and partial logits summed 1, routing done 2,
 // gate/up unit done 3, h received 4, down tiles in LDS 5, wave 1's down dot products 6,
 // down partials summed 7, d stored 8, combiner holds every d 9, x band stored 10, ready
-// published 11.
+// published 11, first pass of partial logits in LDS 12, selection keys written 13, wave 0's
+// first gate/up tile dot product 14, gate/up waves summed (barrier) 15.
 
 struct StackArgs {
   int L, H, I, Ipad, E, k, S, score, renorm, act, residual;
@@ -347,7 +348,8 @@ __device__ __forceinline__ bool select_fast(const SelectParams a, const float* b
 }
 
 template <int NC>
-__device__ __forceinline__ void select_rank(const SelectParams a, const float* __restrict__ bias, SelectLds& sl) {
+__device__ __forceinline__ void select_rank(const SelectParams a, const float* __restrict__ bias, SelectLds& sl,
+                                            int stamp_l, int stamp_g) {
   static_assert(NC >= 1 && NC <= kMaxE / 64, "64-expert chunks");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int E = a.E, K = a.k;
@@ -395,6 +397,7 @@ __device__ __forceinline__ void select_rank(const SelectParams a, const float* _
     if (lane == 0 && a.S > K) sl.id[K] = E;  // shared expert
   }
   __syncthreads();
+  RMOE_STAMP(stamp_l, stamp_g, 13, 0);
   {
     auto rank_pass = [&](auto QW) {
       constexpr int qw = decltype(QW)::value;  // uint4 words (2 keys each) per quarter
@@ -626,9 +629,9 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     // issued before the first use, so the latencies overlap.
     {
       // x_l: 64-bit loads (tid covers dwords 2*idx, 2*idx+1).  The partial logits
-      // [nb2][Ep] are contiguous: chunks of up to kLRow floats are copied into LDS with
-      // 16-byte loads (the first chunk's loads issued together with x's), then thread e
-      // sums its expert's bands in band order.
+      // [nb2][Ep] are contiguous: passes of up to kLRow floats are copied into LDS with
+      // 16-byte loads (the first pass's loads issued right after x's, before either is
+      // used), then P threads per expert sum its bands.
       uint64_t xv[kMaxH / 4 / kThreads];
 #pragma unroll
       for (int i = 0; i < kMaxH / 4 / kThreads; ++i) {
@@ -637,6 +640,20 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
         if (2 * idx < Hp)
           xv[i] = l == 0 ? reinterpret_cast<const uint64_t*>(a.x0)[idx] : ld_hand_u64(xin + 2 * idx);
       }
+      const int lstride = a.Ep + kLPad;
+      const int nbc = min(kLRow / a.Ep, kLRowLds / lstride);  // bands per pass
+      const int rq = a.Ep / 4;
+      // Two 16-byte pieces per thread and pass (kLRow = 4096 floats); piece j of the pass
+      // is row j / rq of it.
+      static_assert(kLRow / 4 == 2 * kThreads, "two 16-byte pieces per thread");
+      auto load_pass = [&](int b0, uint4& v0, uint4& v1) {
+        const int nf4 = (min(nbc, a.nb2 - b0) * a.Ep) / 4;
+        const uint4* src = reinterpret_cast<const uint4*>(lpart + (size_t)b0 * a.Ep);
+        v0 = tid < nf4 ? src[tid] : make_uint4(0u, 0u, 0u, 0u);
+        v1 = tid + kThreads < nf4 ? src[tid + kThreads] : make_uint4(0u, 0u, 0u, 0u);
+      };
+      uint4 pv0, pv1;
+      load_pass(0, pv0, pv1);
       // x_l into LDS, and the group sums of x_l from the registers: the 32 values of a
       // group are held by 8 neighbouring lanes (4 each), summed in a fixed tree.
 #pragma unroll
@@ -656,31 +673,24 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
           if ((idx & 7) == 0 && 2 * idx < Hp) xsum[idx >> 3] = sv;
         }
       }
-      const int lstride = a.Ep + kLPad;
-      const int nbc = min(kLRow / a.Ep, kLRowLds / lstride);  // bands per pass
       // P threads per expert (neighbouring lanes) sum every P-th band; then a fixed tree.
       const int P = a.E <= 128 ? 4 : 2;
       const int pe = tid / P, pp = tid % P;
       float lacc = 0.f;
       for (int b0 = 0; b0 < a.nb2; b0 += nbc) {
         const int nb = min(nbc, a.nb2 - b0);
-        const int nf4 = (nb * a.Ep) / 4, rq = a.Ep / 4;
-        const uint4* src = reinterpret_cast<const uint4*>(lpart + (size_t)b0 * a.Ep);
-        // Two 16-byte loads per thread (kLRow = 4096 floats), both issued before either
-        // store; piece j of row j / rq goes to the padded row.
-        static_assert(kLRow / 4 == 2 * kThreads, "two 16-byte pieces per thread");
-        const bool h0 = tid < nf4, h1 = tid + kThreads < nf4;
-        const uint4 v0 = h0 ? src[tid] : make_uint4(0u, 0u, 0u, 0u);
-        const uint4 v1 = h1 ? src[tid + kThreads] : make_uint4(0u, 0u, 0u, 0u);
+        const int nf4 = (nb * a.Ep) / 4;
+        if (b0 > 0) load_pass(b0, pv0, pv1);
         // Row of piece j by a float reciprocal, not an integer division: j < 1024 and
         // rq >= 8, so (j + 0.5) / rq stays >= 1/16 away from an integer, far beyond the
         // reciprocal's rounding.
         const float rinv = 1.0f / (float)rq;
         const int j1 = tid + kThreads;
         const int r0 = (int)(((float)tid + 0.5f) * rinv), r1 = (int)(((float)j1 + 0.5f) * rinv);
-        if (h0) *reinterpret_cast<uint4*>(lrow + r0 * lstride + 4 * (tid - r0 * rq)) = v0;
-        if (h1) *reinterpret_cast<uint4*>(lrow + r1 * lstride + 4 * (j1 - r1 * rq)) = v1;
+        if (tid < nf4) *reinterpret_cast<uint4*>(lrow + r0 * lstride + 4 * (tid - r0 * rq)) = pv0;
+        if (j1 < nf4) *reinterpret_cast<uint4*>(lrow + r1 * lstride + 4 * (j1 - r1 * rq)) = pv1;
         __syncthreads();
+        if (b0 == 0) RMOE_STAMP(l, g, 12, 0);
         if (pe < a.E) {
           // Eight of the thread's bands are read at a time (one LDS round trip, not one
           // per band), then added in band order.
@@ -705,7 +715,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     __syncthreads();
     RMOE_STAMP(l, g, 1, 0);
     const SelectParams sp{a.E, a.k, a.S, a.score, a.renorm, a.scaling};
-    select_rank<2 * NIT>(sp, a.rb[l], sl);  // E <= 128 * NIT: at most 2 * NIT chunks of 64
+    select_rank<2 * NIT>(sp, a.rb[l], sl, l, g);  // E <= 128 * NIT: at most 2 * NIT chunks of 64
     RMOE_STAMP(l, g, 2, 0);
 
     // ---- issue every weight load of this workgroup's units for this layer.
@@ -762,6 +772,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     auto gu_unit = [&](int s, int hb) {
       float acc = 0.f;
       if (wave < a.nkt1) acc = tile_dot(mt0, xs + wave * 64, xsum + wave * 4, acc);
+      RMOE_STAMP(l, g, 14, 0);
       if (wave + kWaves < a.nkt1) acc = tile_dot(mt1, xs + (wave + kWaves) * 64, xsum + (wave + kWaves) * 4, acc);
       for (int kt = wave + 2 * kWaves; kt < a.nkt1; kt += kWaves) {
         TileRegs r;
@@ -770,6 +781,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
       }
       red[wave][0][lane] = acc;
       __syncthreads();
+      RMOE_STAMP(l, g, 15, 0);
       if (wave == 0) {
         float gs = 0.f, us = 0.f;
 #pragma unroll

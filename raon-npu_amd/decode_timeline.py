@@ -24,8 +24,12 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 EVENTS = [
     (0, "ready seen"),
+    (12, "first pass of partial logits in LDS"),
     (1, "x and partial logits in LDS, summed"),
+    (13, "selection keys written"),
     (2, "routing done (ranked)"),
+    (14, "first gate/up tile dot product (wave 0)"),
+    (15, "gate/up waves summed (barrier)"),
     (3, "gate/up unit done, h published"),
     (4, "down waves hold their h"),
     (5, "down tiles in LDS"),
