@@ -81,7 +81,8 @@ struct StackArgs {
   float scaling, gb, vb;
   size_t gu_bytes, dn_bytes;
   int nb1, nb2, nkt1, nkt2, nhb, n_gu, n_dn;
-  int Ep;  // n_routed rounded up to 32: row stride of the partial router logits
+  int Ep;      // n_routed rounded up to 32: row stride of the partial router logits
+  int gu_pre;  // 1: a workgroup whose GU unit is in the shared slot copies its tiles into LDS early
   const uint16_t* x0;
   uint16_t* out;
   int32_t* ids_out;  // [L, k] or null
@@ -594,6 +595,28 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
   const uint32_t epoch = epoch_s;
   const uint32_t tag = 2u * epoch + 1u;
 
+  // A GU unit in the shared slot does not depend on the routing: its 2 * nkt1 half tiles
+  // (the unit's 32 gate and 32 up rows of every K tile, 5 KB per K tile) are copied into
+  // the DN tiles' LDS while the workgroup is idle at the end of the previous layer (at
+  // the start for layer 0), and computed as soon as x_l is in LDS, before the routing.
+  // The routed gate/up stream after the routing is then smaller by one slot.  LDS layout:
+  // piece p = 5 kt + j (code pieces j = 0..3, then scale|min) at p KB, lane L's 16 bytes
+  // (lanes 0..31 gate rows, 32..63 up rows, as load_rows reads them) at 16 L.
+  const bool gu_pre = a.gu_pre && gu_d[0] == a.k;
+  auto issue_gu_pre = [&](int ll) {  // waves 1..7
+    if (wave == 0) return;
+    const int hb = gu_d[1];
+    const size_t band = lane < 32 ? (size_t)(hb >> 1) : (size_t)(a.nb1 + (hb >> 1));
+    const uint8_t* base = a.gu[ll] + (size_t)a.E * a.gu_bytes + band * a.nkt1 * kTileBytes +
+                          (size_t)(32 * (hb & 1) + (lane & 31)) * 16;
+    for (int p = wave - 1; p < 5 * a.nkt1; p += kWaves - 1) {
+      const int kt = p / 5, j = p - 5 * kt;
+      __builtin_amdgcn_global_load_lds((global_void_ptr)(base + (size_t)kt * kTileBytes + j * 1024),
+                                       (lds_void_ptr)(dn_lds + (size_t)p * 1024), 16, 0, 0);
+    }
+  };
+  if (gu_pre) issue_gu_pre(0);
+
   // Layer 0: the band share of the router logits of x0 (workgroups b < nb2).
   if (g < a.nb2) {
     if (tid < 32) xband[tid] = reinterpret_cast<const uint32_t*>(a.x0)[32 * g + tid];
@@ -714,6 +737,44 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     }
     __syncthreads();
     RMOE_STAMP(l, g, 1, 0);
+
+    // GU outputs of a unit: the waves' sums in order, then h = RTNE(act(RTNE(g), RTNE(u)))
+    // of its 32 columns, published as 16 tagged words of bf16 pairs.
+    auto gu_publish = [&](int s, int hb, float acc) {
+      red[wave][0][lane] = acc;
+      __syncthreads();
+      RMOE_STAMP(l, g, 15, 0);
+      if (wave == 0) {
+        float gs = 0.f, us = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          gs += red[w][0][lane & 31];
+          us += red[w][0][32 + (lane & 31)];
+        }
+        const uint32_t hb16 = f32_to_bf16(act_apply(a.act, bf16_round(gs), bf16_round(us), a.gb, a.vb));
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hb16, 0xB1, 0xF, 0xF, false);  // lane ^ 1
+        if (lane < 32 && (lane & 1) == 0)
+          st_dev_u64(&hbuf[(size_t)s * hstride + 16 * hb + (lane >> 1)],
+                     (uint64_t)(hb16 | (hi << 16)) | ((uint64_t)tag << 32));
+      }
+    };
+    // The shared-slot GU unit from its tiles in LDS (copied during the previous layer:
+    // every wave's copies have landed, as its later loads have).
+    if (gu_pre) {
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      float acc = 0.f;
+      for (int kt = wave; kt < a.nkt1; kt += kWaves) {
+        TileRegs r;
+        const uint8_t* t = dn_lds + (size_t)kt * kTileBytes + lane * 16;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r.c[j] = *reinterpret_cast<const uint4*>(t + j * 1024);
+        r.sm = *reinterpret_cast<const uint4*>(t + kCodeBytes);
+        acc = tile_dot(r, xs + kt * 64, xsum + kt * 4, acc);
+      }
+      gu_publish(gu_d[0], gu_d[1], acc);  // its barrier also ends every wave's LDS reads
+      RMOE_STAMP(l, g, 3, 0);
+    }
     const SelectParams sp{a.E, a.k, a.S, a.score, a.renorm, a.scaling};
     select_rank<2 * NIT>(sp, a.rb[l], sl, l, g);  // E <= 128 * NIT: at most 2 * NIT chunks of 64
     RMOE_STAMP(l, g, 2, 0);
@@ -732,7 +793,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     };
     TileRegs mt0, mt1;
     {
-      const int s = gu_d[0];
+      const int s = gu_pre ? -1 : gu_d[0];
       const bool ok0 = s >= 0 && wave < a.nkt1, ok1 = s >= 0 && wave + kWaves < a.nkt1;
       load_rows(mt0, ok0, ok0 ? gu_row(s, gu_d[1], wave) : dummy, dummy);
       load_rows(mt1, ok1, ok1 ? gu_row(s, gu_d[1], wave + kWaves) : dummy, dummy);
@@ -753,7 +814,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
                  dn_sink, lane);
       }
     };
-    if (gu_d[0] < 0) issue_dn();
+    if (gu_d[0] < 0 || gu_pre) issue_dn();
     // ---- slot weights and id order (read by the combine, after later barriers), while
     // the weight loads are in flight.
     if (wave == 0) {
@@ -764,11 +825,10 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
       }
     }
 
-    // ---- GU units: g and u of the unit's rows over all of K (waves summed in order), then
-    // h = RTNE(act(RTNE(g), RTNE(u))) of its 32 columns, published as 16 tagged words of
-    // bf16 pairs.  The first unit uses the tiles loaded above (kept out of the loop so the
-    // compiler's wait for them does not also cover the DN loads); any further ones (more
-    // units than workgroups) load on the spot.
+    // ---- GU units: g and u of the unit's rows over all of K, then gu_publish.  The first
+    // unit uses the tiles loaded above (kept out of the loop so the compiler's wait for
+    // them does not also cover the DN loads); any further ones (more units than
+    // workgroups) load on the spot.
     auto gu_unit = [&](int s, int hb) {
       float acc = 0.f;
       if (wave < a.nkt1) acc = tile_dot(mt0, xs + wave * 64, xsum + wave * 4, acc);
@@ -779,24 +839,9 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
         load_rows(r, true, gu_row(s, hb, kt), dummy);
         acc = tile_dot(r, xs + kt * 64, xsum + kt * 4, acc);
       }
-      red[wave][0][lane] = acc;
-      __syncthreads();
-      RMOE_STAMP(l, g, 15, 0);
-      if (wave == 0) {
-        float gs = 0.f, us = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-          gs += red[w][0][lane & 31];
-          us += red[w][0][32 + (lane & 31)];
-        }
-        const uint32_t hb16 = f32_to_bf16(act_apply(a.act, bf16_round(gs), bf16_round(us), a.gb, a.vb));
-        const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hb16, 0xB1, 0xF, 0xF, false);  // lane ^ 1
-        if (lane < 32 && (lane & 1) == 0)
-          st_dev_u64(&hbuf[(size_t)s * hstride + 16 * hb + (lane >> 1)],
-                     (uint64_t)(hb16 | (hi << 16)) | ((uint64_t)tag << 32));
-      }
+      gu_publish(s, hb, acc);
     };
-    if (gu_d[0] >= 0) {
+    if (gu_d[0] >= 0 && !gu_pre) {
       gu_unit(gu_d[0], gu_d[1]);
       RMOE_STAMP(l, g, 3, 0);
       issue_dn();
@@ -1021,6 +1066,11 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
       }
       if (wave > 0) __builtin_amdgcn_s_waitcnt(0);  // router slice copies have landed
     }
+    // The next layer's shared-slot GU tiles, once every wave is done with the LDS.
+    if (gu_pre && l + 1 < a.L) {
+      __syncthreads();
+      issue_gu_pre(l + 1);
+    }
   }
 
   // Every wave's stores and counter updates are complete before the workgroup counts
@@ -1046,12 +1096,17 @@ size_t al256(size_t v) { return (v + 255) / 256 * 256; }
 
 // Dynamic LDS of the kernel: the DN tiles of kMaxDnUnits units plus the 1 KB sink.
 // The same LDS holds the next layer's router slice of the combined band once the DN
-// tiles are consumed (E rounded up to 8 rows of 128 B each).
-size_t dn_lds_bytes(int nkt2, int n_routed) {
-  return std::max((size_t)kMaxDnUnits * nkt2 * kTileBytes + 1024, (size_t)((n_routed + 7) & ~7) * 128);
-}
+// tiles are consumed (E rounded up to 8 rows of 128 B each), and the shared-slot GU
+// tiles between layers.
 constexpr size_t kLdsLimit = 160 * 1024;   // per CU on gfx950
 constexpr size_t kStaticLds = 48 * 1024;   // bound on the kernel's static LDS
+// The shared-slot GU unit's tiles (nkt1 K tiles, 5 KB each) are copied into the same LDS
+// when the layer has a shared slot and they fit.
+bool gu_prefetch_fits(int nkt1) { return (size_t)nkt1 * kTileBytes + kStaticLds <= kLdsLimit; }
+size_t dn_lds_bytes(int nkt2, int n_routed, int nkt1, bool gu_pre) {
+  return std::max({(size_t)kMaxDnUnits * nkt2 * kTileBytes + 1024, (size_t)((n_routed + 7) & ~7) * 128,
+                   gu_pre ? (size_t)nkt1 * kTileBytes : (size_t)0});
+}
 
 StackShape stack_shape(const RmoeLayer& L) {
   StackShape sh{};
@@ -1098,7 +1153,7 @@ size_t stack_counter_count(const RmoeLayer& L, int n_layers) {
 hipError_t stack_check(const RmoeLayer& L, int n_cu) {
   const StackShape sh = stack_shape(L);
   if (L.H > kMaxH || L.n_routed > kMaxE || sh.S > kMaxSlots || kMaxDnUnits * sh.nkt2 > (kWaves - 1) * kMaxDnPos ||
-      L.I % 64 != 0 || dn_lds_bytes(sh.nkt2, L.n_routed) + kStaticLds > kLdsLimit)
+      L.I % 64 != 0 || dn_lds_bytes(sh.nkt2, L.n_routed, sh.nkt1, false) + kStaticLds > kLdsLimit)
     return hipErrorInvalidValue;
 
   if (sh.n_dn > kMaxDnUnits * n_cu || n_cu < sh.nb2) return hipErrorInvalidValue;
@@ -1139,6 +1194,7 @@ hipError_t launch_decode_stack(const RmoeLayer* const* layers, int n_layers, con
   a.n_gu = sh.n_gu;
   a.n_dn = sh.n_dn;
   a.Ep = (L0.n_routed + 31) / 32 * 32;
+  a.gu_pre = sh.S > L0.top_k && gu_prefetch_fits(sh.nkt1) ? 1 : 0;
   a.x0 = x;
   a.out = out;
   a.ids_out = ids_out;
@@ -1162,7 +1218,7 @@ hipError_t launch_decode_stack(const RmoeLayer* const* layers, int n_layers, con
     a.rw[l] = Ll.router_w;
     a.rb[l] = Ll.router_bias;
   }
-  const size_t lds = dn_lds_bytes(sh.nkt2, L0.n_routed);
+  const size_t lds = dn_lds_bytes(sh.nkt2, L0.n_routed, sh.nkt1, a.gu_pre != 0);
   const dim3 grid(n_cu), block(kThreads);
   const int pos_need = (kMaxDnUnits * sh.nkt2 + kWaves - 2) / (kWaves - 1);
   if (pos_need <= 2 && a.E <= 128)
