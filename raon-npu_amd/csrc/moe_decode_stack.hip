@@ -179,7 +179,7 @@ __device__ __forceinline__ unsigned* cnt_at(const StackArgs& a, int l, int i) {
 }
 // `ready` of a layer is kept in kReadyCopies copies: a band publishes to every copy and
 // workgroup g polls copy g % kReadyCopies, so 32 rather than 256 workgroups poll a line.
-constexpr int kReadyCopies = 8;
+constexpr int kReadyCopies = 32;
 __device__ __forceinline__ void publish_ready(const StackArgs& a, int l) {
   for (int c = 0; c < kReadyCopies; ++c)
     __hip_atomic_fetch_add(cnt_at(a, l, c), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -617,6 +617,32 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
   };
   if (gu_pre) issue_gu_pre(0);
 
+  // DN tiles of this workgroup's units, flattened as t = d * nkt2 + kt: wave 1 + t % 7
+  // copies tile t into LDS slot t at its position t / 7.  Units whose bit is clear in
+  // `mask` copy 16 dummy bytes into the sink instead (the same number of loads).  A unit
+  // in the shared slot does not depend on the routing: unless the shared-slot GU tiles
+  // use the same LDS (gu_pre), its tiles are copied at the end of the previous layer (at
+  // the start for layer 0), and only the routed units' tiles after the routing.
+  // (dn_pre: the bits of those units; in LDS like the unit indices.)
+  __shared__ unsigned dn_pre;
+  if (tid == 0)
+    dn_pre = gu_pre || a.S <= a.k ? 0u : (dn_d[0][0] == a.k ? 1u : 0u) | (dn_d[1][0] == a.k ? 2u : 0u);
+  __syncthreads();
+  auto issue_dn_at = [&](const uint8_t* dnb, unsigned mask, int wv, int ln) {
+    const int n_dn_t = (dn_d[0][0] >= 0 ? a.nkt2 : 0) + (dn_d[1][0] >= 0 ? a.nkt2 : 0);
+#pragma unroll
+    for (int p = 0; p < DNPOS; ++p) {
+      const int t = wv - 1 + (kWaves - 1) * p;
+      const bool ok = wv > 0 && t < n_dn_t && ((mask >> (t / a.nkt2)) & 1u);
+      const int d = ok ? t / a.nkt2 : 0, kt = ok ? t % a.nkt2 : 0;
+      const int slot = ok ? dn_d[d][0] : 0;
+      const uint8_t* W = dnb + (size_t)(slot == a.k ? a.E : sl.id[slot]) * a.dn_bytes;
+      dma_tile(ok, W + ((size_t)dn_d[d][1] * a.nkt2 + kt) * kTileBytes, dummy, dn_lds + (size_t)t * kTileBytes,
+               dn_sink, ln);
+    }
+  };
+  if (dn_pre) issue_dn_at(a.dn[0], dn_pre, wave, lane);
+
   // Layer 0: the band share of the router logits of x0 (workgroups b < nb2).
   if (g < a.nb2) {
     if (tid < 32) xband[tid] = reinterpret_cast<const uint32_t*>(a.x0)[32 * g + tid];
@@ -798,23 +824,12 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
       load_rows(mt0, ok0, ok0 ? gu_row(s, gu_d[1], wave) : dummy, dummy);
       load_rows(mt1, ok1, ok1 ? gu_row(s, gu_d[1], wave + kWaves) : dummy, dummy);
     }
-    // DN tiles of both units, flattened as t = d * nkt2 + kt: wave 1 + t % 7 copies tile t
-    // into LDS slot t at its position t / 7.  A workgroup with a GU unit issues them
-    // after its GU tiles have arrived, so the gate/up stream (on the critical path) does
-    // not share HBM with the down stream; the others issue them at once.
+    // The routed DN units' tiles: a workgroup with a GU unit issues them after its GU
+    // tiles have arrived, so the gate/up stream (on the critical path) does not share HBM
+    // with the down stream; the others issue them at once.
     const int n_dn_t = (dn_d[0][0] >= 0 ? a.nkt2 : 0) + (dn_d[1][0] >= 0 ? a.nkt2 : 0);
-    auto issue_dn = [&]() {
-#pragma unroll
-      for (int p = 0; p < DNPOS; ++p) {
-        const int t = wave - 1 + (kWaves - 1) * p;
-        const bool ok = wave > 0 && t < n_dn_t;
-        const int d = ok ? t / a.nkt2 : 0, kt = ok ? t % a.nkt2 : 0;
-        const uint8_t* W = dn_l + (size_t)sl.id[ok ? dn_d[d][0] : 0] * a.dn_bytes;
-        dma_tile(ok, W + ((size_t)dn_d[d][1] * a.nkt2 + kt) * kTileBytes, dummy, dn_lds + (size_t)t * kTileBytes,
-                 dn_sink, lane);
-      }
-    };
-    if (gu_d[0] < 0 || gu_pre) issue_dn();
+    auto issue_dn = [&](const uint8_t* dnb, unsigned mask) { issue_dn_at(dnb, mask, wave, lane); };
+    if (gu_d[0] < 0 || gu_pre) issue_dn(dn_l, 3u & ~dn_pre);
     // ---- slot weights and id order (read by the combine, after later barriers), while
     // the weight loads are in flight.
     if (wave == 0) {
@@ -844,7 +859,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     if (gu_d[0] >= 0 && !gu_pre) {
       gu_unit(gu_d[0], gu_d[1]);
       RMOE_STAMP(l, g, 3, 0);
-      issue_dn();
+      issue_dn(dn_l, 3u & ~dn_pre);
     }
     for (int u = g + G; u < a.n_gu; u += G) {
       const int s = u / a.nhb, hb = u % a.nhb;
@@ -1070,6 +1085,12 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     if (gu_pre && l + 1 < a.L) {
       __syncthreads();
       issue_gu_pre(l + 1);
+    }
+    // The next layer's shared-slot DN tiles, once every wave is done with the LDS (the
+    // DN products, and a combiner's router slice: read before its logits).
+    if (dn_pre && l + 1 < a.L) {
+      __syncthreads();
+      issue_dn(a.dn[l + 1], dn_pre);
     }
   }
 
