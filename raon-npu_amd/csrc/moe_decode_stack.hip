@@ -348,16 +348,18 @@ __device__ __forceinline__ bool select_fast(const SelectParams a, const float* b
   return a.score == 1 && bias == nullptr;
 }
 
+// keys_ready: the caller has already written the keys and the shared slot (the fast path,
+// from the threads that summed the logits) and published them with a barrier.
 template <int NC>
 __device__ __forceinline__ void select_rank(const SelectParams a, const float* __restrict__ bias, SelectLds& sl,
-                                            int stamp_l, int stamp_g) {
+                                            bool keys_ready, int stamp_l, int stamp_g) {
   static_assert(NC >= 1 && NC <= kMaxE / 64, "64-expert chunks");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int E = a.E, K = a.k;
   const int nc = (E + 63) >> 6;     // 64-key chunks; keys in [E, 64*nc) are 0
   const int ncp = nc <= 2 ? 2 : 4;  // the rank pass reads 128 or 256 keys
   const int qkeys = 16 * ncp;       // keys per quarter
-  if (wave == 0) {
+  if (!keys_ready && wave == 0) {
     float sc[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) sc[c] = c < nc && lane + 64 * c < E ? sl.lg[lane + 64 * c] : -__builtin_inff();
@@ -397,7 +399,7 @@ __device__ __forceinline__ void select_rank(const SelectParams a, const float* _
     }
     if (lane == 0 && a.S > K) sl.id[K] = E;  // shared expert
   }
-  __syncthreads();
+  if (!keys_ready) __syncthreads();
   RMOE_STAMP(stamp_l, stamp_g, 13, 0);
   {
     auto rank_pass = [&](auto QW) {
@@ -674,6 +676,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     if (!wait_geq(a, c_ready, (unsigned)a.nb2, &flag)) return;
     RMOE_STAMP(l, g, 0, 0);
 
+    const bool keys_fast = a.score == 1 && a.rb[l] == nullptr;
     // ---- x_l and the routing of this layer.  Every device-scope load of a thread is
     // issued before the first use, so the latencies overlap.
     {
@@ -760,6 +763,15 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
       lacc += dpp_f32<0xB1>(lacc);
       if (P == 4) lacc += dpp_f32<0x4E>(lacc);
       if (pe < a.E && pp == 0) sl.lg[pe] = lacc;
+      // Softmax scores without a bias rank like the logits: the same threads write the
+      // selection keys (padded entries below every key) and the shared slot, and the
+      // barrier below publishes them with the logits.
+      if (keys_fast && pp == 0) {
+        const int ncp = ((a.E + 63) >> 6) <= 2 ? 2 : 4;
+        if (pe < 64 * ncp)
+          sl.key[key_pos(pe, 16 * ncp)] = pe < a.E ? ((uint64_t)order_key(lacc) << 8) | (uint64_t)(255 - pe) : 0ull;
+        if (pe == 0 && a.S > a.k) sl.id[a.k] = a.E;
+      }
     }
     __syncthreads();
     RMOE_STAMP(l, g, 1, 0);
@@ -802,7 +814,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
       RMOE_STAMP(l, g, 3, 0);
     }
     const SelectParams sp{a.E, a.k, a.S, a.score, a.renorm, a.scaling};
-    select_rank<2 * NIT>(sp, a.rb[l], sl, l, g);  // E <= 128 * NIT: at most 2 * NIT chunks of 64
+    select_rank<2 * NIT>(sp, a.rb[l], sl, keys_fast, l, g);  // E <= 128 * NIT: at most 2 * NIT chunks of 64
     RMOE_STAMP(l, g, 2, 0);
 
     // ---- issue every weight load of this workgroup's units for this layer.

@@ -191,6 +191,30 @@ def test_stack_reference_model_shape(gpu_ctx):
         lyr.free()
 
 
+@pytest.mark.parametrize("score,bias_seed", [("softmax", 1850), ("sigmoid", None)], ids=["softmax-bias", "sigmoid"])
+def test_stack_selection_variants(gpu_ctx, score, bias_seed):
+    """The selection keys outside the softmax-without-bias fast path (which ranks logits):
+    softmax scores plus a selection bias, and sigmoid scores without one.  Three layers in one
+    launch equal three chained 1-layer launches bit for bit, and each layer's routing and
+    output match the oracle on the same input."""
+    geom, layers, oracle_layers = _small_stack(gpu_ctx, 3, 1860 if bias_seed else 1880, score=score,
+                                               bias_seed=bias_seed)
+    gpu_ctx.reserve_decode_stack(layers)
+    for t, x in enumerate(random_tokens(3, geom.hidden, 1830)):
+        out, top, _ = gpu_ctx.decode_stack(layers, x, residual=True)
+        h = x
+        for li, (lyr, ol) in enumerate(zip(layers, oracle_layers)):
+            got, ids, _ = lyr.moe_decode(h, residual=True)
+            ref, routes = _oracle_stack([ol], h)
+            if routes[0][1] > MARGIN:
+                assert ids.tolist() == routes[0][0].tolist() == top[li].tolist(), (score, t, li)
+            _check_ulp(got, ref, f"{score} token {t} layer {li}")
+            h = got
+        assert np.array_equal(out, h), f"{score} token {t}: stack differs from chained layers"
+    for lyr in layers:
+        lyr.free()
+
+
 def test_stack_graph_replays_match_eager(gpu_ctx):
     """Captured in a HIP graph: every replay equals an eager launch (counters are cleared by
     the kernel itself, so replays need no memset node)."""
