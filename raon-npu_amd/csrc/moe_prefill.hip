@@ -112,17 +112,19 @@ __device__ __forceinline__ void store_split3_planar(uint16_t* dst, int Gp, float
 
 // ---------------------------------------------------------------- router GEMM --
 // logits[T, E] = x[T, H] . Wr[E, H]^T on MFMA (exact bf16 products, fp32 sums).
-// Block: 32 tokens x all E experts, split over K: wave w takes columns w*H/4..+H/4 and
-// loads its A (token rows) and B (router rows) fragments straight from global memory
-// (the 0.5 MB router stays in L2); the four partial sums meet in LDS and are added in
-// wave order.
+// Block: 32 tokens x up to 64 experts x a quarter of K: wave w takes a sixteenth of the
+// columns and loads its A (token rows) and B (router rows) fragments straight from global
+// memory (the 0.5 MB router stays in L2); the four partial sums meet in LDS and are added
+// in wave order.
 constexpr int kMaxEFrags = 16;  // E <= 256
 constexpr int kRouterTok = 32;
 
-// Grid (ceil(T / 32), 4): workgroup (b, q) takes tokens 32b.. and the K quarter q; its
-// wave w the sixteenth 4q + w, whose sum runs over 32-column steps in order.  The
-// workgroup adds its waves' sums in wave order and writes the quarter's partial logits
-// plogits[q][t][e]; topk_kernel adds the quarters in order.
+// Grid (ceil(T / 32), 4, E / (16 NFR)): workgroup (b, q, c) takes tokens 32b.., the K
+// quarter q and the experts 16 NFR c ..+16 NFR; its wave w the sixteenth 4q + w, whose sum
+// runs over 32-column steps in order.  The workgroup adds its waves' sums in wave order and
+// writes the quarter's partial logits plogits[q][t][e]; topk_kernel adds the quarters in
+// order.  (An expert's sums do not depend on which workgroup holds it, so the split over
+// experts, which gives small batches more workgroups, changes no result.)
 template <int NFR>
 __global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __restrict__ x, int T, int H,
                                                           const uint16_t* __restrict__ w, int E,
@@ -130,7 +132,7 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __rest
   __shared__ float part[4][kRouterTok][NFR * 16 + 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lq = lane >> 4;
-  const int t0 = blockIdx.x * kRouterTok, q = blockIdx.y;
+  const int t0 = blockIdx.x * kRouterTok, q = blockIdx.y, e0 = 16 * NFR * blockIdx.z;
   const int kq = H / 16, k0 = (4 * q + wave) * kq;
   f32x4_t acc[2][NFR];
 #pragma unroll
@@ -140,7 +142,7 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __rest
   const uint16_t* xr[2];
 #pragma unroll
   for (int m = 0; m < 2; ++m) xr[m] = x + (size_t)min(t0 + 16 * m + l16, T - 1) * H + k0 + 8 * lq;
-  const uint16_t* wr = w + (size_t)l16 * H + k0 + 8 * lq;
+  const uint16_t* wr = w + (size_t)(e0 + l16) * H + k0 + 8 * lq;
 #pragma unroll 2
   for (int kk = 0; kk < kq; kk += 32) {
     uint4 a[2], b[NFR];
@@ -160,11 +162,12 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __rest
 #pragma unroll
       for (int i = 0; i < 4; ++i) part[wave][16 * m + 4 * lq + i][16 * f + l16] = acc[m][f][i];
   __syncthreads();
-  for (int idx = tid; idx < kRouterTok * E; idx += 256) {
-    const int r = idx / E, c = idx % E;
+  constexpr int kCols = NFR * 16;
+  for (int idx = tid; idx < kRouterTok * kCols; idx += 256) {
+    const int r = idx / kCols, c = idx % kCols;
     const int t = t0 + r;
     if (t < T)
-      plogits[((size_t)q * T + t) * E + c] = ((part[0][r][c] + part[1][r][c]) + part[2][r][c]) + part[3][r][c];
+      plogits[((size_t)q * T + t) * E + e0 + c] = ((part[0][r][c] + part[1][r][c]) + part[2][r][c]) + part[3][r][c];
   }
 }
 
@@ -1359,16 +1362,15 @@ __global__ void h_unify_kernel(uint16_t* __restrict__ h, const int8_t* __restric
 // ------------------------------------------------------------------ launchers --
 hipError_t launch_router_gemm(const uint16_t* x, int T, int H, const uint16_t* w, int E, float* logits, hipStream_t st) {
   if (E % 16 || E > 16 * kMaxEFrags || H % 512) return hipErrorInvalidValue;
-  const dim3 grid((T + kRouterTok - 1) / kRouterTok, 4), block(256);
-  switch (E / 16) {
+  // Workgroups of up to 64 experts (NFR <= 4), E / 16 NFR of them per (token block, quarter).
+  const int nfr = E / 16 <= 4 ? E / 16 : (E / 16) % 4 == 0 ? 4 : (E / 16) % 3 == 0 ? 3 : (E / 16) % 2 == 0 ? 2 : 1;
+  const dim3 grid((T + kRouterTok - 1) / kRouterTok, 4, (E / 16) / nfr), block(256);
+  switch (nfr) {
 #define RMOE_ROUTER_CASE(n) \
   case n:                   \
     hipLaunchKernelGGL(router_gemm_kernel<n>, grid, block, 0, st, x, T, H, w, E, logits); \
     break;
-    RMOE_ROUTER_CASE(1) RMOE_ROUTER_CASE(2) RMOE_ROUTER_CASE(3) RMOE_ROUTER_CASE(4) RMOE_ROUTER_CASE(5)
-    RMOE_ROUTER_CASE(6) RMOE_ROUTER_CASE(7) RMOE_ROUTER_CASE(8) RMOE_ROUTER_CASE(9) RMOE_ROUTER_CASE(10)
-    RMOE_ROUTER_CASE(11) RMOE_ROUTER_CASE(12) RMOE_ROUTER_CASE(13) RMOE_ROUTER_CASE(14) RMOE_ROUTER_CASE(15)
-    RMOE_ROUTER_CASE(16)
+    RMOE_ROUTER_CASE(1) RMOE_ROUTER_CASE(2) RMOE_ROUTER_CASE(3) RMOE_ROUTER_CASE(4)
 #undef RMOE_ROUTER_CASE
     default:
       return hipErrorInvalidValue;
