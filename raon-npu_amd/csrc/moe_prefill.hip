@@ -126,13 +126,13 @@ constexpr int kRouterTok = 32;
 // order.  (An expert's sums do not depend on which workgroup holds it, so the split over
 // experts, which gives small batches more workgroups, changes no result.)
 template <int NFR>
-__global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __restrict__ x, int T, int H,
-                                                          const uint16_t* __restrict__ w, int E,
-                                                          float* __restrict__ plogits) {
+__device__ __forceinline__ void router_gemm_block(const uint16_t* __restrict__ x, int T, int H,
+                                                  const uint16_t* __restrict__ w, int E, float* __restrict__ plogits,
+                                                  int bx, int by, int bz) {
   __shared__ float part[4][kRouterTok][NFR * 16 + 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lq = lane >> 4;
-  const int t0 = blockIdx.x * kRouterTok, q = blockIdx.y, e0 = 16 * NFR * blockIdx.z;
+  const int t0 = bx * kRouterTok, q = by, e0 = 16 * NFR * bz;
   const int kq = H / 16, k0 = (4 * q + wave) * kq;
   f32x4_t acc[2][NFR];
 #pragma unroll
@@ -219,7 +219,7 @@ __device__ __forceinline__ uint32_t float_order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// One wave per token: logits (the four K-quarter partials of router_gemm_kernel, [4][T][E],
+// One wave per token: logits (the four K-quarter partials of router_gemm_block, [4][T][E],
 // added in order), scores, selection (score + bias, ties to the lower id), renorm.
 // Selection by rank: expert e has key (order bits of its selection score << 8) | (255 - e)
 // and rank #{keys larger than its own}; the experts of rank < k are the top k, in rank
@@ -312,10 +312,9 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
 // group as an exact 3-way bf16 split (planar layout of store_split3_planar).
 // One wave per row; lane L holds the 16-byte chunks L + 64i (K <= 8192).
 constexpr int kPrepMaxChunks = 16;
-__global__ __launch_bounds__(256) void prep_x_kernel(const uint16_t* __restrict__ x, int T, int K,
-                                                     uint16_t* __restrict__ xh, int8_t* __restrict__ xe,
-                                                     uint16_t* __restrict__ xsum) {
-  const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+__device__ __forceinline__ void prep_x_block(const uint16_t* __restrict__ x, int T, int K, uint16_t* __restrict__ xh,
+                                             int8_t* __restrict__ xe, uint16_t* __restrict__ xsum, int bx) {
+  const int lane = threadIdx.x & 63, t = bx * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const int nch = K / 8, G = K / 32, Gp = sum_planes_gp(G);
   const uint4* src = reinterpret_cast<const uint4*>(x + (size_t)t * K);
@@ -353,6 +352,26 @@ __global__ __launch_bounds__(256) void prep_x_kernel(const uint16_t* __restrict_
                           bf16x2_to_f16x2(v[i].w, e));
   }
   if (lane == 0) xe[t] = (int8_t)e;
+}
+__global__ __launch_bounds__(256) void prep_x_kernel(const uint16_t* __restrict__ x, int T, int K,
+                                                     uint16_t* __restrict__ xh, int8_t* __restrict__ xe,
+                                                     uint16_t* __restrict__ xsum) {
+  prep_x_block(x, T, K, xh, xe, xsum, blockIdx.x);
+}
+// The router GEMM and the activation-row preparation (both read only x) in one launch:
+// workgroups 0..n_router-1 are router workgroups (token block, K quarter, expert group),
+// the rest prepare four rows each.  One launch fewer on the routing's critical path.
+template <int NFR>
+__global__ __launch_bounds__(256) void router_prep_kernel(const uint16_t* __restrict__ x, int T, int H,
+                                                          const uint16_t* __restrict__ w, int E,
+                                                          float* __restrict__ plogits, int n_router, int ngroups,
+                                                          uint16_t* __restrict__ xh, int8_t* __restrict__ xe,
+                                                          uint16_t* __restrict__ xsum) {
+  const int b = blockIdx.x;
+  if (b < n_router)
+    router_gemm_block<NFR>(x, T, H, w, E, plogits, b / (4 * ngroups), (b / ngroups) % 4, b % ngroups);
+  else
+    prep_x_block(x, T, H, xh, xe, xsum, b - n_router);
 }
 
 // ----------------------------------------------------------------- tile table --
@@ -1360,15 +1379,20 @@ __global__ void h_unify_kernel(uint16_t* __restrict__ h, const int8_t* __restric
 }  // namespace
 
 // ------------------------------------------------------------------ launchers --
-hipError_t launch_router_gemm(const uint16_t* x, int T, int H, const uint16_t* w, int E, float* logits, hipStream_t st) {
-  if (E % 16 || E > 16 * kMaxEFrags || H % 512) return hipErrorInvalidValue;
-  // Workgroups of up to 64 experts (NFR <= 4), E / 16 NFR of them per (token block, quarter).
+hipError_t launch_router_prep(const uint16_t* x, int T, int H, const uint16_t* w, int E, float* logits,
+                              uint16_t* xh, int8_t* xe, uint16_t* xsum, hipStream_t st) {
+  if (E % 16 || E > 16 * kMaxEFrags || H % 512 || H / 8 > 64 * kPrepMaxChunks) return hipErrorInvalidValue;
+  // Workgroups of up to 64 experts (NFR <= 4), E / 16 NFR of them per (token block, quarter),
+  // then the preparation workgroups of four rows.
   const int nfr = E / 16 <= 4 ? E / 16 : (E / 16) % 4 == 0 ? 4 : (E / 16) % 3 == 0 ? 3 : (E / 16) % 2 == 0 ? 2 : 1;
-  const dim3 grid((T + kRouterTok - 1) / kRouterTok, 4, (E / 16) / nfr), block(256);
+  const int ngroups = (E / 16) / nfr;
+  const int n_router = (T + kRouterTok - 1) / kRouterTok * 4 * ngroups;
+  const dim3 grid((unsigned)(n_router + (T + 3) / 4)), block(256);
   switch (nfr) {
-#define RMOE_ROUTER_CASE(n) \
-  case n:                   \
-    hipLaunchKernelGGL(router_gemm_kernel<n>, grid, block, 0, st, x, T, H, w, E, logits); \
+#define RMOE_ROUTER_CASE(n)                                                                                   \
+  case n:                                                                                                     \
+    hipLaunchKernelGGL(router_prep_kernel<n>, grid, block, 0, st, x, T, H, w, E, logits, n_router, ngroups, xh, xe, \
+                       xsum);                                                                                 \
     break;
     RMOE_ROUTER_CASE(1) RMOE_ROUTER_CASE(2) RMOE_ROUTER_CASE(3) RMOE_ROUTER_CASE(4)
 #undef RMOE_ROUTER_CASE
@@ -1456,12 +1480,16 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   const int32_t* ids = ids_in;
   const float* wts = wts_in;
   if (!ids_in) {
-    err = launch_router_gemm(x, T, L.H, L.router_w, E, logits, st);
+    // The router GEMM launch also prepares the activation rows.
+    err = launch_router_prep(x, T, L.H, L.router_w, E, logits, xh, xexp, xsum, st);
     if (err != hipSuccess) return err;
     err = launch_topk(logits, T, E, k, L.score, L.router_bias, L.renorm, L.scaling, ids_out, wts_out, st);
     if (err != hipSuccess) return err;
     ids = ids_out;
     wts = wts_out;
+  } else {
+    hipLaunchKernelGGL(prep_x_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, x, T, L.H, xh, xexp, xsum);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
   }
   // The gate/up GEMM's groups: routed, and the shared expert unless its gate/up is given.
   const int gu_shared_rows = shared_gu ? 0 : T;
@@ -1470,8 +1498,6 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
                                       gu_shared_rows)
                     : launch_dispatch(ids, T, k, E, s.order, s.inv, s.offsets, s, st);
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL(prep_x_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, x, T, L.H, xh, xexp, xsum);
-  if ((err = hipGetLastError()) != hipSuccess) return err;
   if (L.Ipad > L.I) {
     // h columns past I (their group sums and chunk exponents) feed the zero-padded down
     // columns.

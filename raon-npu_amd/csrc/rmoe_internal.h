@@ -432,8 +432,10 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
                               bool residual, uint16_t* out, uint16_t* routed, uint16_t* shared_down, uint8_t* scratch,
                               size_t scratch_bytes, RmoeScratch& s, hipStream_t st);
 // Prefill router: logits as four K-quarter partials [4][T][E] (H % 512 == 0), which
-// launch_topk adds in order.
-hipError_t launch_router_gemm(const uint16_t* x, int T, int H, const uint16_t* w, int E, float* logits, hipStream_t st);
+// launch_topk adds in order; the same launch prepares the activation rows of the grouped
+// GEMM (xh, xe, xsum; see moe_prefill.hip).
+hipError_t launch_router_prep(const uint16_t* x, int T, int H, const uint16_t* w, int E, float* logits,
+                              uint16_t* xh, int8_t* xe, uint16_t* xsum, hipStream_t st);
 hipError_t launch_topk(const float* logits, int T, int E, int k, int score, const float* bias, int renorm,
                        float scaling, int32_t* ids, float* wts, hipStream_t st);
 
