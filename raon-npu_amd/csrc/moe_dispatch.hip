@@ -13,7 +13,7 @@
 namespace rmoe {
 namespace {
 
-constexpr int kChunk = 1024;
+constexpr int kChunk = kDispatchChunk;
 
 __global__ __launch_bounds__(256) void dispatch_count_kernel(const int32_t* __restrict__ ids, int n, int E,
                                                              int32_t* __restrict__ counts, int* err) {
@@ -137,15 +137,18 @@ __global__ __launch_bounds__(256) void dispatch_scatter_kernel(const int32_t* __
 
 hipError_t launch_dispatch(const int32_t* ids, int T, int k, int n_experts, int32_t* order, int32_t* inv,
                            int32_t* offsets, RmoeScratch& s, hipStream_t st, uint32_t* tiles, int* ntiles, int cap,
-                           int shared_rows) {
+                           int shared_rows, bool counted) {
   const int n = T * k;
   const int nchunks = (n + kChunk - 1) / kChunk;
   if (n_experts < 1 || n_experts > 256) return hipErrorInvalidValue;
   if (tiles && n_experts + (shared_rows > 0 ? 1 : 0) > 256) return hipErrorInvalidValue;
   if ((size_t)nchunks * n_experts > s.chunk_elems) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(dispatch_count_kernel, dim3(nchunks), dim3(256), 0, st, ids, n, n_experts, s.chunk_counts, s.err);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (!counted) {
+    hipLaunchKernelGGL(dispatch_count_kernel, dim3(nchunks), dim3(256), 0, st, ids, n, n_experts, s.chunk_counts,
+                       s.err);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nchunks), dim3(256), 0, st, ids, n, n_experts, s.chunk_counts,
                      nchunks, offsets, order, inv, tiles, ntiles, cap, shared_rows);
   return hipGetLastError();

@@ -225,16 +225,27 @@ __device__ __forceinline__ uint32_t float_order_key(float f) {
 // and rank #{keys larger than its own}; the experts of rank < k are the top k, in rank
 // order -- the order of repeated arg-max with ties to the lower id.
 // NE: experts per lane (E <= 64 * NE).
+// counts (may be null): the dispatch chunk counts [chunk][E] (zero on entry), to which the
+// workgroup adds its assignments, 4 tokens' k routes at most spanning two chunks, counted in
+// LDS first and then added once per (chunk, expert).
 template <int NE>
 __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int T, int E, int k, int score,
                                                    const float* __restrict__ bias, int renorm, float scaling,
-                                                   int32_t* __restrict__ ids, float* __restrict__ wts) {
+                                                   int32_t* __restrict__ ids, float* __restrict__ wts,
+                                                   int32_t* __restrict__ counts) {
   __shared__ float sc[4][256];
   __shared__ __attribute__((aligned(16))) uint64_t keys[4][256];
   __shared__ float ch[4][16];
+  __shared__ int hist[2][256];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
-  if (t >= T) return;
+  const int cbase = blockIdx.x * 4 * k / kDispatchChunk;
+  if (counts) {
+    hist[0][threadIdx.x] = 0;
+    hist[1][threadIdx.x] = 0;
+    __syncthreads();
+  }
+  if (t < T) {
   // Logits: the router GEMM's four K-quarter partials, added in order.
   const size_t qs = (size_t)T * E;
   const float* lq0 = logits + (size_t)t * E;
@@ -293,6 +304,7 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
     if (e < E && rank[i] < k) {
       ids[(size_t)t * k + rank[i]] = e;
       ch[wave][rank[i]] = s[e];
+      if (counts) atomicAdd(&hist[(t * k + rank[i]) / kDispatchChunk - cbase][e], 1);
     }
   }
   __builtin_amdgcn_wave_barrier();
@@ -303,6 +315,18 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
   if (lane < k) {
     float v = renorm ? ch[wave][lane] / denom : ch[wave][lane];
     wts[(size_t)t * k + lane] = __fmul_rn(v, scaling);
+  }
+  }
+  if (counts) {
+    __syncthreads();
+    const int nch = (T * k + kDispatchChunk - 1) / kDispatchChunk;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int v = hist[c][threadIdx.x];
+      if (v && (int)threadIdx.x < E && cbase + c < nch)
+        __hip_atomic_fetch_add(&counts[(size_t)(cbase + c) * E + threadIdx.x], v, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -366,12 +390,17 @@ __global__ __launch_bounds__(256) void router_prep_kernel(const uint16_t* __rest
                                                           const uint16_t* __restrict__ w, int E,
                                                           float* __restrict__ plogits, int n_router, int ngroups,
                                                           uint16_t* __restrict__ xh, int8_t* __restrict__ xe,
-                                                          uint16_t* __restrict__ xsum) {
+                                                          uint16_t* __restrict__ xsum, int32_t* __restrict__ zero,
+                                                          int nzero) {
   const int b = blockIdx.x;
-  if (b < n_router)
+  if (b < n_router) {
     router_gemm_block<NFR>(x, T, H, w, E, plogits, b / (4 * ngroups), (b / ngroups) % 4, b % ngroups);
-  else
-    prep_x_block(x, T, H, xh, xe, xsum, b - n_router);
+  } else {
+    // The preparation workgroups also clear nzero ints at zero (the top-k's chunk counts).
+    const int pb = b - n_router;
+    for (int i = pb * 256 + (int)threadIdx.x; i < nzero; i += (gridDim.x - n_router) * 256) zero[i] = 0;
+    prep_x_block(x, T, H, xh, xe, xsum, pb);
+  }
 }
 
 // ----------------------------------------------------------------- tile table --
@@ -1380,7 +1409,7 @@ __global__ void h_unify_kernel(uint16_t* __restrict__ h, const int8_t* __restric
 
 // ------------------------------------------------------------------ launchers --
 hipError_t launch_router_prep(const uint16_t* x, int T, int H, const uint16_t* w, int E, float* logits,
-                              uint16_t* xh, int8_t* xe, uint16_t* xsum, hipStream_t st) {
+                              uint16_t* xh, int8_t* xe, uint16_t* xsum, int32_t* zero, int nzero, hipStream_t st) {
   if (E % 16 || E > 16 * kMaxEFrags || H % 512 || H / 8 > 64 * kPrepMaxChunks) return hipErrorInvalidValue;
   // Workgroups of up to 64 experts (NFR <= 4), E / 16 NFR of them per (token block, quarter),
   // then the preparation workgroups of four rows.
@@ -1392,7 +1421,7 @@ hipError_t launch_router_prep(const uint16_t* x, int T, int H, const uint16_t* w
 #define RMOE_ROUTER_CASE(n)                                                                                   \
   case n:                                                                                                     \
     hipLaunchKernelGGL(router_prep_kernel<n>, grid, block, 0, st, x, T, H, w, E, logits, n_router, ngroups, xh, xe, \
-                       xsum);                                                                                 \
+                       xsum, zero, nzero);                                                                    \
     break;
     RMOE_ROUTER_CASE(1) RMOE_ROUTER_CASE(2) RMOE_ROUTER_CASE(3) RMOE_ROUTER_CASE(4)
 #undef RMOE_ROUTER_CASE
@@ -1403,15 +1432,19 @@ hipError_t launch_router_prep(const uint16_t* x, int T, int H, const uint16_t* w
 }
 
 hipError_t launch_topk(const float* logits, int T, int E, int k, int score, const float* bias, int renorm,
-                       float scaling, int32_t* ids, float* wts, hipStream_t st) {
+                       float scaling, int32_t* ids, float* wts, int32_t* counts, hipStream_t st) {
   if (E > 256 || k > 16 || k > 64) return hipErrorInvalidValue;
+  static_assert(4 * 16 <= kDispatchChunk, "a workgroup's assignments span at most two chunks");
   const dim3 grid((T + 3) / 4), block(256);
   if (E <= 64)
-    hipLaunchKernelGGL(topk_kernel<1>, grid, block, 0, st, logits, T, E, k, score, bias, renorm, scaling, ids, wts);
+    hipLaunchKernelGGL(topk_kernel<1>, grid, block, 0, st, logits, T, E, k, score, bias, renorm, scaling, ids, wts,
+                       counts);
   else if (E <= 128)
-    hipLaunchKernelGGL(topk_kernel<2>, grid, block, 0, st, logits, T, E, k, score, bias, renorm, scaling, ids, wts);
+    hipLaunchKernelGGL(topk_kernel<2>, grid, block, 0, st, logits, T, E, k, score, bias, renorm, scaling, ids, wts,
+                       counts);
   else
-    hipLaunchKernelGGL(topk_kernel<4>, grid, block, 0, st, logits, T, E, k, score, bias, renorm, scaling, ids, wts);
+    hipLaunchKernelGGL(topk_kernel<4>, grid, block, 0, st, logits, T, E, k, score, bias, renorm, scaling, ids, wts,
+                       counts);
   return hipGetLastError();
 }
 
@@ -1479,11 +1512,17 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   hipError_t err;
   const int32_t* ids = ids_in;
   const float* wts = wts_in;
+  // With the routing on the device, the router GEMM launch also prepares the activation
+  // rows and clears the dispatch chunk counts, which the top-k then adds up (no count
+  // kernel).
+  const int nchunks = (int)((A + kDispatchChunk - 1) / kDispatchChunk);
+  const bool counted = !ids_in && (size_t)nchunks * E <= s.chunk_elems;
   if (!ids_in) {
-    // The router GEMM launch also prepares the activation rows.
-    err = launch_router_prep(x, T, L.H, L.router_w, E, logits, xh, xexp, xsum, st);
+    err = launch_router_prep(x, T, L.H, L.router_w, E, logits, xh, xexp, xsum, counted ? s.chunk_counts : nullptr,
+                             counted ? nchunks * E : 0, st);
     if (err != hipSuccess) return err;
-    err = launch_topk(logits, T, E, k, L.score, L.router_bias, L.renorm, L.scaling, ids_out, wts_out, st);
+    err = launch_topk(logits, T, E, k, L.score, L.router_bias, L.renorm, L.scaling, ids_out, wts_out,
+                      counted ? s.chunk_counts : nullptr, st);
     if (err != hipSuccess) return err;
     ids = ids_out;
     wts = wts_out;
@@ -1495,8 +1534,8 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   const int gu_shared_rows = shared_gu ? 0 : T;
   const bool fused_table = E + (gu_shared_rows > 0 ? 1 : 0) <= 256;
   err = fused_table ? launch_dispatch(ids, T, k, E, s.order, s.inv, s.offsets, s, st, tiles, ntiles, tile_cap,
-                                      gu_shared_rows)
-                    : launch_dispatch(ids, T, k, E, s.order, s.inv, s.offsets, s, st);
+                                      gu_shared_rows, counted)
+                    : launch_dispatch(ids, T, k, E, s.order, s.inv, s.offsets, s, st, nullptr, nullptr, 0, 0, counted);
   if (err != hipSuccess) return err;
   if (L.Ipad > L.I) {
     // h columns past I (their group sums and chunk exponents) feed the zero-padded down

@@ -415,12 +415,17 @@ hipError_t launch_moe_decode(const RmoeLayer& L, const uint16_t* x, const int32_
                              uint16_t* out_routed, RmoeScratch& s, hipStream_t st, int stages = 3, int ntok = 1);
 
 // h[T, Ipad] = RTNE(act(gu[t, :I], gu[t, I:2I])) with zero columns [I, Ipad).
+// Assignments per dispatch chunk (per workgroup of the count and scatter kernels); the
+// chunk counts are counts[chunk][expert].
+constexpr int kDispatchChunk = 1024;
+// With counted, counts[][] already hold the chunk counts (the prefill top-k adds them) and
+// the count kernel is skipped.
 // With tiles != nullptr the first scatter workgroup also writes the grouped GEMM's tile
 // table for the routed groups plus, when shared_rows > 0, a shared group of that many rows
 // (n_experts + 1 <= 256 groups then).
 hipError_t launch_dispatch(const int32_t* ids, int T, int k, int n_experts, int32_t* order, int32_t* inv,
                            int32_t* offsets, RmoeScratch& s, hipStream_t st, uint32_t* tiles = nullptr,
-                           int* ntiles = nullptr, int cap = 0, int shared_rows = 0);
+                           int* ntiles = nullptr, int cap = 0, int shared_rows = 0, bool counted = false);
 
 // Prefill MoE (moe_prefill.hip).  With ids_in == nullptr the router runs on the device
 // and writes ids_out/wts_out; otherwise ids_in/wts_in are used.  With shared_gu the
@@ -435,9 +440,11 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
 // launch_topk adds in order; the same launch prepares the activation rows of the grouped
 // GEMM (xh, xe, xsum; see moe_prefill.hip).
 hipError_t launch_router_prep(const uint16_t* x, int T, int H, const uint16_t* w, int E, float* logits,
-                              uint16_t* xh, int8_t* xe, uint16_t* xsum, hipStream_t st);
+                              uint16_t* xh, int8_t* xe, uint16_t* xsum, int32_t* zero, int nzero, hipStream_t st);
+// counts (may be null): the dispatch chunk counts [chunk][E], zero on entry, to which the
+// selected assignments are added.
 hipError_t launch_topk(const float* logits, int T, int E, int k, int score, const float* bias, int renorm,
-                       float scaling, int32_t* ids, float* wts, hipStream_t st);
+                       float scaling, int32_t* ids, float* wts, int32_t* counts, hipStream_t st);
 
 // Persistent decode of n_layers (<= kMaxStack) layers of one geometry for one token
 // (moe_decode_stack.hip).  One workgroup per CU (grid n_cu).  ids_out/wts_out: [n_layers, k]
