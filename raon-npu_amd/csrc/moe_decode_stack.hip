@@ -1047,7 +1047,11 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
             __builtin_amdgcn_s_sleep(1);
           }
         }
-        if (__syncthreads_or(cfailed ? 1 : 0)) return;
+        // A barrier that waits for LDS only: waves 1..7 still have the router slice in
+        // flight, which the combine does not read (they drain it before the logits).
+        if (wave == 0 && lane == 0) flag = cfailed ? 1u : 0u;
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (flag != 0u) return;
         RMOE_STAMP(l, g, 9, 0);
         if (wave == 0) {
           // Ascending expert id: the slot order, then each slot's value and weight, read
@@ -1081,7 +1085,9 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
         }
         if (l + 1 < a.L) {
           if (wave > 0) __builtin_amdgcn_s_waitcnt(0);  // the router slice is in LDS
-          __syncthreads();
+          // Again for LDS only (xband): wave 0's x stores stay in flight while the logits
+          // are computed; block_publish_ready waits for them before ready is counted.
+          asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
           float* lnext = reinterpret_cast<float*>(lay + a.layer_bytes + a.off_lpart);
           uint4 rwv[NIT][2];
           RMOE_STAMP(l, g, 10, 0);
