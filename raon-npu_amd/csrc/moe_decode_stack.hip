@@ -137,14 +137,15 @@ typedef __attribute__((address_space(1))) void* global_void_ptr;
 // Direct global -> LDS copy of one tile by one wave (five 1 KB pieces; lane L moves
 // bytes [16L, 16L+16) of each piece).  Invalid tiles copy 16 bytes of `dummy` into the
 // 1 KB `sink` instead, so the number of loads does not depend on validity.  The data is
-// in LDS once the wave's vmcnt has drained.
+// in LDS once the wave's vmcnt has drained.  The copies carry the non-temporal hint: each
+// DN tile is read once per layer.
 __device__ __forceinline__ void dma_tile(bool valid, const uint8_t* tile, const uint8_t* dummy, uint8_t* lds_tile,
                                          uint8_t* sink, int lane) {
 #pragma unroll
   for (int j = 0; j < 5; ++j) {
     const uint8_t* src = valid ? tile + j * 1024 + lane * 16 : dummy;
     uint8_t* dst = valid ? lds_tile + j * 1024 : sink;
-    __builtin_amdgcn_global_load_lds((global_void_ptr)src, (lds_void_ptr)dst, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((global_void_ptr)src, (lds_void_ptr)dst, 16, 0, 2 /* nt */);
   }
 }
 

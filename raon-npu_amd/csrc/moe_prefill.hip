@@ -490,6 +490,20 @@ __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
       : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
       : "memory");
 }
+// dma16 with the non-temporal hint, for the weight tiles: each is copied by one tile of
+// the GEMM (the m-tiles of an expert share them only through L2, close in time), so
+// they should not push out the activation rows, which every N-tile of an m-tile reads.
+__device__ __forceinline__ void dma16_nt(const void* g, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %1, off nt\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+      : "memory");
+}
 // A 16-byte global load the compiler does not count: its result may be used only after
 // a wait_tied() on it (compiler-counted loads would make the compiler wait for every
 // copy issued after them).
@@ -646,7 +660,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint32_t* __r
     for (int i = 0; i < 3; ++i) {
       if (i < n_wcopy) {
         const int v = wave + 8 * i, t = v / 5, p = v % 5;
-        dma16(wg[i] + (size_t)kt * kTileBytes, sb + (uint32_t)(kXBytes + t * kTileBytes + 1024 * p));
+        dma16_nt(wg[i] + (size_t)kt * kTileBytes, sb + (uint32_t)(kXBytes + t * kTileBytes + 1024 * p));
       }
     }
   };
@@ -1095,8 +1109,8 @@ __device__ __forceinline__ void gemm_tile_b16(const GemmArgs& a, const uint32_t*
     for (int i = 0; i < 5; ++i) {
       if (i < n_wcopy) {
         const int v = wave + 8 * i, t = v / 9, p = v % 9;
-        dma16(W + ((size_t)(4 * nt + t) * nkt + kt) * kB16TileBytes + 1024 * p + 16 * lane,
-              sb + (uint32_t)(kXBytes + t * kB16TileBytes + 1024 * p));
+        dma16_nt(W + ((size_t)(4 * nt + t) * nkt + kt) * kB16TileBytes + 1024 * p + 16 * lane,
+                 sb + (uint32_t)(kXBytes + t * kB16TileBytes + 1024 * p));
       }
     }
   };
