@@ -454,6 +454,9 @@ struct GemmArgs {
   // bfp16 weights (down of a weights-d layer): per expert and weight row the largest
   // max(e, 7) of the row's blocks ([experts][N_total]).
   const uint8_t* rowexp;
+  // mode 1: D rows are stored with the non-temporal hint (a large D, read once by the
+  // combine, then stays out of the caches the GEMM reuses weights and rows from).
+  int out_nt;
 };
 
 __device__ __forceinline__ int group_end(const GemmArgs& a, int e) {
@@ -1037,9 +1040,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint32_t* __r
     for (int q = 0; q < 8; ++q) {
       const int cid = tid + 512 * q, r = cid >> 5, c = cid & 31;
       const uint16_t* st = stage0 + (c >> 4) * (kStageBytes / 2);
-      if (r < nrows)
-        *reinterpret_cast<uint4*>(a.out + (size_t)(row0 + r) * a.out_ld + 256 * nt + 8 * c) =
-            *reinterpret_cast<const uint4*>(st + r * kOutStride + 8 * (c & 15));
+      if (r < nrows) {
+        const uint4 v = *reinterpret_cast<const uint4*>(st + r * kOutStride + 8 * (c & 15));
+        uint16_t* dst = a.out + (size_t)(row0 + r) * a.out_ld + 256 * nt + 8 * c;
+        if (a.out_nt)
+          __builtin_nontemporal_store(u32x4v{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4v*>(dst));
+        else
+          *reinterpret_cast<uint4*>(dst) = v;
+      }
     }
   }
 }
@@ -1621,6 +1629,10 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   d.out_ssum = nullptr;
   d.out_exp = nullptr;
   d.rowexp = L.dn_rowexp;
+  // Non-temporal D stores pay off when D is large: 0.948 -> 0.940 ms at 6,700 tokens
+  // (247 MB of D), but 0.170 -> 0.171 ms at 445 tokens (16 MB), where the combine finds
+  // more of D in the caches.
+  d.out_nt = R * (size_t)L.H * 2 > ((size_t)64 << 20) ? 1 : 0;
   if ((err = launch_grouped(d, tiles, ntiles, tile_cap, E, st, L.dn_fmt == RMOE_FMT_BFP16)) != hipSuccess) return err;
   hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, st, D, L.H, ids, wts, s.inv, k, (int)A,
                      residual ? x : nullptr, out, routed, shared_down, 1);
