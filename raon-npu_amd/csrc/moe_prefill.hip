@@ -1293,7 +1293,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   for (int c0 = 8 * threadIdx.x; c0 < H; c0 += 8 * blockDim.x) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int r = 0; r < k; ++r) {
-      const uint4 v = *reinterpret_cast<const uint4*>(D + (size_t)s_pos[r] * H + c0);
+      // Each row of D is read once here: non-temporal loads.
+      const u32x4v dv = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(D + (size_t)s_pos[r] * H + c0));
+      const uint4 v = make_uint4(dv.x, dv.y, dv.z, dv.w);
       const float w = s_w[r];
       const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
