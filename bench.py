@@ -39,7 +39,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 # WRITE_SIZE (calibrated against a 512 MiB copy) over `bench.py --profile-pass`; the
 # summary and commands are in profiles/decode_prefill_hbm_counters.txt.  Re-measure
 # after changing the kernel.
-DECODE_TRAFFIC_BYTES = 1341421977
+DECODE_TRAFFIC_BYTES = 1341868544
 # HBM bytes per lm_head GEMV launch from the same counter passes (1.001x its 749,076,480
 # algorithmic bytes).
 LM_HEAD_TRAFFIC_BYTES = 749777961
