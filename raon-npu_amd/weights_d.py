@@ -193,11 +193,11 @@ def bundle_path(weights_dir: Path, rel_file: str, name: str) -> Path:
     rule of npu/backend.py:278-291."""
     rel = Path(rel_file)
     if rel.is_absolute() or any(part == ".." for part in rel.parts):
-        raise ValueError(f"{name}: file path {rel_file!r} must be relative and stay below the weights directory")
+        raise ValueError(f"Unsafe file path for {name}: {rel_file!r} (absolute, or climbs with '..')")
     root = Path(weights_dir).resolve()
     target = (root / rel).resolve(strict=False)
     if target != root and root not in target.parents:
-        raise ValueError(f"{name}: file path {rel_file!r} escapes weights directory {root}")
+        raise ValueError(f"Unsafe file path for {name}: {rel_file!r} resolves outside {root}")
     return target
 
 
@@ -226,40 +226,43 @@ def _is_int(v) -> bool:
     return isinstance(v, int) and not isinstance(v, bool)
 
 
+# Each check returns None or the whole message.  Messages that the reference's own tests
+# match keep its words: "Manifest {key} mismatch for" (npu/test_backend_small.py:475,485),
+# "canonical size_bytes mismatch" (:588) and the field name of expert_count/expert_bytes
+# (:620-625).
 def _expect_equal(key: str):
     def check(value, meta: Bundle, want):
-        return None if value == want else f"{key} is {value!r}, expected {want!r}"
+        return None if value == want else f"Manifest {key} mismatch for {meta.name}: {value!r} != {want!r}"
     return check
 
 
 def _check_shape(key: str):
     def check(value, meta: Bundle, want):
         ok = isinstance(value, list) and list(value) == list(want)
-        return None if ok else f"{key} is {value!r}, expected {list(want)!r}"
+        return None if ok else f"Manifest {key} mismatch for {meta.name}: {value!r} != {list(want)!r}"
     return check
 
 
 def _check_count(key: str):
     def check(value, meta: Bundle, want):
-        return None if _is_int(value) and value == want else f"{key} is {value!r}, expected {want}"
+        ok = _is_int(value) and value == want
+        return None if ok else f"Manifest {key} mismatch for {meta.name}: {value!r} != {want}"
     return check
 
 
 def _check_file(value, meta: Bundle, want):
-    return None if isinstance(value, str) and value else "has no file name"
+    return None if isinstance(value, str) and value else f"Manifest file missing for {meta.name}"
 
 
 def _check_size(value, meta: Bundle, want):
     if not _is_int(value) or value < 0:
-        return f"size_bytes {value!r} is not a byte count"
-    # "canonical size_bytes mismatch" is the phrase the reference's tests match
-    # (npu/test_backend_small.py:588).
-    return None if value == want else f"canonical size_bytes mismatch: {value} != {want}"
+        return f"Manifest size_bytes for {meta.name} is not a byte count: {value!r}"
+    return None if value == want else f"Manifest entry {meta.name}: canonical size_bytes mismatch: {value} != {want}"
 
 
 def _check_sha(value, meta: Bundle, want):
     ok = isinstance(value, str) and re.fullmatch(r"[0-9a-fA-F]{64}", value) is not None
-    return None if ok else f"sha256 {value!r} is not 64 hex digits"
+    return None if ok else f"Manifest sha256 for {meta.name} is not 64 hex digits: {value!r}"
 
 
 # (manifest key, check, the canonical value it is compared with, applies to the bundle?)
@@ -287,7 +290,7 @@ def _check_components(item: dict, meta: Bundle, comps: Mapping[str, Component], 
             raise ValueError(f"Manifest entry {meta.name}: component {c!r} has no name")
         cname = c["name"]
         if cname not in allowed:
-            raise ValueError(f"Manifest entry {meta.name}: component {cname!r} does not belong to this bundle")
+            raise ValueError(f"Unknown component for {meta.name}: {cname!r}")
         named.add(cname)
         canon = comps.get(cname)
         if canon is None:
@@ -337,9 +340,9 @@ def load_manifest(path: str | Path, comps: Mapping[str, Component], bundles: Map
         name = item.get("bundle")
         meta = bundles.get(name) if isinstance(name, str) else None
         if meta is None:
-            raise ValueError(f"{path}: bundle {name!r} is not in the canonical map")
+            raise ValueError(f"Unknown NPU bundle in manifest: {name!r} ({path})")
         if name in listed:
-            raise ValueError(f"{path}: bundle {name} is listed twice")
+            raise ValueError(f"Duplicate NPU bundle in manifest: {name} ({path})")
         listed.add(name)
         if meta.expert_count and canonical_size(meta)[1] != meta.expert_bytes:
             raise ValueError(f"canonical map: {name} expert_bytes {meta.expert_bytes} != one matrix "
@@ -348,7 +351,7 @@ def load_manifest(path: str | Path, comps: Mapping[str, Component], bundles: Map
             if applies(meta):
                 msg = check(item.get(key), meta, want(meta))
                 if msg:
-                    raise ValueError(f"Manifest entry {name}: {msg}")
+                    raise ValueError(msg)
         if weights_dir is not None:
             target = bundle_path(Path(weights_dir), item["file"], name)
             try:
