@@ -64,9 +64,21 @@ def parse_args():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-lm-head", action="store_true", help="skip the lm_head bfp16 GEMV measurement")
     ap.add_argument("--no-configs", action="store_true", help="skip configs 1-3 and the weights-d layer")
+    ap.add_argument("--no-weights-d", action="store_true", help="skip the weights-d layer rows of 'configs'")
     ap.add_argument("--profile-pass", action="store_true",
                     help="short run for hardware counters: 2 decode launches, 1 prefill layer and a "
                          "512 MiB device copy (the calibration kernel of known size); prints no JSON")
+    ap.add_argument("--profile-configs", action="store_true",
+                    help="short run for hardware counters of configs 1-3: a 512 MiB device copy twice "
+                         "(calibration), then 20 config-1 GEMVs, 10 config-2 1-layer decode launches and 5 "
+                         "config-3 prefill layers, eager, one at a time; prints no JSON")
+    ap.add_argument("--build-timeline", action="store_true",
+                    help="build the timeline variant of librmoe.so (RMOE_DECODE_TIMELINE) into --timeline-dir "
+                         "and exit (CPU host; no GPU needed)")
+    ap.add_argument("--timeline", action="store_true",
+                    help="per-layer timeline of the 48-layer decode stack from the timeline variant library "
+                         "(built beforehand with --build-timeline); prints a table, no JSON")
+    ap.add_argument("--timeline-dir", type=Path, default=ROOT / "_build_timeline")
     return ap.parse_args()
 
 
@@ -228,52 +240,120 @@ def graph_us(fn, n: int, stream) -> float:
     return time_graph(g, 1, stream) / n * 1e6
 
 
-def configs_bench(ctx, layers, geom, seed: int, stream) -> dict:
+def roofline(bound: str, work: float, seconds: float, kernel: str, per: str, traffic=None) -> dict:
+    """The roofline block of one workload: `work` algorithmic bytes (hbm) or FLOPs (mfma) per
+    launch (or per layer, `per`) over its measured duration, against MI355X's peak."""
+    if bound == "hbm":
+        achieved, peak, unit = work / seconds / 1e9, HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved, peak, unit = work / seconds / 1e12, MFMA_BF16_PEAK_TFLOPS, "TFLOP/s"
+    return {"bound": bound, "kernel": kernel, "per": per, "work": work, "us": round(seconds * 1e6, 3),
+            "achieved": round(achieved, 1), "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
+            "traffic": traffic}
+
+
+# HBM bytes per launch of the configs 1-3 workloads measured with rocprofv3 FETCH_SIZE and
+# WRITE_SIZE over `bench.py --profile-configs` (calibrated against a 512 MiB copy); the
+# summary and commands are in profiles/configs123_hbm_counters.txt.  Re-measure after
+# changing the kernels.
+CONFIG_TRAFFIC_BYTES = {"config1_gemv": 1142209, "config2_decode_layer": 28710137, "config3_prefill_445": 466973329}
+
+
+class ConfigWorkloads:
+    """SURVEY configs 1-3 on the device: one q4nx GEMV [768, 2048] (config 1), one BASELINE
+    decode layer in a 1-layer persistent launch (config 2) and one BASELINE prefill layer of
+    445 tokens (config 3), each a callable that queues one launch (sequence) on `stream`."""
+
+    def __init__(self, ctx, layers, geom, seed: int, stream):
+        import torch
+
+        self.geom, self.stream = geom, stream
+        gen = torch.Generator(device="cuda").manual_seed(seed + 21)
+        # config 1: one q4nx GEMV, W [768, 2048] (the down width of a BASELINE expert), x 1 x 2048
+        w = torch.randn(768, 2048, device="cuda", generator=gen) * 0.02
+        self.mat = ctx.quantize_matrix(w, 768, 2048)
+        del w
+        self.mat.reserve(1)
+        self.x = torch.randn(1, 2048, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
+        self.y = torch.empty(1, 768, dtype=torch.int16, device="cuda")
+        # config 2: one decode layer (router + 8 routed + shared + combine), one persistent launch
+        self.layer0 = layers[0]
+        self.ctx = ctx
+        self.x1 = torch.randn(geom.hidden, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
+        self.o1 = torch.empty_like(self.x1)
+        # config 3: prefill of 445 tokens, router without selection bias (near-uniform routing)
+        self.T = 445
+        self.layer0.reserve(self.T)
+        self.xp = torch.randn(self.T, geom.hidden, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
+        self.op = torch.empty_like(self.xp)
+
+    def config1(self):
+        self.mat.linear_dev(self.x, 1, self.y, stream=self.stream)
+
+    def config2(self):
+        self.ctx.decode_stack_dev([self.layer0], self.x1, self.o1, residual=True, stream=self.stream)
+
+    def config3(self):
+        self.layer0.moe_prefill_dev(self.xp, self.T, self.op, stream=self.stream)
+
+    # algorithmic work per launch (SURVEY 8(d) figures)
+    CONFIG1_BYTES = 990208  # weights 983,040 + x 4,096 + y 3,072
+
+    def config3_flops(self) -> int:
+        g = self.geom
+        return self.T * (g.top_k + 1) * g.flops_per_assignment + 2 * self.T * g.hidden * g.n_routed
+
+    def config3_bytes(self) -> int:
+        """Every expert's weights (445 x 8 routes leave no expert unused) + the router + x in and out."""
+        g = self.geom
+        return g.n_experts * g.expert_bytes + g.router_bytes + 2 * self.T * g.hidden * 2
+
+    def free(self):
+        self.mat.free()
+
+
+def configs_bench(ctx, layers, geom, seed: int, stream, weights_d: bool = True) -> dict:
     """SURVEY configs 1-3 (the other rows of the measurement table) and one weights-d MoE
-    layer at the released model's shapes; each timed as back-to-back launches in a graph."""
+    layer at the released model's shapes; each timed as back-to-back launches in a graph,
+    with its roofline block (algorithmic bytes or FLOPs over the measured time)."""
     import numpy as np
     import torch
 
     from raon_npu_amd.geometry import RAON_1_MINI
 
     out = {}
-    gen = torch.Generator(device="cuda").manual_seed(seed + 21)
-    # config 1: one q4nx GEMV, W [768, 2048] (the down width of a BASELINE expert), x 1 x 2048
-    w = torch.randn(768, 2048, device="cuda", generator=gen) * 0.02
-    mat = ctx.quantize_matrix(w, 768, 2048)
-    del w
-    mat.reserve(1)
-    x = torch.randn(1, 2048, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
-    y = torch.empty(1, 768, dtype=torch.int16, device="cuda")
-    us = graph_us(lambda: mat.linear_dev(x, 1, y, stream=stream), 1000, stream)
-    b = 990208  # weights 983,040 + x 4,096 + y 3,072 (per-call algorithmic bytes)
+    wl = ConfigWorkloads(ctx, layers, geom, seed, stream)
+    gen = torch.Generator(device="cuda").manual_seed(seed + 22)
+    us = graph_us(wl.config1, 1000, stream)
+    b = wl.CONFIG1_BYTES
     out["config1_gemv"] = {"workload": "q4nx GEMV [768, 2048] x 1 token, 1000 launches in a graph",
                            "us_per_launch": round(us, 3), "GBps": round(b / us / 1e3, 1),
-                           "frac_hbm_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
-    out["_config1_bytes"] = mat.download()
-    mat.free()
-    # config 2: one decode layer (router + 8 routed + shared + combine), one persistent launch
-    x1 = torch.randn(geom.hidden, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
-    o1 = torch.empty_like(x1)
-    us = graph_us(lambda: ctx.decode_stack_dev([layers[0]], x1, o1, residual=True, stream=stream), 200, stream)
+                           "frac_hbm_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                           "roofline": roofline("hbm", b, us / 1e6, "linear_band_kernel<16>", "launch",
+                                                CONFIG_TRAFFIC_BYTES["config1_gemv"])}
+    out["_config1_bytes"] = wl.mat.download()
+    us = graph_us(wl.config2, 200, stream)
     b = geom.decode_bytes()
     out["config2_decode_layer"] = {"workload": "one BASELINE decode layer, batch 1 (1-layer persistent launch)",
                                    "us_per_layer": round(us, 3), "GBps": round(b / us / 1e3, 1),
-                                   "frac_hbm_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+                                   "frac_hbm_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                                   "roofline": roofline("hbm", b, us / 1e6, "decode_stack_kernel (1 layer)", "launch",
+                                                        CONFIG_TRAFFIC_BYTES["config2_decode_layer"])}
     ctx.reserve_decode_stack(layers)
-    # config 3: prefill of 445 tokens, router without selection bias (near-uniform routing)
-    lyr = layers[0]
-    T = 445
-    lyr.reserve(T)
-    xp = torch.randn(T, geom.hidden, device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
-    op = torch.empty_like(xp)
-    us = graph_us(lambda: lyr.moe_prefill_dev(xp, T, op, stream=stream), 20, stream)
-    fl = T * (geom.top_k + 1) * geom.flops_per_assignment + 2 * T * geom.hidden * geom.n_routed
+    us = graph_us(wl.config3, 20, stream)
+    fl = wl.config3_flops()
     wb = geom.n_experts * geom.expert_bytes
     out["config3_prefill_445"] = {"workload": "one BASELINE prefill layer, 445 tokens, softmax top-8 routing",
                                   "ms_per_layer": round(us / 1e3, 4), "tflops": round(fl / us / 1e6, 2),
                                   "weight_GBps": round(wb / us / 1e3, 1),
-                                  "frac_hbm_peak": round(wb / us / 1e3 / HBM_PEAK_GBS, 4)}
+                                  "frac_hbm_peak": round(wb / us / 1e3 / HBM_PEAK_GBS, 4),
+                                  "roofline": roofline("hbm", wl.config3_bytes(), us / 1e6,
+                                                       "prefill layer (router, top-k, dispatch, grouped GEMMs, combine)",
+                                                       "layer", CONFIG_TRAFFIC_BYTES["config3_prefill_445"]),
+                                  "mfma": roofline("mfma", fl, us / 1e6, "prefill layer", "layer")}
+    wl.free()
+    if not weights_d:
+        return out
     # weights-d layer: moe_b1 (q4nx) + moe_b2 (bfp16) at H=2560, I=1088, 128+1 experts, top-6
     g = RAON_1_MINI
     rng = np.random.default_rng(seed + 23)
@@ -495,6 +575,39 @@ def cpu_legs(layer0, geom, cfg1_bytes: bytes, args) -> dict:
     return {"headline": headline, "configs": out}
 
 
+def calibration_copy(n_copies: int = 2) -> None:
+    """A plain device copy of 512 MiB, n_copies times: its FETCH_SIZE / WRITE_SIZE per
+    dispatch calibrate the counters against a known byte count."""
+    import torch
+
+    n = 512 * 1024 * 1024
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(n_copies):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def profile_configs(ctx, layers, geom, args, stream) -> int:
+    """Configs 1-3 for per-dispatch hardware counters: the calibration copy, then each
+    config's launch sequence a fixed number of times, eagerly, one at a time."""
+    import torch
+
+    calibration_copy()
+    wl = ConfigWorkloads(ctx, layers[:1], geom, args.seed, stream)
+    ctx.reserve_decode_stack(layers[:1])
+    for name, fn, n in (("config1", wl.config1, 20), ("config2", wl.config2, 10), ("config3", wl.config3, 5)):
+        for _ in range(n):
+            with torch.cuda.stream(stream):
+                fn()
+            torch.cuda.synchronize()
+        log(f"profile configs: {name} x{n} done")
+    wl.free()
+    ctx.close()
+    return 0
+
+
 def profile_pass(ctx, layers, geom, args, stream, gen) -> int:
     """A short, fixed sequence of kernels for per-dispatch hardware counters: a plain
     device copy of 512 MiB (twice; its FETCH_SIZE / WRITE_SIZE per dispatch calibrate the
@@ -502,13 +615,7 @@ def profile_pass(ctx, layers, geom, args, stream, gen) -> int:
     prefill layer of config 5 and the lm_head GEMV."""
     import torch
 
-    n = 512 * 1024 * 1024
-    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
-    dst = torch.empty_like(src)
-    for _ in range(2):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    del src, dst
+    calibration_copy()
     x = (torch.randn(2, geom.hidden, device="cuda", generator=gen) * STACK_HIDDEN_STD).to(torch.bfloat16)
     x = x.view(torch.int16)
     out = torch.empty_like(x)
@@ -526,14 +633,112 @@ def profile_pass(ctx, layers, geom, args, stream, gen) -> int:
     return 0
 
 
+# Timeline stamps of the decode stack's timeline build (event index, meaning); the
+# product library has none.  One wave per workgroup stores s_memrealtime (100 MHz).
+TIMELINE_EVENTS = [
+    (0, "ready seen"),
+    (12, "first pass of partial logits in LDS"),
+    (1, "x and partial logits in LDS, summed"),
+    (13, "selection keys written"),
+    (2, "routing done (ranked)"),
+    (14, "first gate/up tile dot product (wave 0)"),
+    (15, "gate/up waves summed (barrier)"),
+    (3, "gate/up unit done, h published"),
+    (4, "down waves hold their h"),
+    (5, "down tiles in LDS"),
+    (6, "down tile dot products done (wave 1)"),
+    (7, "down partials summed (barrier)"),
+    (8, "d stored as tagged words"),
+    (9, "combiner holds every slot's d"),
+    (10, "combiner has stored its x band"),
+    (11, "combiner has published ready"),
+]
+TIMELINE_SHAPE = (48, 256, 16)  # layers, workgroups, events of the device buffer
+
+
+def build_timeline(out_dir: Path) -> Path:
+    """The timeline variant of librmoe.so (RMOE_DECODE_TIMELINE) under out_dir."""
+    sys.path.insert(0, str(ROOT / "raon-npu_amd"))
+    import build as B
+
+    return B.build(verbose=True, out_dir=out_dir, defines=("RMOE_DECODE_TIMELINE",))
+
+
+def timeline(lib_path: Path, seed: int) -> int:
+    """Four launches of the 48-layer BASELINE stack on the timeline library; prints, per
+    event, the median and the maximum over workgroups of the time since the layer's first
+    `ready`, averaged over layers 1..46, and the start of the next layer."""
+    import ctypes
+
+    import numpy as np
+
+    if not lib_path.exists():
+        log(f"{lib_path} is missing: build it first with --build-timeline")
+        return 2
+    from __graft_entry__ import load_package
+
+    load_package()
+    import raon_npu_amd._lib as L
+
+    L.LIB_PATH = lib_path  # the timeline build instead of the in-tree library
+    import torch
+
+    from raon_npu_amd.device import Context
+    from raon_npu_amd.geometry import BASELINE
+
+    nl, ng, ne = TIMELINE_SHAPE
+    ctx = Context(0)
+    layers = build_stack(ctx, BASELINE, nl, seed)
+    gen = torch.Generator(device="cuda").manual_seed(seed + 7)
+    x = (torch.randn(4, BASELINE.hidden, device="cuda", generator=gen) * STACK_HIDDEN_STD).to(torch.bfloat16)
+    x = x.view(torch.int16)
+    out = torch.empty_like(x)
+    ctx.reserve_decode_stack(layers)
+    stream = torch.cuda.Stream()
+    for i in range(4):
+        ctx.decode_stack_dev(layers, x[i], out[i], residual=True, stream=stream)
+    torch.cuda.synchronize()
+    fn = L.load().rmoe_debug_stack_timeline
+    fn.argtypes = [ctypes.POINTER(ctypes.c_ulonglong), ctypes.c_size_t]
+    buf = np.zeros((nl, ng, ne), np.uint64)
+    rc = fn(buf.ctypes.data_as(ctypes.POINTER(ctypes.c_ulonglong)), buf.size)
+    if rc != 0:
+        raise RuntimeError(f"rmoe_debug_stack_timeline returned {rc}")
+    b = buf.astype(np.int64)
+    rows, nxt = [], []
+    for l in range(1, nl - 1):
+        t0 = b[l, :, 0][b[l, :, 0] > 0].min()
+        r = []
+        for ev, _ in TIMELINE_EVENTS:
+            v = b[l, :, ev]
+            v = v[v > 0]
+            r.append(((np.median(v) - t0) / 100.0, (v.max() - t0) / 100.0) if len(v) else (np.nan, np.nan))
+        rows.append(r)
+        n = b[l + 1, :, 0]
+        nxt.append((n[n > 0].min() - t0) / 100.0)
+    m = np.nanmean(np.array(rows), axis=0)
+    print("decode stack timeline, 48-layer BASELINE stack, medians over workgroups averaged over layers 1..46")
+    print(f"{'event':44s} {'median':>9s} {'max':>9s}   (us from the layer's first ready)")
+    for (ev, name), (med, mx) in zip(TIMELINE_EVENTS, m):
+        print(f"{name:44s} {med:9.2f} {mx:9.2f}")
+    print(f"{'next layer first ready':44s} {np.mean(nxt):9.2f}", flush=True)
+    ctx.close()
+    return 0
+
+
 def main() -> int:
     args = parse_args()
+    if args.build_timeline:
+        build_timeline(args.timeline_dir)
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build runs on a single "
               f"MI355X; the multi-GPU expert-parallel layout is a design in DESIGN.md)", file=sys.stderr)
         return 2
     import torch
 
+    if args.timeline:
+        return timeline(args.timeline_dir / "librmoe.so", args.seed)
     from __graft_entry__ import load_package
 
     load_package()
@@ -551,6 +756,8 @@ def main() -> int:
     gen = torch.Generator(device="cuda").manual_seed(args.seed + 7)
     if args.profile_pass:
         return profile_pass(ctx, layers, geom, args, stream, gen)
+    if args.profile_configs:
+        return profile_configs(ctx, layers, geom, args, stream)
     K, W = max(1, args.steps), max(0, args.warmup)
     P = min(32, K)  # distinct tokens, resident in HBM; launch i carries token i % P
     x_pool = (torch.randn(P, geom.hidden, device="cuda", generator=gen) * STACK_HIDDEN_STD).to(torch.bfloat16)
@@ -609,7 +816,7 @@ def main() -> int:
 
     configs = None
     if not args.no_configs:
-        configs = configs_bench(ctx, layers, geom, args.seed, stream)
+        configs = configs_bench(ctx, layers, geom, args.seed, stream, weights_d=not args.no_weights_d)
         for k, v in configs.items():
             if not k.startswith("_"):
                 log(f"{k}: {v}")

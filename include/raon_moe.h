@@ -66,7 +66,9 @@ const char* rmoe_version(void);
  * and the XRT device/runner it opens. */
 int rmoe_create(int device, rmoe_ctx** out);
 int rmoe_destroy(rmoe_ctx* ctx);
-/* Wait for all work queued on the context's stream (run.wait(), npu/backend.py:2236-2244). */
+/* Wait for all work queued on the device (the context's stream and the streams of _dev calls;
+ * run.wait(), npu/backend.py:2236-2244), then report any error the kernels flagged since the
+ * last synchronous call (e.g. device expert ids out of range, a decode-stack timeout). */
 int rmoe_synchronize(rmoe_ctx* ctx);
 /* The context's HIP stream, as void*. */
 void* rmoe_stream(rmoe_ctx* ctx);
@@ -255,6 +257,13 @@ int rmoe_moe_decode(rmoe_ctx* ctx, int layer, const uint16_t* x, uint16_t* out, 
  * shared expert.  rmoe_reserve_decode_stack sizes the hand-off buffers (host call,
  * allocates); the _dev call never allocates. */
 int rmoe_reserve_decode_stack(rmoe_ctx* ctx, const int* layers, int n_layers);
+/* Diagnostic, no counterpart in the reference: the number of polls (about a microsecond
+ * each) after which a wait of the persistent decode kernel gives up (0 restores the default,
+ * about two seconds).  A wait that gives up abandons the launch (every workgroup leaves),
+ * and the next synchronous call returns RMOE_EDEVICE naming the first wait that gave up:
+ * its workgroup, layer and hand-off (the layer's input, a down unit's h, or a combiner's d).
+ * For callers that need a shorter bound, and for tests of the error report. */
+int rmoe_set_stack_wait_limit(rmoe_ctx* ctx, unsigned polls);
 int rmoe_moe_decode_stack_dev(rmoe_ctx* ctx, const int* layers, int n_layers, const void* x_dev, void* out_dev,
                               int residual, int act, float gate_beta, float value_beta, void* top_ids_dev,
                               void* top_weights_dev, void* stream);

@@ -74,6 +74,7 @@ SIGNATURES: dict[str, list] = {
     "rmoe_moe_decode_dev": [_p, _i, _p, _p, _i, _i, _f, _f, _p, _p, _p],
     "rmoe_moe_decode_stage_dev": [_p, _i, _i, _p, _p, _i, _i, _f, _f, _p],
     "rmoe_reserve_decode_stack": [_p, _p, _i],
+    "rmoe_set_stack_wait_limit": [_p, C.c_uint],
     "rmoe_moe_decode_stack_dev": [_p, _p, _i, _p, _p, _i, _i, _f, _f, _p, _p, _p],
     "rmoe_moe_decode_stack": [_p, _p, _i, _p, _p, _i, _i, _f, _f, _p, _p],
     "rmoe_moe_decode": [_p, _i, _p, _p, _i, _i, _f, _f, _p, _p],

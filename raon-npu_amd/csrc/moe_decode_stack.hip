@@ -53,8 +53,8 @@ constexpr int kLPad = 16;
 constexpr int kLRowLds = 4608;    // LDS floats for one pass (32 rows of 128 + 16)
 constexpr unsigned kSpinLimit = 1u << 21;
 
-// Per-layer timeline of the stack, in the timeline build only (RMOE_DECODE_TIMELINE; see
-// raon-npu_amd/decode_timeline.py): one wave of each workgroup stores the device clock
+// Per-layer timeline of the stack, in the timeline build only (RMOE_DECODE_TIMELINE; built
+// and read by bench.py --build-timeline / --timeline): one wave of each workgroup stores the device clock
 // (s_memrealtime, 100 MHz) at fixed points of every layer.  Other builds compile the
 // stamps to nothing.
 constexpr int kTimelineLayers = 48, kTimelineGroups = 256, kTimelineEvents = 16;
@@ -91,6 +91,7 @@ struct StackArgs {
   size_t layer_bytes, off_lpart, off_h, off_dout;
   unsigned* cnt;     // per layer cnt_stride counters, then exit, abort
   int cnt_stride;
+  unsigned spin_limit;  // polls before a wait gives up (about a microsecond each)
   int* err;
   const uint8_t* gu[kMaxStack];
   const uint8_t* dn[kMaxStack];
@@ -189,6 +190,20 @@ __device__ __forceinline__ unsigned* exit_cnt(const StackArgs& a) { return cnt_a
 __device__ __forceinline__ unsigned* abort_flag(const StackArgs& a) { return cnt_at(a, a.L, 1); }
 // Launch counter: read by every workgroup at the start, advanced by the last one out.
 __device__ __forceinline__ unsigned* epoch_cnt(const StackArgs& a) { return a.cnt; }
+// Which wait gave up first (0 while none has): kAbortValid | phase << 26 | layer << 12 |
+// workgroup, in word 1 of the launch counter's line (a fixed place, whatever the depth).
+__device__ __forceinline__ unsigned* abort_info(const StackArgs& a) { return a.cnt + 1; }
+
+// A bounded wait that ran out of polls: raise the abort flag (every other wait of the
+// grid sees it within 64 polls and its workgroup leaves), set error bit 8 and record the
+// first giver-up's wait (phase), layer and workgroup.
+__device__ __forceinline__ void give_up(const StackArgs& a, unsigned phase, int l, int g) {
+  st_dev_u32(abort_flag(a), 1u);
+  __hip_atomic_fetch_or(a.err, 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  unsigned expected = 0u;
+  __hip_atomic_compare_exchange_strong(abort_info(a), &expected, abort_code(phase, l, g), __ATOMIC_RELAXED,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Tagged hand-off words: 32 bits of data and the launch's tag (2 * epoch + 1: odd, so
 // never the zero of fresh memory) in one 64-bit device-scope store; a reader polls each
@@ -247,11 +262,12 @@ __device__ __forceinline__ void block_publish_ready(const StackArgs& a, int l) {
   if (threadIdx.x == 0) publish_ready(a, l);
 }
 
-// Block-wide wait until *p >= target (thread 0 polls).  Bounded: after kSpinLimit polls
-// (seconds) or when another workgroup gave up, the stack is abandoned (error bit 8,
-// abort flag) and false is returned in every thread, so every wave of the grid still
-// reaches its end.
-__device__ __forceinline__ bool wait_geq(const StackArgs& a, const unsigned* p, unsigned target, unsigned* flag_lds) {
+// Block-wide wait until *p >= target (thread 0 polls).  Bounded: after a.spin_limit polls
+// (seconds by default) or when another workgroup gave up, the stack is abandoned
+// (give_up) and false is returned in every thread, so every wave of the grid still
+// reaches its end.  phase, l: what the wait is for (recorded when it gives up).
+__device__ __forceinline__ bool wait_geq(const StackArgs& a, const unsigned* p, unsigned target, unsigned* flag_lds,
+                                         unsigned phase, int l) {
   if (threadIdx.x == 0) {
     unsigned ok = 1u;
     unsigned it = 0;
@@ -261,9 +277,8 @@ __device__ __forceinline__ bool wait_geq(const StackArgs& a, const unsigned* p, 
         ok = 0u;
         break;
       }
-      if (it > kSpinLimit) {
-        st_dev_u32(abort_flag(a), 1u);
-        __hip_atomic_fetch_or(a.err, 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (it > a.spin_limit) {
+        give_up(a, phase, l, blockIdx.x);
         ok = 0u;
         break;
       }
@@ -674,7 +689,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     const int hstride = a.Ipad / 2;
     uint64_t* dtag = reinterpret_cast<uint64_t*>(lay + a.off_dout);  // [S][H] tagged d words
 
-    if (!wait_geq(a, c_ready, (unsigned)a.nb2, &flag)) return;
+    if (!wait_geq(a, c_ready, (unsigned)a.nb2, &flag, kAbortReady, l)) return;
     RMOE_STAMP(l, g, 0, 0);
 
     const bool keys_fast = a.score == 1 && a.rb[l] == nullptr;
@@ -918,11 +933,8 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
             failed = true;
             break;
           }
-          if (it > kSpinLimit) {
-            if (lane == 0) {
-              st_dev_u32(abort_flag(a), 1u);
-              __hip_atomic_fetch_or(a.err, 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+          if (it > a.spin_limit) {
+            if (lane == 0) give_up(a, kAbortH, l, g);
             failed = true;
             break;
           }
@@ -1037,11 +1049,8 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
               cfailed = true;
               break;
             }
-            if (it > kSpinLimit) {
-              if (lane == 0) {
-                st_dev_u32(abort_flag(a), 1u);
-                __hip_atomic_fetch_or(a.err, 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-              }
+            if (it > a.spin_limit) {
+              if (lane == 0) give_up(a, kAbortD, l, g);
               cfailed = true;
               break;
             }
@@ -1202,7 +1211,7 @@ hipError_t stack_check(const RmoeLayer& L, int n_cu) {
 
 hipError_t launch_decode_stack(const RmoeLayer* const* layers, int n_layers, const uint16_t* x, uint16_t* out,
                                bool residual, int act, float gb, float vb, int32_t* ids_out, float* wts_out,
-                               RmoeScratch& s, int n_cu, hipStream_t st) {
+                               RmoeScratch& s, int n_cu, unsigned spin_limit, hipStream_t st) {
   if (n_layers < 1 || n_layers > kMaxStack) return hipErrorInvalidValue;
   const RmoeLayer& L0 = *layers[0];
   if (stack_check(L0, n_cu) != hipSuccess) return hipErrorInvalidValue;
@@ -1246,6 +1255,7 @@ hipError_t launch_decode_stack(const RmoeLayer* const* layers, int n_layers, con
   a.off_dout = sh.off_dout;
   a.cnt = s.stack_cnt;
   a.cnt_stride = sh.cnt_stride;
+  a.spin_limit = spin_limit ? spin_limit : kSpinLimit;
   a.err = s.err;
   for (int l = 0; l < n_layers; ++l) {
     const RmoeLayer& Ll = *layers[l];

@@ -125,11 +125,13 @@ __global__ __launch_bounds__(256) void dispatch_scatter_kernel(const int32_t* __
     if (same[j] && (same[j] >> lane) == 1ull) slot[wave][e] += __popcll(same[j]);
   }
   // The grouped GEMM's tile table (when asked for): routed group e holds sorted rows
-  // [offset, offset + total); the shared group (shared_rows > 0) follows them.
+  // [offset, offset + total); the shared group (shared_rows > 0) starts at row n (after
+  // every assignment, whether or not its id was valid), where the GEMM places it.
   if (c == 0 && tiles) {
     __shared__ int tsum[kTileClasses][4];
     const int ng = E + (shared_rows > 0 ? 1 : 0);
-    tile_table_block<4>(tid, ng, offset, offset + (tid < E ? total : shared_rows), tiles, ntiles, cap, tsum);
+    const int gb = tid < E ? offset : n;
+    tile_table_block<4>(tid, ng, gb, gb + (tid < E ? total : shared_rows), tiles, ntiles, cap, tsum);
   }
 }
 

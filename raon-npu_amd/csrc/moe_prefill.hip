@@ -121,7 +121,9 @@ constexpr int kRouterTok = 32;
 
 // Grid (ceil(T / 32), 4, E / (16 NFR)): workgroup (b, q, c) takes tokens 32b.., the K
 // quarter q and the experts 16 NFR c ..+16 NFR; its wave w the sixteenth 4q + w, whose sum
-// runs over 32-column steps in order.  The workgroup adds its waves' sums in wave order and
+// runs over 32-column steps in order.  The H/32 steps are dealt to the sixteenths as
+// evenly as they divide (sixteenth s: steps [s n / 16, (s+1) n / 16) of n); the split
+// depends on H only.  The workgroup adds its waves' sums in wave order and
 // writes the quarter's partial logits plogits[q][t][e]; topk_kernel adds the quarters in
 // order.  (An expert's sums do not depend on which workgroup holds it, so the split over
 // experts, which gives small batches more workgroups, changes no result.)
@@ -133,7 +135,8 @@ __device__ __forceinline__ void router_gemm_block(const uint16_t* __restrict__ x
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lq = lane >> 4;
   const int t0 = bx * kRouterTok, q = by, e0 = 16 * NFR * bz;
-  const int kq = H / 16, k0 = (4 * q + wave) * kq;
+  const int nsteps = H / 32, sx = 4 * q + wave;
+  const int k0 = (sx * nsteps / 16) * 32, kq = ((sx + 1) * nsteps / 16) * 32 - k0;
   f32x4_t acc[2][NFR];
 #pragma unroll
   for (int m = 0; m < 2; ++m)
@@ -405,19 +408,19 @@ __global__ __launch_bounds__(256) void router_prep_kernel(const uint16_t* __rest
 
 // ----------------------------------------------------------------- tile table --
 // One workgroup of 512 threads; thread e owns group e (routed 0..n_routed-1, shared
-// n_routed).  (The dispatch scatter builds the same table in its first workgroup when
-// the groups fit its 256 threads; this kernel serves the other cases and the table for
-// a second GEMM with other shared rows.)
+// n_routed, whose rows start at shared_base).  (The dispatch scatter builds the same table
+// in its first workgroup when the groups fit its 256 threads; this kernel serves the other
+// cases and the table for a second GEMM with other shared rows.)
 __global__ __launch_bounds__(512) void tile_table_kernel(const int32_t* __restrict__ offsets, int n_routed,
-                                                         int shared_rows, uint32_t* __restrict__ tiles,
+                                                         int shared_base, int shared_rows, uint32_t* __restrict__ tiles,
                                                          int* __restrict__ ntiles, int cap) {
   __shared__ int wsum[kTileClasses][8];
   const int e = threadIdx.x;
   const int ng = n_routed + (shared_rows > 0 ? 1 : 0);
   int b = 0, end = 0;
   if (e < ng) {
-    b = offsets[min(e, n_routed)];
-    end = e < n_routed ? offsets[e + 1] : b + shared_rows;
+    b = e < n_routed ? offsets[e] : shared_base;
+    end = e < n_routed ? offsets[e + 1] : shared_base + shared_rows;
   }
   tile_table_block<8>(e, ng, b, end, tiles, ntiles, cap, wsum);
 }
@@ -1269,9 +1272,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // ---------------------------------------------------------------- combine --
 // out[t] = RTNE(RTNE(sum_{routes by ascending expert} f32(D[inv[t,r]]) * w[t,r]) + D_shared[t])
 // (+ x[t] with residual); optionally also the routed and shared rows separately.
+// A route whose expert id is outside [0, E) (device ids are not checked on the host; the
+// dispatch flags them with error bit 4 and places no row for them) adds nothing, so the
+// output does not depend on stale scratch before the error is reported.
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ D, int H, const int32_t* __restrict__ ids,
                                                       const float* __restrict__ wts, const int32_t* __restrict__ inv,
-                                                      int k, int shared_base, const uint16_t* __restrict__ x,
+                                                      int k, int E, int shared_base, const uint16_t* __restrict__ x,
                                                       uint16_t* __restrict__ out, uint16_t* __restrict__ routed,
                                                       uint16_t* __restrict__ shared_out, int has_shared) {
   const int t = blockIdx.x;
@@ -1285,7 +1291,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
       const int e2 = ids[(size_t)t * k + q2];
       rank += (e2 < eq) || (e2 == eq && q2 < q);
     }
-    s_pos[rank] = inv[(size_t)t * k + q];
+    const bool valid = eq >= 0 && eq < E;
+    s_pos[rank] = valid ? inv[(size_t)t * k + q] : -1;
     s_w[rank] = wts[(size_t)t * k + q];
   }
   __syncthreads();
@@ -1293,6 +1300,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   for (int c0 = 8 * threadIdx.x; c0 < H; c0 += 8 * blockDim.x) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int r = 0; r < k; ++r) {
+      if (s_pos[r] < 0) continue;
       // Each row of D is read once here: non-temporal loads.
       const u32x4v dv = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(D + (size_t)s_pos[r] * H + c0));
       const uint4 v = make_uint4(dv.x, dv.y, dv.z, dv.w);
@@ -1432,9 +1440,17 @@ __global__ void h_unify_kernel(uint16_t* __restrict__ h, const int8_t* __restric
 }  // namespace
 
 // ------------------------------------------------------------------ launchers --
+const char* prefill_shape_error(const RmoeLayer& L, bool device_router) {
+  if (L.H % 128 || L.H > 64 * kPrepMaxChunks * 8) return "the grouped prefill needs hidden % 128 == 0 and hidden <= 8192";
+  if (L.Ipad % 256) return "the grouped prefill needs the padded intermediate size to be a multiple of 256";
+  if (device_router && (L.n_routed % 16 || L.n_routed > 16 * kMaxEFrags))
+    return "the device router of the grouped prefill needs n_routed % 16 == 0 and n_routed <= 256";
+  return nullptr;
+}
+
 hipError_t launch_router_prep(const uint16_t* x, int T, int H, const uint16_t* w, int E, float* logits,
                               uint16_t* xh, int8_t* xe, uint16_t* xsum, int32_t* zero, int nzero, hipStream_t st) {
-  if (E % 16 || E > 16 * kMaxEFrags || H % 512 || H / 8 > 64 * kPrepMaxChunks) return hipErrorInvalidValue;
+  if (E % 16 || E > 16 * kMaxEFrags || H % 128 || H / 8 > 64 * kPrepMaxChunks) return hipErrorInvalidValue;
   // Workgroups of up to 64 experts (NFR <= 4), E / 16 NFR of them per (token block, quarter),
   // then the preparation workgroups of four rows.
   const int nfr = E / 16 <= 4 ? E / 16 : (E / 16) % 4 == 0 ? 4 : (E / 16) % 3 == 0 ? 3 : (E / 16) % 2 == 0 ? 2 : 1;
@@ -1596,8 +1612,8 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   g.gb = gb;
   g.vb = vb;
   if (!fused_table) {
-    hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(512), 0, st, s.offsets, E, g.shared_rows, tiles, ntiles,
-                       tile_cap);
+    hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(512), 0, st, s.offsets, E, (int)A, g.shared_rows, tiles,
+                       ntiles, tile_cap);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
   if (shared_gu) {
@@ -1612,7 +1628,8 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   if ((err = hipGetLastError()) != hipSuccess) return err;
   // Down: every sorted row (routed + shared), rows of h contiguous.
   if (shared_gu) {
-    hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(512), 0, st, s.offsets, E, T, tiles, ntiles, tile_cap);
+    hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(512), 0, st, s.offsets, E, (int)A, T, tiles, ntiles,
+                       tile_cap);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
   GemmArgs d = g;
@@ -1636,7 +1653,7 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
   // more of D in the caches.
   d.out_nt = R * (size_t)L.H * 2 > ((size_t)64 << 20) ? 1 : 0;
   if ((err = launch_grouped(d, tiles, ntiles, tile_cap, E, st, L.dn_fmt == RMOE_FMT_BFP16)) != hipSuccess) return err;
-  hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, st, D, L.H, ids, wts, s.inv, k, (int)A,
+  hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, st, D, L.H, ids, wts, s.inv, k, E, (int)A,
                      residual ? x : nullptr, out, routed, shared_down, 1);
   return hipGetLastError();
 }

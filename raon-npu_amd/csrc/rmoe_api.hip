@@ -162,11 +162,24 @@ int sync_and_check(rmoe_ctx* ctx, hipStream_t st) {
       // A wait of the persistent decode kernel timed out: its counters are left
       // mid-way; clear them for the next launch.
       // Its launch counter restarts with them, so its tagged hand-off words are cleared
-      // as well.
+      // as well.  Word 1 of the counter area says which wait gave up first.
+      unsigned info = 0u;
       if (ctx->s.stack_cnt) {
+        HIP_TRY(hipMemcpy(&info, ctx->s.stack_cnt + 1, sizeof(unsigned), hipMemcpyDeviceToHost));
         HIP_TRY(hipMemsetAsync(ctx->s.stack_cnt, 0, ctx->s.stack_cnt_n * sizeof(unsigned), ctx->stream));
         if (ctx->s.stack) HIP_TRY(hipMemsetAsync(ctx->s.stack, 0, ctx->s.stack_bytes, ctx->stream));
         HIP_TRY(hipStreamSynchronize(ctx->stream));
+      }
+      if (info & rmoe::kAbortValid) {
+        const unsigned phase = (info >> 26) & 15u;
+        const char* what = phase == rmoe::kAbortReady ? "its input (the previous layer's combined bands, ready counter)"
+                           : phase == rmoe::kAbortH   ? "h of its down unit (the gate/up units of the slot)"
+                           : phase == rmoe::kAbortD   ? "d of its band (the down units, as the band's combiner)"
+                                                      : "an unknown hand-off";
+        return fail(RMOE_EDEVICE,
+                    "persistent decode kernel timed out waiting for other workgroups: workgroup %u gave up at layer "
+                    "%u waiting for %s",
+                    info & 0xfffu, (info >> 12) & 0x3fffu, what);
       }
       return fail(RMOE_EDEVICE, "persistent decode kernel timed out waiting for other workgroups");
     }
@@ -328,8 +341,9 @@ int rmoe_destroy(rmoe_ctx* ctx) {
 
 int rmoe_synchronize(rmoe_ctx* ctx) {
   if (!ctx) return fail(RMOE_EINVAL, "null context");
-  HIP_TRY(hipStreamSynchronize(ctx->stream));
-  return RMOE_OK;
+  HIP_TRY(hipSetDevice(ctx->device));
+  HIP_TRY(hipDeviceSynchronize());
+  return sync_and_check(ctx, ctx->stream);
 }
 
 void* rmoe_stream(rmoe_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
@@ -959,6 +973,12 @@ static int stack_layers(rmoe_ctx* ctx, const int* layers, int n_layers, std::vec
   return RMOE_OK;
 }
 
+int rmoe_set_stack_wait_limit(rmoe_ctx* ctx, unsigned polls) {
+  if (!ctx) return fail(RMOE_EINVAL, "null context");
+  ctx->stack_wait_limit = polls;
+  return RMOE_OK;
+}
+
 int rmoe_reserve_decode_stack(rmoe_ctx* ctx, const int* layers, int n_layers) {
   std::vector<const RmoeLayer*> ptrs;
   TRY(stack_layers(ctx, layers, n_layers, ptrs));
@@ -976,7 +996,7 @@ int rmoe_moe_decode_stack_dev(rmoe_ctx* ctx, const int* layers, int n_layers, co
   hipStream_t st = pick_stream(ctx, stream);
   hipError_t e = rmoe::launch_decode_stack(ptrs.data(), n_layers, (const uint16_t*)x_dev, (uint16_t*)out_dev,
                                            residual != 0, act, gate_beta, value_beta, (int32_t*)top_ids_dev,
-                                           (float*)top_weights_dev, ctx->s, ctx->n_cu, st);
+                                           (float*)top_weights_dev, ctx->s, ctx->n_cu, ctx->stack_wait_limit, st);
   if (e == hipErrorInvalidValue)
     return fail(RMOE_EINVAL, "decode stack scratch too small for %d layers: call rmoe_reserve_decode_stack", n_layers);
   HIP_TRY(e);
@@ -1074,6 +1094,7 @@ int rmoe_moe_experts_grouped(rmoe_ctx* ctx, int layer, const uint16_t* x, int T,
   if (L->n_shared < 1) return fail(RMOE_EINVAL, "layer %d has no shared expert", layer);
   if (act != RMOE_ACT_SITU && act != RMOE_ACT_SWIGLU) return fail(RMOE_EINVAL, "unknown activation %d", act);
   TRY(check_ids(top_ids, T, L->top_k, L->n_routed));
+  if (const char* why = rmoe::prefill_shape_error(*L, false)) return fail(RMOE_EINVAL, "layer %d: %s", layer, why);
   HIP_TRY(hipSetDevice(ctx->device));
   TRY(reserve_layer(ctx, *L, T, L->top_k));
   const int k = L->top_k;
@@ -1112,6 +1133,7 @@ int rmoe_moe_experts_grouped_dev(rmoe_ctx* ctx, int layer, const void* x_dev, in
   if (L->n_shared < 1) return fail(RMOE_EINVAL, "layer %d has no shared expert", layer);
   if (act != RMOE_ACT_SITU && act != RMOE_ACT_SWIGLU) return fail(RMOE_EINVAL, "unknown activation %d", act);
   if (T > ctx->s.max_tokens) return fail(RMOE_EINVAL, "T=%d exceeds the reserved %d tokens: call rmoe_reserve", T, ctx->s.max_tokens);
+  if (const char* why = rmoe::prefill_shape_error(*L, false)) return fail(RMOE_EINVAL, "layer %d: %s", layer, why);
   hipError_t e = rmoe::launch_moe_prefill(*L, (const uint16_t*)x_dev, T, (const int32_t*)top_ids_dev,
                                           (const float*)top_weights_dev, nullptr, nullptr,
                                           (const uint16_t*)shared_gu_dev, act, gate_beta, value_beta, false, nullptr,
@@ -1129,6 +1151,7 @@ int rmoe_moe_prefill_dev(rmoe_ctx* ctx, int layer, const void* x_dev, int T, voi
   if (!L->has_router) return fail(RMOE_EINVAL, "layer %d has no router", layer);
   if (L->n_shared < 1) return fail(RMOE_EINVAL, "layer %d has no shared expert", layer);
   TRY(require_q4nx_layer(*L, layer, "rmoe_moe_prefill_dev"));
+  if (const char* why = rmoe::prefill_shape_error(*L, true)) return fail(RMOE_EINVAL, "layer %d: %s", layer, why);
   if (!x_dev || !out_dev || T < 1) return fail(RMOE_EINVAL, "bad argument");
   if (act != RMOE_ACT_SITU && act != RMOE_ACT_SWIGLU) return fail(RMOE_EINVAL, "unknown activation %d", act);
   if (T > ctx->s.max_tokens) return fail(RMOE_EINVAL, "T=%d exceeds the reserved %d tokens: call rmoe_reserve", T, ctx->s.max_tokens);

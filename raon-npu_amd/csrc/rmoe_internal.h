@@ -375,6 +375,7 @@ struct rmoe_ctx {
   int next_handle = 1;
   std::map<int, RmoeLayer> layers;
   RmoeScratch s;
+  unsigned stack_wait_limit = 0;  // polls before a wait of the decode stack gives up (0: default)
 };
 
 // ------------------------------------------------------- kernel launch wrappers --
@@ -436,7 +437,10 @@ hipError_t launch_moe_prefill(const RmoeLayer& L, const uint16_t* x, int T, cons
                               int32_t* ids_out, float* wts_out, const uint16_t* shared_gu, int act, float gb, float vb,
                               bool residual, uint16_t* out, uint16_t* routed, uint16_t* shared_down, uint8_t* scratch,
                               size_t scratch_bytes, RmoeScratch& s, hipStream_t st);
-// Prefill router: logits as four K-quarter partials [4][T][E] (H % 512 == 0), which
+// Shapes the grouped prefill cannot run (a message), or null.  device_router: the
+// routing is computed on the device (rmoe_moe_prefill_dev).
+const char* prefill_shape_error(const RmoeLayer& L, bool device_router);
+// Prefill router: logits as four K-quarter partials [4][T][E] (H % 128 == 0), which
 // launch_topk adds in order; the same launch prepares the activation rows of the grouped
 // GEMM (xh, xe, xsum; see moe_prefill.hip).
 hipError_t launch_router_prep(const uint16_t* x, int T, int H, const uint16_t* w, int E, float* logits,
@@ -454,9 +458,19 @@ size_t stack_scratch_bytes(const RmoeLayer& L, int n_layers);
 size_t stack_counter_count(const RmoeLayer& L, int n_layers);
 hipError_t stack_check(const RmoeLayer& L, int n_cu);
 hipError_t decode_stack_occupancy(int* blocks_per_cu);
+// spin_limit: polls before a wait gives up (0: the default, about two seconds).
 hipError_t launch_decode_stack(const RmoeLayer* const* layers, int n_layers, const uint16_t* x, uint16_t* out,
                                bool residual, int act, float gb, float vb, int32_t* ids_out, float* wts_out,
-                               RmoeScratch& s, int n_cu, hipStream_t st);
+                               RmoeScratch& s, int n_cu, unsigned spin_limit, hipStream_t st);
+// The persistent kernel's record of the wait that gave up first (word 1 of its counter
+// area; 0 while none has): kAbortValid | phase << 26 | layer << 12 | workgroup.
+constexpr unsigned kAbortValid = 0x80000000u;
+constexpr unsigned kAbortReady = 1u;  // a layer's input (the previous layer's combined bands)
+constexpr unsigned kAbortH = 2u;      // a down unit's h (the gate/up units of its slot)
+constexpr unsigned kAbortD = 3u;      // a combiner's d (the down units of its band)
+__host__ __device__ constexpr unsigned abort_code(unsigned phase, int layer, int wg) {
+  return kAbortValid | (phase & 15u) << 26 | ((unsigned)layer & 0x3fffu) << 12 | ((unsigned)wg & 0xfffu);
+}
 
 // Scratch requirements (bytes) for the launch wrappers above.
 // The per-stage decode kernels' shape limit: hipSuccess if `slots` slots of layer L fit

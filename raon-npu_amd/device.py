@@ -136,6 +136,12 @@ class Context:
         ids = self._layer_ids(layers)
         call("rmoe_reserve_decode_stack", self._h, ptr(ids), ids.size)
 
+    def set_stack_wait_limit(self, polls: int = 0):
+        """Polls (about a microsecond each) after which a wait of the persistent decode
+        kernel gives up; 0 restores the default (about two seconds).  The next synchronous
+        call then raises RmoeError naming the workgroup, layer and hand-off that gave up."""
+        call("rmoe_set_stack_wait_limit", self._h, int(polls))
+
     def decode_stack(self, layers, x, residual: bool = True, gate_beta=None, value_beta=None):
         """One token through every layer in ``layers`` (one persistent launch).
         Returns (out u16[H], top_ids int32[L, k], weights f32[L, k])."""

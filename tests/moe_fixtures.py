@@ -71,6 +71,18 @@ def routing_margin(x_u16: np.ndarray, spec: om.RouterSpec) -> float:
     return float(s[spec.top_k - 1] - s[spec.top_k]) if s.size > spec.top_k else np.inf
 
 
+def routing_margins(xs_u16: np.ndarray, spec: om.RouterSpec) -> np.ndarray:
+    """routing_margin of every row of xs (one batched fp32 product; its rounding may differ
+    from route_token's in the last bits, far below the 1e-6 near-tie threshold)."""
+    from oracle.bf16 import bf16_to_f32
+
+    logits = bf16_to_f32(xs_u16) @ spec.weight_f32().T
+    scores = om.router_scores(logits, spec.score)
+    choice = scores if spec.bias is None else scores + spec.bias
+    srt = -np.sort(-choice, axis=1)
+    return (srt[:, spec.top_k - 1] - srt[:, spec.top_k]).astype(np.float64)
+
+
 def compare_bf16(a_u16: np.ndarray, b_u16: np.ndarray) -> tuple[float, float, float]:
     """(max-abs, rel-L2, fraction of bit-identical elements) of two bf16 arrays."""
     from oracle.bf16 import bf16_to_f32

@@ -245,6 +245,30 @@ def test_stack_graph_replays_match_eager(gpu_ctx):
         lyr.free()
 
 
+def test_stack_wait_timeout_is_reported(gpu_ctx):
+    """A wait that gives up is reported with its workgroup, layer and hand-off.  The host
+    forces it by lowering the kernel's own poll bound (every workgroup still leaves
+    normally: the others see the abort flag); the context is cleared for the next launch,
+    which equals the result from before."""
+    from raon_npu_amd._lib import RmoeError
+
+    geom, layers, _ = _small_stack(gpu_ctx, 3, 1900)
+    gpu_ctx.reserve_decode_stack(layers)
+    x = random_tokens(1, geom.hidden, 1910)[0]
+    good, top, _ = gpu_ctx.decode_stack(layers, x, residual=True)
+    try:
+        gpu_ctx.set_stack_wait_limit(1)
+        with pytest.raises(RmoeError, match=r"workgroup \d+ gave up at layer \d+ waiting for"):
+            gpu_ctx.decode_stack(layers, x, residual=True)
+    finally:
+        gpu_ctx.set_stack_wait_limit(0)
+    again, top2, _ = gpu_ctx.decode_stack(layers, x, residual=True)
+    np.testing.assert_array_equal(again, good)
+    np.testing.assert_array_equal(top2, top)
+    for lyr in layers:
+        lyr.free()
+
+
 def test_stack_rejects_mixed_geometry(gpu_ctx):
     a = gpu_ctx.create_layer(1700, G.MoeGeometry(hidden=512, inter=256, n_routed=16, n_shared=1, top_k=4))
     b = gpu_ctx.create_layer(1701, G.MoeGeometry(hidden=512, inter=128, n_routed=16, n_shared=1, top_k=4))
@@ -303,16 +327,34 @@ def _chained(layers, x_dev, stream):
     return inputs, h, ids
 
 
+def _stack48_routers(geom, n=N48, seed=9100):
+    """The router of each layer of stack48 (bf16 bit patterns), regenerated from its seed."""
+    import torch
+
+    routers = []
+    for li in range(n):
+        gen = torch.Generator(device="cuda").manual_seed(seed + li)
+        rw = (torch.randn(geom.n_routed, geom.hidden, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+        routers.append(rw.view(torch.int16).cpu().numpy().view(np.uint16))
+    return routers
+
+
 def test_stack48_equals_chained_layers_and_oracle_routing(gpu_ctx, stack48):
     """One 48-layer persistent launch == 48 chained 1-layer launches bit for bit (outputs and
-    routing of every layer); the routing of layers 0, 1, 23, 46 and 47 equals the oracle's on
-    the GPU's own layer input, and those layers' outputs match the oracle within the bar."""
+    routing of every layer), for four tokens; the routing of all 48 layers of every token
+    equals the oracle's (host/raon.py:1224-1247) on the GPU's own layer input, apart from
+    near-ties (k/k+1 gap <= 1e-6, reported); and the outputs of layers 0, 1, 23, 46 and 47
+    of the first token match the oracle within the bar."""
     import torch
 
     geom, layers = stack48
     s = torch.cuda.current_stream()
-    xs = random_tokens(2, geom.hidden, 3010, STACK_HIDDEN_STD)
-    for t in range(2):
+    specs = [om.RouterSpec(r, geom.top_k, score="softmax") for r in _stack48_routers(geom)]
+    wfs = [sp.weight_f32() for sp in specs]
+    n_tok = 4
+    xs = random_tokens(n_tok, geom.hidden, 3010, STACK_HIDDEN_STD)
+    checked = ties = 0
+    for t in range(n_tok):
         x_dev = torch.from_numpy(xs[t].view(np.int16)).cuda()
         inputs, h, ids_l = _chained(layers, x_dev, s)
         out = torch.empty_like(x_dev)
@@ -322,20 +364,24 @@ def test_stack48_equals_chained_layers_and_oracle_routing(gpu_ctx, stack48):
         assert torch.equal(ids_s, ids_l), f"token {t}: routing differs from the chained launches"
         assert torch.equal(out, h), f"token {t}: 48-layer launch differs from the chained launches"
         assert np.all(np.isfinite(bf16_to_f32(out.cpu().numpy().view(np.uint16)))), "residual stream overflowed"
+        got_ids = ids_s.cpu().numpy()
+        xin_all = [inp.cpu().numpy().view(np.uint16) for inp in inputs]
+        for li in range(N48):
+            top, _, _ = om.route_token(xin_all[li], specs[li], wfs[li])
+            if routing_margin(xin_all[li], specs[li]) > MARGIN:
+                assert got_ids[li].tolist() == top.tolist(), f"token {t} layer {li}"
+                checked += 1
+            else:
+                ties += 1
         if t:
             continue
         for li in (0, 1, 23, 46, 47):
-            lyr = layers[li]
-            xin = inputs[li].cpu().numpy().view(np.uint16)
-            gen = torch.Generator(device="cuda").manual_seed(9100 + li)
-            rw = (torch.randn(geom.n_routed, geom.hidden, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
-            router = rw.view(torch.int16).cpu().numpy().view(np.uint16)
-            spec = om.RouterSpec(router, geom.top_k, score="softmax")
-            ref, top, _, _ = om.moe_token(LazyBank(lyr), spec, xin, None, None, shared_id=geom.shared_id)
-            if routing_margin(xin, spec) > MARGIN:
-                assert ids_s[li].cpu().tolist() == top.tolist(), f"layer {li}"
+            xin = xin_all[li]
+            ref, _, _, _ = om.moe_token(LazyBank(layers[li]), specs[li], xin, None, None, shared_id=geom.shared_id)
             got = (inputs[li + 1] if li + 1 < N48 else h).cpu().numpy().view(np.uint16)
             check_bf16(got, f32_to_bf16(bf16_to_f32(xin) + bf16_to_f32(ref)), f"48-stack layer {li}")
+    print(f"48-layer routing: {checked} (token, layer) pairs equal the oracle, {ties} near-ties reported")
+    assert checked >= n_tok * N48 - 4
 
 
 def test_stack48_graph_back_to_back(gpu_ctx, stack48):
