@@ -17,9 +17,10 @@
 //     wave w streams K tiles w, w + 8, ...).  The workgroup sums its waves, applies the
 //     activation and publishes h of its 32 columns.
 //   DN unit (slot s, output band b of 64 rows): all K tiles of the band; waves 1..7
-//     stream them, each with the h of its 128 columns.
+//     copy them into LDS, and all eight waves take their half tiles (64 columns each,
+//     with the h of those columns).
 // Hand-offs between workgroups (per layer):
-//   h         tagged words (below): DN waves poll the words of their own columns
+//   h         tagged words (below): every wave polls the words of its own columns
 //   d         tagged words: the combiner of band b (the workgroup whose first DN unit is
 //             slot 0 of band b) polls the band's words of every slot, combines the band,
 //             writes x_{l+1}[band] and the band's share of the router logits of layer l+1
@@ -58,16 +59,30 @@ constexpr unsigned kSpinLimit = 1u << 21;
 // (s_memrealtime, 100 MHz) at fixed points of every layer.  Other builds compile the
 // stamps to nothing.
 constexpr int kTimelineLayers = 48, kTimelineGroups = 256, kTimelineEvents = 16;
+// The stamps of a layer go to LDS; wave 0 copies them to memory at the top of the next
+// layer (RMOE_STAMP_FLUSH), so that no store of the timeline sits before a barrier of the
+// layer it measures (a barrier also waits for the workgroup's stores in flight).
 #ifdef RMOE_DECODE_TIMELINE
 __device__ unsigned long long g_stack_timeline[kTimelineLayers][kTimelineGroups][kTimelineEvents];
-#define RMOE_STAMP(l, g, ev, who)                                                           \
-  do {                                                                                       \
-    if (threadIdx.x == (who) && (l) < kTimelineLayers && (g) < kTimelineGroups)              \
-      g_stack_timeline[l][g][ev] = __builtin_amdgcn_s_memrealtime();                         \
+__shared__ unsigned long long g_tl_lds[kTimelineEvents];
+#define RMOE_STAMP(l, g, ev, who)                                              \
+  do {                                                                          \
+    if (threadIdx.x == (who)) g_tl_lds[ev] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#define RMOE_STAMP_FLUSH(l, g)                                                                          \
+  do {                                                                                                   \
+    if (threadIdx.x < kTimelineEvents) {                                                                 \
+      if ((l) >= 0 && (l) < kTimelineLayers && (g) < kTimelineGroups)                                    \
+        g_stack_timeline[l][g][threadIdx.x] = g_tl_lds[threadIdx.x];                                     \
+      g_tl_lds[threadIdx.x] = 0ull;                                                                      \
+    }                                                                                                    \
   } while (0)
 #else
 #define RMOE_STAMP(l, g, ev, who) \
   do {                            \
+  } while (0)
+#define RMOE_STAMP_FLUSH(l, g) \
+  do {                         \
   } while (0)
 #endif
 // Stamp points (event index): ready seen 0, x and partial logits summed 1, routing done 2,
@@ -561,9 +576,10 @@ __device__ __forceinline__ void read_router_slice(const StackArgs& a, const uint
 // They size register and LDS arrays, so they are template
 // parameters.
 //
-// Wave roles: every wave streams GU tiles; waves 1..7 stream the DN tiles; wave 0 does
-// the cross-workgroup hand-offs (partial sums, h, d, the combine) and holds no DN
-// prefetch, so its waits for its own stores are short.  Loads that have no valid
+// Wave roles: every wave streams GU tiles; waves 1..7 copy the DN tiles into LDS, and
+// all eight waves compute their dot products; wave 0 does the cross-workgroup stores
+// (partial sums, h, d, the combine) and holds no DN copies in flight, so its waits for
+// its own stores are short.  Loads that have no valid
 // target read `dummy` instead of being skipped: every wave issues the same number of
 // loads on every path, which keeps the compiler's s_waitcnt counts exact (a GU tile is
 // consumed without waiting for the DN tiles issued after it).
@@ -573,8 +589,11 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
   __shared__ float xsum[kMaxH / 32];                              // group sums of x_l
   __shared__ SelectLds sl;
   __shared__ float red[kWaves][2][64];
-  __shared__ __attribute__((aligned(16))) uint32_t hs[kWaves][DNPOS][64];
-  __shared__ float hsum[kWaves][DNPOS][4];
+  // h of each wave's half-tile items (32 bf16 pairs) and their two group sums.  Up to
+  // 7 * DNPOS tiles = 14 * DNPOS half tiles over the 8 waves, two items per pair.
+  constexpr int kHalfPairs = ((2 * DNPOS * (kWaves - 1) + kWaves - 1) / kWaves + 1) / 2;
+  __shared__ __attribute__((aligned(16))) uint32_t hs2[kWaves][2 * kHalfPairs][32];
+  __shared__ float hsum2[kWaves][2 * kHalfPairs][2];
   __shared__ float cmb[kMaxSlots][64];                         // d of every slot of a band
   __shared__ __attribute__((aligned(16))) uint32_t xband[32];  // x_{l+1} of a band, bf16 pairs
   __shared__ __attribute__((aligned(16))) float lrow[kLRowLds];  // partial logits being summed
@@ -689,6 +708,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     const int hstride = a.Ipad / 2;
     uint64_t* dtag = reinterpret_cast<uint64_t*>(lay + a.off_dout);  // [S][H] tagged d words
 
+    RMOE_STAMP_FLUSH(l - 1, g);
     if (!wait_geq(a, c_ready, (unsigned)a.nb2, &flag, kAbortReady, l)) return;
     RMOE_STAMP(l, g, 0, 0);
 
@@ -769,12 +789,11 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
               const int b = bb + P * i;
               v[i] = b < nb ? lrow[b * lstride + pe] : 0.f;
             }
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-              if (bb + P * i < nb) lacc += v[i];
+            // (absent bands read 0: adding +0 leaves every sum unchanged)
+            lacc += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
           }
         }
-        __syncthreads();
+        if (b0 + nbc < a.nb2) __syncthreads();  // lrow is refilled by the next pass
       }
       lacc += dpp_f32<0xB1>(lacc);
       if (P == 4) lacc += dpp_f32<0x4E>(lacc);
@@ -905,26 +924,40 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
       // are zero).  Bounded: past kSpinLimit polls, or when another workgroup gave up,
       // the stack is abandoned after the whole workgroup has agreed to stop.
       bool failed = false;
-      if (wave > 0) {
-        uint64_t hv[DNPOS];
-        const uint64_t* hp[DNPOS];
+      // Work items: half tiles (item it: tile it >> 1, its groups 2 (it & 1) and +1), dealt
+      // round robin to all eight waves, so that the two waves of every SIMD share its
+      // work (a DN tile's dot products are one dependent chain per row; a SIMD runs two
+      // waves' chains interleaved at twice the rate of one).  The tiles were copied into
+      // LDS by waves 1..7; the barrier below makes every copy visible to every wave.
+      // h of an item: lanes 0..31 poll the 32 tagged words of item 2q, lanes 32..63 those
+      // of item 2q + 1 (columns 128 kt + 64 (it & 1) + 2 (lane & 31), +1; columns past I
+      // are zero), until they carry this launch's tag.  Bounded: past a.spin_limit polls,
+      // or when another workgroup gave up, the stack is abandoned after the whole
+      // workgroup has agreed to stop.
+      const int n_items = 2 * n_dn_t;
+      auto item_of = [&](int m) { return wave + kWaves * m; };
+      {
+        uint64_t hv[kHalfPairs];
+        const uint64_t* hp[kHalfPairs];
         unsigned need = 0u;
 #pragma unroll
-        for (int p = 0; p < DNPOS; ++p) {
-          const int t = wave - 1 + (kWaves - 1) * p;
-          const int d = t < n_dn_t ? t / a.nkt2 : 0;
-          const int c0 = 128 * (t < n_dn_t ? t % a.nkt2 : 0) + 2 * lane;
-          hv[p] = 0ull;
-          hp[p] = hbuf + (size_t)(dn_d[d][0] < 0 ? 0 : dn_d[d][0]) * hstride + (c0 >> 1);
-          if (t < n_dn_t && c0 < a.I) need |= 1u << p;
+        for (int q = 0; q < kHalfPairs; ++q) {
+          const int it = item_of(2 * q + (lane >> 5));
+          const bool ok = it < n_items;
+          const int t = ok ? it >> 1 : 0;
+          const int d = t / a.nkt2;
+          const int c0 = 128 * (t % a.nkt2) + 64 * (it & 1) + 2 * (lane & 31);
+          hv[q] = 0ull;
+          hp[q] = hbuf + (size_t)(dn_d[d][0] < 0 ? 0 : dn_d[d][0]) * hstride + (c0 >> 1);
+          if (ok && c0 < a.I) need |= 1u << q;
         }
         unsigned it = 0;
         while (__any(need != 0u)) {
 #pragma unroll
-          for (int p = 0; p < DNPOS; ++p) {
-            if (need & (1u << p)) {
-              hv[p] = ld_dev_u64(hp[p]);
-              if ((uint32_t)(hv[p] >> 32) == tag) need &= ~(1u << p);
+          for (int q = 0; q < kHalfPairs; ++q) {
+            if (need & (1u << q)) {
+              hv[q] = ld_dev_u64(hp[q]);
+              if ((uint32_t)(hv[q] >> 32) == tag) need &= ~(1u << q);
             }
           }
           if (!__any(need != 0u)) break;
@@ -941,36 +974,43 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
           __builtin_amdgcn_s_sleep(1);
         }
 #pragma unroll
-        for (int p = 0; p < DNPOS; ++p) {
-          const int t = wave - 1 + (kWaves - 1) * p;
-          if (t < n_dn_t) {
-            const uint32_t hw = (uint32_t)hv[p];  // zero for columns past I
+        for (int q = 0; q < kHalfPairs; ++q) {
+          const int m = 2 * q + (lane >> 5);
+          if (item_of(2 * q) < n_items) {  // the pair's first item exists (uniform)
+            const uint32_t hw = (uint32_t)hv[q];  // zero for columns past I and absent items
             const float h0 = bf16_to_f32(hw & 0xffffu), h1 = bf16_to_f32(hw >> 16);
-            hs[wave][p][lane] = hw;
-            // Sum over the 16 lanes of a row (32 columns, one group) on DPP: quad swaps,
-            // then the half-row and row mirrors.
+            hs2[wave][m][lane & 31] = hw;
             float gs = h0 + h1;
             gs += dpp_f32<0xB1>(gs);
             gs += dpp_f32<0x4E>(gs);
             gs += dpp_f32<0x141>(gs);
             gs += dpp_f32<0x140>(gs);
-            if ((lane & 15) == 0) hsum[wave][p][lane >> 4] = gs;
+            if ((lane & 15) == 0) hsum2[wave][m][(lane >> 4) & 1] = gs;
           }
         }
       }
       if (__syncthreads_or(failed ? 1 : 0)) return;
       RMOE_STAMP(l, g, 4, 0);
-      // This wave's DN tiles were copied into LDS by its own loads: drain them.
+      // The DN tiles were copied into LDS by the waves' own loads: drain them.
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       RMOE_STAMP(l, g, 5, 0);
       float acc[kMaxDnUnits] = {0.f, 0.f};
-      if (wave > 0) {
+      {
+#pragma unroll 1
+        for (int m = 0; m < 2 * kHalfPairs; ++m) {
+          const int it = item_of(m);
+          if (it < n_items) {
+            const int t = it >> 1, hf = it & 1;
+            const uint8_t* tp = dn_lds + (size_t)t * kTileBytes + lane * 16;
+            const uint2 smv = *reinterpret_cast<const uint2*>(tp + kCodeBytes + 8 * hf);
+            const uint32_t sm[2] = {smv.x, smv.y};
+            float v = 0.f;
 #pragma unroll
-        for (int p = 0; p < DNPOS; ++p) {
-          const int t = wave - 1 + (kWaves - 1) * p;
-          if (t < n_dn_t) {
-            const float v = tile_dot_lds(dn_lds + (size_t)t * kTileBytes, lane, hs[wave][p], hsum[wave][p], 0.f);
+            for (int j = 0; j < 2; ++j) {
+              const uint4 cw = *reinterpret_cast<const uint4*>(tp + (2 * hf + j) * 1024);
+              v = group_apply(sm[j], group_dot(cw, hs2[wave][m] + 16 * j), hsum2[wave][m][j], v);
+            }
             if (t < a.nkt2) acc[0] += v;
             else acc[1] += v;
           }
@@ -991,17 +1031,25 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
       // They are drained before the logits.
       uint8_t* rw_lds = dn_lds;  // [E rounded up to 8][128 B]
       if (comb && wave > 0 && l + 1 < a.L) dma_router_slice(a, a.rw[l + 1], cb, rw_lds, wave - 1, lane);
+      // d of both units as tagged words: no store acknowledgement and no counter; the
+      // combiner of the band polls them.  A combiner keeps the d of its own units of its
+      // band in LDS instead (own: their slot bits), so it polls only the other slots.
+      unsigned own = 0u;
       if (wave == 0) {
-        // d of both units as tagged words: no store acknowledgement and no counter; the
-        // combiner polls the words of its band.
 #pragma unroll
         for (int d = 0; d < kMaxDnUnits; ++d) {
           if (dn_d[d][0] < 0) continue;
           float dd = 0.f;
 #pragma unroll
-          for (int w = 1; w < kWaves; ++w) dd += red[w][d][lane];
-          st_dev_u64(&dtag[(size_t)dn_d[d][0] * a.H + 64 * dn_d[d][1] + lane],
-                     (uint64_t)__float_as_uint(bf16_round(dd)) | ((uint64_t)tag << 32));
+          for (int w = 0; w < kWaves; ++w) dd += red[w][d][lane];
+          const float v = bf16_round(dd);
+          if (comb && dn_d[d][1] == cb) {
+            cmb[dn_d[d][0]][lane] = v;
+            own |= 1u << dn_d[d][0];
+          } else {
+            st_dev_u64(&dtag[(size_t)dn_d[d][0] * a.H + 64 * dn_d[d][1] + lane],
+                       (uint64_t)__float_as_uint(v) | ((uint64_t)tag << 32));
+          }
         }
       }
       RMOE_STAMP(l, g, 8, 0);
@@ -1026,7 +1074,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
           // d of every slot of the band into LDS: each lane polls its row's word of every
           // slot (up to 9 loads in flight) until all carry this launch's tag.  Bounded
           // like the h wait.
-          unsigned need = (1u << a.S) - 1u;
+          unsigned need = ((1u << a.S) - 1u) & ~own;
           unsigned it = 0;
           while (true) {
             for (int q0 = 0; q0 < a.S; q0 += 9) {
@@ -1122,6 +1170,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     }
   }
 
+  RMOE_STAMP_FLUSH(a.L - 1, g);
   // Every wave's stores and counter updates are complete before the workgroup counts
   // itself out; the last workgroup out clears every counter for the next launch.
   if (block_arrive(exit_cnt(a), (unsigned)G, &flag)) {
