@@ -50,16 +50,28 @@ __global__ __launch_bounds__(256) void dispatch_scatter_kernel(const int32_t* __
   __shared__ int wsum[4];
   const int c = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   for (int i = tid; i < 4 * 256; i += 256) (&slot[0][0])[i] = 0;
+  // This wave's assignments (loaded first, so that their latency overlaps the count reads).
+  const int begin = c * kChunk + 256 * wave;
+  int ev[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = begin + 64 * j + lane;
+    ev[j] = i < n ? ids[i] : -1;
+  }
   // Thread e: expert e's assignments in the chunks before this one and in all chunks;
   // the expert's offset is the exclusive scan of the totals (wave scans, then the four
-  // wave sums).
+  // wave sums).  The counts are read 32 chunks at a time, all loads in flight together.
   int before = 0, total = 0;
   if (tid < E) {
-#pragma unroll 8
-    for (int q = 0; q < nchunks; ++q) {
-      const int v = counts[(size_t)q * E + tid];
-      before += q < c ? v : 0;
-      total += v;
+    for (int q0 = 0; q0 < nchunks; q0 += 32) {
+      int v[32];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) v[i] = q0 + i < nchunks ? counts[(size_t)(q0 + i) * E + tid] : 0;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        before += q0 + i < c ? v[i] : 0;
+        total += v[i];
+      }
     }
   }
   int incl = total;
@@ -69,14 +81,7 @@ __global__ __launch_bounds__(256) void dispatch_scatter_kernel(const int32_t* __
     if (lane >= d) incl += y;
   }
   if (lane == 63) wsum[wave] = incl;
-  const int begin = c * kChunk + 256 * wave;
-  int ev[4];
   unsigned long long same[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int i = begin + 64 * j + lane;
-    ev[j] = i < n ? ids[i] : -1;
-  }
   __syncthreads();
   // Lanes of one round with the same expert agree on every bit of the id.
 #pragma unroll

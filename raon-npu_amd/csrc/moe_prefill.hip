@@ -127,50 +127,84 @@ constexpr int kRouterTok = 32;
 // writes the quarter's partial logits plogits[q][t][e]; topk_kernel adds the quarters in
 // order.  (An expert's sums do not depend on which workgroup holds it, so the split over
 // experts, which gives small batches more workgroups, changes no result.)
-template <int NFR>
+template <int NFR, int NTB>
 __device__ __forceinline__ void router_gemm_block(const uint16_t* __restrict__ x, int T, int H,
                                                   const uint16_t* __restrict__ w, int E, float* __restrict__ plogits,
                                                   int bx, int by, int bz) {
   __shared__ float part[4][kRouterTok][NFR * 16 + 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lq = lane >> 4;
-  const int t0 = bx * kRouterTok, q = by, e0 = 16 * NFR * bz;
+  const int q = by, e0 = 16 * NFR * bz;
   const int nsteps = H / 32, sx = 4 * q + wave;
   const int k0 = (sx * nsteps / 16) * 32, kq = ((sx + 1) * nsteps / 16) * 32 - k0;
-  f32x4_t acc[2][NFR];
-#pragma unroll
-  for (int m = 0; m < 2; ++m)
-#pragma unroll
-    for (int f = 0; f < NFR; ++f) acc[m][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const uint16_t* xr[2];
-#pragma unroll
-  for (int m = 0; m < 2; ++m) xr[m] = x + (size_t)min(t0 + 16 * m + l16, T - 1) * H + k0 + 8 * lq;
   const uint16_t* wr = w + (size_t)(e0 + l16) * H + k0 + 8 * lq;
-#pragma unroll 2
-  for (int kk = 0; kk < kq; kk += 32) {
-    uint4 a[2], b[NFR];
+  // With NTB > 1 the workgroup takes NTB blocks of 32 tokens and keeps the router rows of
+  // its K slice (at most kRouterKeep steps of 32 columns) in registers across them, so
+  // the router is read once per NTB blocks.  A token's sums do not depend on the block.
+  constexpr int kRouterKeep = 4;
+  uint4 bk[NTB > 1 ? kRouterKeep : 1][NFR];
+  const bool keep = NTB > 1 && kq <= 32 * kRouterKeep;
+  if constexpr (NTB > 1) {
 #pragma unroll
-    for (int m = 0; m < 2; ++m) a[m] = *reinterpret_cast<const uint4*>(xr[m] + kk);
+    for (int st = 0; st < kRouterKeep; ++st)
 #pragma unroll
-    for (int f = 0; f < NFR; ++f) b[f] = *reinterpret_cast<const uint4*>(wr + (size_t)16 * f * H + kk);
-#pragma unroll
-    for (int f = 0; f < NFR; ++f)
-#pragma unroll
-      for (int m = 0; m < 2; ++m) acc[m][f] = mfma16(a[m], b[f], acc[m][f]);
+      for (int f = 0; f < NFR; ++f)
+        bk[st][f] = keep && 32 * st < kq ? *reinterpret_cast<const uint4*>(wr + (size_t)16 * f * H + 32 * st)
+                                          : make_uint4(0u, 0u, 0u, 0u);
   }
+  for (int tb = 0; tb < NTB; ++tb) {
+    const int t0 = (bx * NTB + tb) * kRouterTok;
+    if (t0 >= T) break;
+    f32x4_t acc[2][NFR];
 #pragma unroll
-  for (int m = 0; m < 2; ++m)
+    for (int m = 0; m < 2; ++m)
 #pragma unroll
-    for (int f = 0; f < NFR; ++f)
+      for (int f = 0; f < NFR; ++f) acc[m][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const uint16_t* xr[2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) part[wave][16 * m + 4 * lq + i][16 * f + l16] = acc[m][f][i];
-  __syncthreads();
-  constexpr int kCols = NFR * 16;
-  for (int idx = tid; idx < kRouterTok * kCols; idx += 256) {
-    const int r = idx / kCols, c = idx % kCols;
-    const int t = t0 + r;
-    if (t < T)
-      plogits[((size_t)q * T + t) * E + e0 + c] = ((part[0][r][c] + part[1][r][c]) + part[2][r][c]) + part[3][r][c];
+    for (int m = 0; m < 2; ++m) xr[m] = x + (size_t)min(t0 + 16 * m + l16, T - 1) * H + k0 + 8 * lq;
+    if (keep) {
+#pragma unroll
+      for (int st = 0; st < kRouterKeep; ++st) {
+        if (32 * st < kq) {
+          uint4 a[2];
+#pragma unroll
+          for (int m = 0; m < 2; ++m) a[m] = *reinterpret_cast<const uint4*>(xr[m] + 32 * st);
+#pragma unroll
+          for (int f = 0; f < NFR; ++f)
+#pragma unroll
+            for (int m = 0; m < 2; ++m) acc[m][f] = mfma16(a[m], bk[st][f], acc[m][f]);
+        }
+      }
+    } else {
+#pragma unroll 2
+      for (int kk = 0; kk < kq; kk += 32) {
+        uint4 a[2], b[NFR];
+#pragma unroll
+        for (int m = 0; m < 2; ++m) a[m] = *reinterpret_cast<const uint4*>(xr[m] + kk);
+#pragma unroll
+        for (int f = 0; f < NFR; ++f) b[f] = *reinterpret_cast<const uint4*>(wr + (size_t)16 * f * H + kk);
+#pragma unroll
+        for (int f = 0; f < NFR; ++f)
+#pragma unroll
+          for (int m = 0; m < 2; ++m) acc[m][f] = mfma16(a[m], b[f], acc[m][f]);
+      }
+    }
+    if (tb > 0) __syncthreads();  // the previous block's sums have been read from part
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int f = 0; f < NFR; ++f)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[wave][16 * m + 4 * lq + i][16 * f + l16] = acc[m][f][i];
+    __syncthreads();
+    constexpr int kCols = NFR * 16;
+    for (int idx = tid; idx < kRouterTok * kCols; idx += 256) {
+      const int r = idx / kCols, c = idx % kCols;
+      const int t = t0 + r;
+      if (t < T)
+        plogits[((size_t)q * T + t) * E + e0 + c] = ((part[0][r][c] + part[1][r][c]) + part[2][r][c]) + part[3][r][c];
+    }
   }
 }
 
@@ -388,7 +422,7 @@ __global__ __launch_bounds__(256) void prep_x_kernel(const uint16_t* __restrict_
 // The router GEMM and the activation-row preparation (both read only x) in one launch:
 // workgroups 0..n_router-1 are router workgroups (token block, K quarter, expert group),
 // the rest prepare four rows each.  One launch fewer on the routing's critical path.
-template <int NFR>
+template <int NFR, int NTB>
 __global__ __launch_bounds__(256) void router_prep_kernel(const uint16_t* __restrict__ x, int T, int H,
                                                           const uint16_t* __restrict__ w, int E,
                                                           float* __restrict__ plogits, int n_router, int ngroups,
@@ -397,7 +431,7 @@ __global__ __launch_bounds__(256) void router_prep_kernel(const uint16_t* __rest
                                                           int nzero) {
   const int b = blockIdx.x;
   if (b < n_router) {
-    router_gemm_block<NFR>(x, T, H, w, E, plogits, b / (4 * ngroups), (b / ngroups) % 4, b % ngroups);
+    router_gemm_block<NFR, NTB>(x, T, H, w, E, plogits, b / (4 * ngroups), (b / ngroups) % 4, b % ngroups);
   } else {
     // The preparation workgroups also clear nzero ints at zero (the top-k's chunk counts).
     const int pb = b - n_router;
@@ -1455,15 +1489,20 @@ hipError_t launch_router_prep(const uint16_t* x, int T, int H, const uint16_t* w
   // then the preparation workgroups of four rows.
   const int nfr = E / 16 <= 4 ? E / 16 : (E / 16) % 4 == 0 ? 4 : (E / 16) % 3 == 0 ? 3 : (E / 16) % 2 == 0 ? 2 : 1;
   const int ngroups = (E / 16) / nfr;
-  const int n_router = (T + kRouterTok - 1) / kRouterTok * 4 * ngroups;
+  // Large batches: four blocks of 32 tokens per router workgroup, the router rows kept in
+  // registers across them (every K slice then has at most 4 steps of 32: H <= 2048);
+  // small batches keep one block per workgroup for more workgroups.
+  const int ntb = T >= 2048 && H <= 2048 ? 4 : 1;
+  const int n_router = (T + ntb * kRouterTok - 1) / (ntb * kRouterTok) * 4 * ngroups;
   const dim3 grid((unsigned)(n_router + (T + 3) / 4)), block(256);
-  switch (nfr) {
-#define RMOE_ROUTER_CASE(n)                                                                                   \
-  case n:                                                                                                     \
-    hipLaunchKernelGGL(router_prep_kernel<n>, grid, block, 0, st, x, T, H, w, E, logits, n_router, ngroups, xh, xe, \
-                       xsum, zero, nzero);                                                                    \
+  switch (nfr * 8 + ntb) {
+#define RMOE_ROUTER_CASE(n, tb)                                                                                 \
+  case n * 8 + tb:                                                                                              \
+    hipLaunchKernelGGL((router_prep_kernel<n, tb>), grid, block, 0, st, x, T, H, w, E, logits, n_router, ngroups, xh, \
+                       xe, xsum, zero, nzero);                                                                  \
     break;
-    RMOE_ROUTER_CASE(1) RMOE_ROUTER_CASE(2) RMOE_ROUTER_CASE(3) RMOE_ROUTER_CASE(4)
+    RMOE_ROUTER_CASE(1, 1) RMOE_ROUTER_CASE(2, 1) RMOE_ROUTER_CASE(3, 1) RMOE_ROUTER_CASE(4, 1)
+    RMOE_ROUTER_CASE(1, 4) RMOE_ROUTER_CASE(2, 4) RMOE_ROUTER_CASE(3, 4) RMOE_ROUTER_CASE(4, 4)
 #undef RMOE_ROUTER_CASE
     default:
       return hipErrorInvalidValue;
