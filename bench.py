@@ -722,6 +722,38 @@ def timeline(lib_path: Path, seed: int) -> int:
     for (ev, name), (med, mx) in zip(TIMELINE_EVENTS, m):
         print(f"{name:44s} {med:9.2f} {mx:9.2f}")
     print(f"{'next layer first ready':44s} {np.mean(nxt):9.2f}", flush=True)
+    # The same events per workgroup role (the unit dealing of the stack kernel: workgroup g
+    # holds GU unit g when g < n_gu, GU units of the shared slot are the last nhb of them, and
+    # the combiner of band b is the workgroup whose first DN unit is (slot 0, band b), i.e.
+    # workgroup (n_gu + b) mod G).
+    geom = BASELINE
+    S, nhb, nb2 = geom.top_k + geom.n_shared, geom.inter // 32, geom.hidden // 64
+    n_gu = S * nhb
+    G = int((b[1, :, 0] > 0).sum())
+    comb = {(n_gu + i) % G for i in range(nb2)}
+    roles = [
+        ("gate/up, routed slot", [w for w in range(G) if w < n_gu - nhb]),
+        ("gate/up, shared slot (from LDS)", [w for w in range(G) if n_gu - nhb <= w < n_gu]),
+        ("band combiners (no gate/up)", [w for w in range(G) if w >= n_gu and w in comb]),
+        ("others (one down unit only)", [w for w in range(G) if w >= n_gu and w not in comb]),
+    ]
+    print("per workgroup role: median / max over the role's workgroups, averaged over layers 1..46")
+    for rname, wgs in roles:
+        if not wgs:
+            continue
+        print(f"  {rname} ({len(wgs)} workgroups)")
+        for ev, name in TIMELINE_EVENTS:
+            med, mx = [], []
+            for l in range(1, nl - 1):
+                t0 = b[l, :, 0][b[l, :, 0] > 0].min()
+                v = b[l, wgs, ev]
+                v = v[v > 0]
+                if len(v):
+                    med.append((np.median(v) - t0) / 100.0)
+                    mx.append((v.max() - t0) / 100.0)
+            if med:
+                print(f"    {name:42s} {np.mean(med):9.2f} {np.mean(mx):9.2f}")
+    sys.stdout.flush()
     ctx.close()
     return 0
 
