@@ -66,14 +66,31 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
                                          false);
 }
 
+// (x & m) | o as one v_and_or_b32.  m and o come from q4_unpack_consts(), in VGPRs: a VOP3
+// instruction takes no literal on gfx9, so with the masks as literals the compiler emits a
+// v_and_b32 and a v_or_b32 (two VOP2 instructions with literals) instead.
+__device__ __forceinline__ uint32_t q4_and_or(uint32_t x, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(o));
+  return r;
+}
+// The two masks of unpack_codes in VGPRs.  Not volatile: the compiler merges the copies of
+// every call and hoists them out of loops.
+__device__ __forceinline__ void q4_unpack_consts(uint32_t& mask, uint32_t& one) {
+  asm("v_mov_b32 %0, 0x780078" : "=v"(mask));
+  asm("v_mov_b32 %0, 0x3f803f80" : "=v"(one));
+}
+
 // Codes of one dword -> four bf16 pairs with values 1 + n/16 (n in 0..15, exact).
-// Pair q covers nibbles q and q+4, i.e. columns (8d+2q, 8d+2q+1).
+// Pair q covers nibbles q and q+4, i.e. columns (8d+2q, 8d+2q+1).  Two VALU instructions
+// per pair: a shift and a v_and_or_b32 (masked nibble pair | the bf16 pair 1.0, 1.0).
 __device__ __forceinline__ void unpack_codes(uint32_t v, uint32_t& p0, uint32_t& p1, uint32_t& p2, uint32_t& p3) {
-  const uint32_t mask = 0x00780078u, one = 0x3F803F80u;
-  p0 = ((v << 3) & mask) | one;
-  p1 = ((v >> 1) & mask) | one;
-  p2 = ((v >> 5) & mask) | one;
-  p3 = ((v >> 9) & mask) | one;
+  uint32_t mask, one;  // 0x00780078, 0x3F803F80
+  q4_unpack_consts(mask, one);
+  p0 = q4_and_or(v << 3, mask, one);
+  p1 = q4_and_or(v >> 1, mask, one);
+  p2 = q4_and_or(v >> 5, mask, one);
+  p3 = q4_and_or(v >> 9, mask, one);
 }
 
 // Partial dot of one group: D' = sum_c (1 + n_c/16) * x_c over 32 columns, x as 16
