@@ -329,7 +329,7 @@ def configs_bench(ctx, layers, geom, seed: int, stream, weights_d: bool = True) 
     out["config1_gemv"] = {"workload": "q4nx GEMV [768, 2048] x 1 token, 1000 launches in a graph",
                            "us_per_launch": round(us, 3), "GBps": round(b / us / 1e3, 1),
                            "frac_hbm_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
-                           "roofline": roofline("hbm", b, us / 1e6, "linear_wave_kernel<16>", "launch",
+                           "roofline": roofline("hbm", b, us / 1e6, "linear_lane_kernel<16>", "launch",
                                                 CONFIG_TRAFFIC_BYTES["config1_gemv"])}
     out["_config1_bytes"] = wl.mat.download()
     us = graph_us(wl.config2, 200, stream)

@@ -220,66 +220,54 @@ __global__ __launch_bounds__(1024) void linear_band_kernel(LinearArgs a) {
   }
 }
 
-// One wave per workgroup for one token of a small matrix with few K tiles (nkt = K/128
-// in {4, 8, 16, 32}): the wave covers R = 64 / nkt rows over all of K, lane l taking row
-// l % R of K tile
-// l / R (five 16-byte loads).  x is staged in the wave's LDS with no workgroup barrier,
-// the tiles' sums meet by shuffles in a fixed order (xor R, 2R, ..., 32), and lanes
-// 0..R-1 store the rows.  A launch-latency-bound GEMV (a few hundred KB of weights) then
-// has no cross-wave synchronisation at all, and the grid has M / R workgroups.
+// One token of a small matrix without LDS: lane (q, r) of a wave takes row row0 + r and half
+// hf = q & 1 of K tile kt = q >> 1 (groups 2hf and 2hf + 1: two 16-byte code words and
+// their two scale|min words).  It loads its 64 columns of x straight from memory (the R
+// lanes of one half share the addresses) and takes their group sums S on v_dot2 against
+// the pair (1.0, 1.0).  The 2 NKT lanes of a row add their partial sums by shuffles in a
+// fixed order; R = 64 / (2 NKT) rows per wave.  Half the dot-product work per lane of
+// a one-lane-per-tile form, and no x staging in LDS or wave barrier.
 template <int NKT>
-__global__ __launch_bounds__(64) void linear_wave_kernel(LinearArgs a) {
-  constexpr int R = 64 / NKT;
-  constexpr int kXDw = NKT * 64 + 4;  // dwords of x per token in LDS (bf16 pairs, padded)
-  __shared__ __attribute__((aligned(16))) uint32_t xs[kNT][kXDw];
-  __shared__ float ssum[kNT][NKT * 4];
+__global__ __launch_bounds__(64) void linear_lane_kernel(LinearArgs a) {
+  constexpr int R = 32 / NKT;
   const int lane = threadIdx.x;
   const int row0 = blockIdx.x * R;
-  const int tok0 = blockIdx.y * kNT;
-  const int nt = min(kNT, a.T - tok0);
-  const int kt = lane / R, r = lane % R;
+  const int q = lane / R, r = lane % R, kt = q >> 1, hf = q & 1;
   const uint8_t* tile =
       a.tiles + ((size_t)(row0 / kTileRows) * NKT + kt) * kTileBytes + (size_t)(row0 % kTileRows + r) * 16;
-  uint4 c[4];
+  const uint4 c0 = load_stream16(tile + (2 * hf) * 1024);
+  const uint4 c1 = load_stream16(tile + (2 * hf + 1) * 1024);
+  const uint2 smv = *reinterpret_cast<const uint2*>(tile + kCodeBytes + 8 * hf);
+  const uint4* xp = reinterpret_cast<const uint4*>(a.x) + (kt * 128 + hf * 64) / 8;
+  uint4 xv[8];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) c[j] = load_stream16(tile + j * 1024);
-  const uint4 smq = load_stream16(tile + kCodeBytes);
-  // x: 16-byte unit u of token t at lane u % 64, pass u / 64; the four units of a group are
-  // held by four neighbouring lanes, whose sums meet by two shuffles.
-  constexpr int kUnits = NKT * 16;
+  for (int i = 0; i < 8; ++i) xv[i] = xp[i];
+  uint32_t mask, one;
+  q4_unpack_consts(mask, one);
+  float acc = 0.f;
 #pragma unroll
-  for (int t = 0; t < kNT; ++t) {
-    if (t < nt) {
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t cw[4] = {j ? c1.x : c0.x, j ? c1.y : c0.y, j ? c1.z : c0.z, j ? c1.w : c0.w};
+    float d = 0.f, s = 0.f;
 #pragma unroll
-      for (int pass = 0; pass < kUnits / 64; ++pass) {
-        const int u = pass * 64 + lane;
-        const uint4 v = reinterpret_cast<const uint4*>(a.x + (size_t)(tok0 + t) * a.K)[u];
-        *reinterpret_cast<uint4*>(&xs[t][4 * u]) = v;
-        float sv = ((bf16_to_f32(v.x & 0xffffu) + bf16_to_f32(v.x >> 16)) +
-                    (bf16_to_f32(v.y & 0xffffu) + bf16_to_f32(v.y >> 16))) +
-                   ((bf16_to_f32(v.z & 0xffffu) + bf16_to_f32(v.z >> 16)) +
-                    (bf16_to_f32(v.w & 0xffffu) + bf16_to_f32(v.w >> 16)));
-        sv += __shfl_xor(sv, 1, 64);
-        sv += __shfl_xor(sv, 2, 64);
-        if ((u & 3) == 0) ssum[t][u >> 2] = sv;
-      }
+    for (int dd = 0; dd < 4; ++dd) {
+      uint32_t p0, p1, p2, p3;
+      unpack_codes(cw[dd], p0, p1, p2, p3);
+      const uint4 x4 = xv[4 * j + dd];
+      d = dot2_bf16(p0, x4.x, d);
+      d = dot2_bf16(p1, x4.y, d);
+      d = dot2_bf16(p2, x4.z, d);
+      d = dot2_bf16(p3, x4.w, d);
+      s = dot2_bf16(one, x4.x, s);
+      s = dot2_bf16(one, x4.y, s);
+      s = dot2_bf16(one, x4.z, s);
+      s = dot2_bf16(one, x4.w, s);
     }
+    acc = group_apply(j ? smv.y : smv.x, d, s, acc);
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const uint32_t sm[4] = {smq.x, smq.y, smq.z, smq.w};
 #pragma unroll
-  for (int t = 0; t < kNT; ++t) {
-    if (t < nt) {
-      float acc = 0.f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc = group_apply(sm[j], group_dot(c[j], &xs[t][kt * 64 + j * 16]), ssum[t][kt * 4 + j], acc);
-#pragma unroll
-      for (int m = R; m < 64; m *= 2) acc += __shfl_xor(acc, m, 64);
-      if (lane < R) a.y[(size_t)(tok0 + t) * a.M + row0 + lane] = (uint16_t)f32_to_bf16(acc);
-    }
-  }
+  for (int m = R; m < 64; m *= 2) acc += __shfl_xor(acc, m, 64);
+  if (lane < R) a.y[row0 + lane] = (uint16_t)f32_to_bf16(acc);
 }
 
 }  // namespace
@@ -289,16 +277,17 @@ hipError_t launch_linear(const uint8_t* tiles, int M, int K, const uint16_t* x, 
   const int nkt = K / kTileCols, n_rt = M / kTileRows;
   const int ychunks = (T + kNT - 1) / kNT;
   // One token of a small matrix (fewer than 32 row bands) with 4..32 K tiles: one wave
-  // per workgroup (config 1: 3.32 -> 3.12 us per launch in a graph).  With more tokens the
-  // wave's per-token chains run one after another; the band kernel is faster there.
+  // per workgroup, two lanes per K tile of a row (config 1: 3.05 -> 2.07 us per launch in
+  // a graph against one lane per K tile with x staged in LDS).  With more tokens the band
+  // kernel is faster.
   if (T == 1 && n_rt < 32 && (nkt == 4 || nkt == 8 || nkt == 16 || nkt == 32) &&
       (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
     LinearArgs a{tiles, M, K, x, T, y, nullptr, nullptr, 1};
-    const dim3 grid(M / (64 / nkt), ychunks), block(64);
-    if (nkt == 4) hipLaunchKernelGGL(linear_wave_kernel<4>, grid, block, 0, st, a);
-    else if (nkt == 8) hipLaunchKernelGGL(linear_wave_kernel<8>, grid, block, 0, st, a);
-    else if (nkt == 16) hipLaunchKernelGGL(linear_wave_kernel<16>, grid, block, 0, st, a);
-    else hipLaunchKernelGGL(linear_wave_kernel<32>, grid, block, 0, st, a);
+    const dim3 grid(M / (32 / nkt)), block(64);
+    if (nkt == 4) hipLaunchKernelGGL(linear_lane_kernel<4>, grid, block, 0, st, a);
+    else if (nkt == 8) hipLaunchKernelGGL(linear_lane_kernel<8>, grid, block, 0, st, a);
+    else if (nkt == 16) hipLaunchKernelGGL(linear_lane_kernel<16>, grid, block, 0, st, a);
+    else hipLaunchKernelGGL(linear_lane_kernel<32>, grid, block, 0, st, a);
     return hipGetLastError();
   }
   // The band kernel reads x in 16-byte pieces; other x take the K-split kernel.

@@ -92,3 +92,45 @@ def test_gemv_extreme_inputs(gpu_ctx):
         rel = np.abs(om.bf16_to_f32(y[t]) - om.bf16_to_f32(ref)) / np.maximum(np.abs(om.bf16_to_f32(ref)), 1e-30)
         assert np.mean(a == b) >= 0.95 and np.median(rel) < 1e-2
     mat.free()
+
+
+# One token of a matrix with fewer than 32 row bands and 4, 8, 16 or 32 K tiles runs
+# linear_lane_kernel (two lanes per K tile, x straight from memory, group sums on v_dot2).
+@pytest.mark.parametrize("M,K", [(128, 512), (256, 1024), (128, 4096), (1920, 2048), (384, 2048)])
+def test_gemv_single_token_lane_kernel(gpu_ctx, M, K):
+    blob, wf, rng = _case(M, K, M * 11 + K)
+    x = f32_to_bf16(rng.standard_normal((1, K)).astype(np.float32))
+    mat = gpu_ctx.upload_matrix(blob, M, K)
+    y = mat.linear(x)
+    ref = om.linear(wf, x[0])[None]
+    err, rel, same = compare_bf16(y, ref)
+    assert err <= 1e-2 and rel <= 1e-3 and same >= 0.99, (err, rel, same)
+    mat.free()
+
+
+def test_gemv_single_token_extreme_inputs(gpu_ctx):
+    # The extreme rows of test_gemv_extreme_inputs, one token per call (the lane kernel).
+    M, K = 128, 512
+    rng = np.random.default_rng(23)
+    w = rng.normal(0, 1.0, (M, K)).astype(np.float32)
+    w[:8] = 0.0
+    c, s, m = quantize(w)
+    mat = gpu_ctx.upload_matrix(pack_gemv(c, s, m), M, K)
+    wf = dequantize_simple(c, s, m)
+    rows = [np.zeros(K, np.uint16), f32_to_bf16(np.full(K, 3.0e3, np.float32)),
+            f32_to_bf16(rng.standard_normal(K).astype(np.float32) * 1e-20)]
+    alt = np.zeros(K, np.uint16)
+    alt[::2] = f32_to_bf16(np.ones(K // 2, np.float32))
+    alt[1::2] = f32_to_bf16(-np.ones(K // 2, np.float32))
+    rows.append(alt)
+    for t, xr in enumerate(rows):
+        y = mat.linear(xr[None])[0]
+        ref = om.linear(wf, xr)
+        if t == 0:
+            assert np.all(y == 0)
+            continue
+        a = y.view(np.int16).astype(np.int32)
+        b = ref.view(np.int16).astype(np.int32)
+        rel = np.abs(om.bf16_to_f32(y) - om.bf16_to_f32(ref)) / np.maximum(np.abs(om.bf16_to_f32(ref)), 1e-30)
+        assert np.mean(a == b) >= 0.95 and np.median(rel) < 1e-2, t
+    mat.free()
