@@ -46,6 +46,7 @@ constexpr int kMaxE = 256;
 constexpr int kMaxSlots = 17;
 constexpr int kMaxDnPos = 4;      // DN tiles per DN wave (waves 1..7, both units): Ipad <= 1792
 constexpr int kMaxDnUnits = 2;    // DN units per workgroup and layer (prefetched)
+static_assert(kMaxDnUnits == 2, "the unit indices are read as one int4");
 constexpr int kLRow = 4096;       // floats of partial logits copied into LDS at a time
 // LDS rows of partial logits are Ep + kLPad floats apart: band b starts at bank 16 b mod 64,
 // so the four bands that one instruction reads (see the sum below) fall in four distinct
@@ -605,7 +606,8 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
   // This workgroup's first GU unit (slot, half band) and its DN units (slot, band; -1
   // when absent).  The same in every layer; kept in LDS so that the index arithmetic does
   // not hold registers across the layer loop.  epoch_s: this launch's epoch.
-  __shared__ int gu_d[2], dn_d[kMaxDnUnits][2];
+  __shared__ int gu_d[2];
+  __shared__ __attribute__((aligned(16))) int dn_d[kMaxDnUnits][2];
   __shared__ uint32_t epoch_s;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1024,8 +1026,10 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
       // The combiner of band b is the workgroup whose first DN unit is (slot 0, band b):
       // slot 0's units are units 0..nb2-1, and unit v is the first unit of workgroup
       // (n_gu + v) mod G, so every band has exactly one.
-      const bool comb = dn_d[0][0] == 0;
-      const int cb = dn_d[0][1];
+      // (slot, band) of both units in one LDS read.
+      const int4 ud = *reinterpret_cast<const int4*>(&dn_d[0][0]);
+      const bool comb = ud.x == 0;
+      const int cb = ud.y;
       // The next layer's router weights of the combined band, copied into the DN tiles'
       // LDS (every wave is done with the tiles) by waves 1..7 while wave 0 hands d over.
       // They are drained before the logits.
@@ -1034,21 +1038,28 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
       // d of both units as tagged words: no store acknowledgement and no counter; the
       // combiner of the band polls them.  A combiner keeps the d of its own units of its
       // band in LDS instead (own: their slot bits), so it polls only the other slots.
+      // The eight waves' partial sums of both units are read first, all at once (their
+      // LDS latencies overlap instead of following each other), then added in wave order.
       unsigned own = 0u;
       if (wave == 0) {
+        float pw[kMaxDnUnits][kWaves];
+#pragma unroll
+        for (int d = 0; d < kMaxDnUnits; ++d)
+#pragma unroll
+          for (int w = 0; w < kWaves; ++w) pw[d][w] = red[w][d][lane];
 #pragma unroll
         for (int d = 0; d < kMaxDnUnits; ++d) {
-          if (dn_d[d][0] < 0) continue;
+          const int us = d == 0 ? ud.x : ud.z, ub = d == 0 ? ud.y : ud.w;
+          if (us < 0) continue;
           float dd = 0.f;
 #pragma unroll
-          for (int w = 0; w < kWaves; ++w) dd += red[w][d][lane];
+          for (int w = 0; w < kWaves; ++w) dd += pw[d][w];
           const float v = bf16_round(dd);
-          if (comb && dn_d[d][1] == cb) {
-            cmb[dn_d[d][0]][lane] = v;
-            own |= 1u << dn_d[d][0];
+          if (comb && ub == cb) {
+            cmb[us][lane] = v;
+            own |= 1u << us;
           } else {
-            st_dev_u64(&dtag[(size_t)dn_d[d][0] * a.H + 64 * dn_d[d][1] + lane],
-                       (uint64_t)__float_as_uint(v) | ((uint64_t)tag << 32));
+            st_dev_u64(&dtag[(size_t)us * a.H + 64 * ub + lane], (uint64_t)__float_as_uint(v) | ((uint64_t)tag << 32));
           }
         }
       }
@@ -1113,26 +1124,40 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
         RMOE_STAMP(l, g, 9, 0);
         if (wave == 0) {
           // Ascending expert id: the slot order, then each slot's value and weight, read
-          // from LDS in batches, then summed in order.
-          float acc2 = 0.f;
-          for (int r0 = 0; r0 < a.k; r0 += 8) {
-            int o8[8];
-            float c8[8], w8[8];
+          // from LDS in batches, then summed in order.  The shared slot's d is read with
+          // the first batch.
+          // The first eight slots come straight from the operands read before the wait,
+          // with no branch per slot: a slot past k adds +0 (acc2 starts at +0, so the sum
+          // is unchanged bit for bit).  Slots 8.. (k > 8) follow in batches of 8.
+          const float dsh = a.S > a.k ? cmb[a.k][lane] : 0.f;
+          float c8[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) o8[i] = r0 == 0 ? o8p[i] : (r0 + i < a.k ? sl.ord[r0 + i] : 0);
+          for (int i = 0; i < 8; ++i) c8[i] = cmb[o8p[i]][lane];
+          float acc2 = 0.f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float p = __fmul_rn(c8[i], w8p[i]);
+            acc2 = __fadd_rn(acc2, i < a.k ? p : 0.f);
+          }
+          for (int r0 = 8; r0 < a.k; r0 += 8) {
+            int o8[8];
+            float w8[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o8[i] = r0 + i < a.k ? sl.ord[r0 + i] : 0;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
               c8[i] = cmb[o8[i]][lane];
-              w8[i] = r0 == 0 ? w8p[i] : sl.w[o8[i]];
+              w8[i] = sl.w[o8[i]];
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i)
               if (r0 + i < a.k) acc2 = __fadd_rn(acc2, __fmul_rn(c8[i], w8[i]));
           }
           uint32_t o = f32_to_bf16(acc2);
-          if (a.S > a.k) o = f32_to_bf16(__fadd_rn(bf16_to_f32(o), cmb[a.k][lane]));
+          if (a.S > a.k) o = f32_to_bf16(__fadd_rn(bf16_to_f32(o), dsh));
           if (a.residual) o = f32_to_bf16(__fadd_rn(bf16_to_f32(xres), bf16_to_f32(o)));
-          const uint32_t hi = __shfl_down(o, 1, 64);
+          // The odd neighbour's value (lane ^ 1) by a DPP move, no LDS round trip.
+          const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)o, 0xB1, 0xF, 0xF, false);
           if ((lane & 1) == 0) xband[lane >> 1] = o | (hi << 16);
           if (l + 1 == a.L) {
             a.out[row] = (uint16_t)o;
