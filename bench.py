@@ -35,13 +35,12 @@ sys.path.insert(0, str(ROOT))
 STACK_HIDDEN_STD = 0.25
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
-# HBM bytes per launch of the decode stack kernel measured with rocprofv3 FETCH_SIZE and
-# WRITE_SIZE (calibrated against a 512 MiB copy) over `bench.py --profile-pass`; the
-# summary and commands are in profiles/decode_prefill_hbm_counters.txt.  Re-measure
-# after changing the kernel.
+# HBM bytes per launch of the decode stack kernel and of the lm_head GEMV: each run
+# measures them itself (measure_traffic: rocprofv3 FETCH_SIZE and WRITE_SIZE passes over
+# child `bench.py --profile-pass` runs, calibrated against a 512 MiB copy).  These are the
+# figures of the committed counter profile (profiles/decode_prefill_hbm_counters.txt),
+# reported instead only when rocprofv3 is absent, a pass fails, or --no-traffic is given.
 DECODE_TRAFFIC_BYTES = 1341868544
-# HBM bytes per lm_head GEMV launch from the same counter passes (1.001x its 749,076,480
-# algorithmic bytes).
 LM_HEAD_TRAFFIC_BYTES = 749777961
 
 
@@ -65,6 +64,9 @@ def parse_args():
     ap.add_argument("--no-lm-head", action="store_true", help="skip the lm_head bfp16 GEMV measurement")
     ap.add_argument("--no-configs", action="store_true", help="skip configs 1-3 and the weights-d layer")
     ap.add_argument("--no-weights-d", action="store_true", help="skip the weights-d layer rows of 'configs'")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the in-run rocprofv3 FETCH_SIZE/WRITE_SIZE passes (roofline.traffic then comes "
+                         "from the committed counter profile)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="short run for hardware counters: 2 decode launches, 1 prefill layer and a "
                          "512 MiB device copy (the calibration kernel of known size); prints no JSON")
@@ -633,6 +635,81 @@ def profile_pass(ctx, layers, geom, args, stream, gen) -> int:
     return 0
 
 
+def _counter_pass(counter: str, out_dir: Path, extra_args: list[str], timeout_s: float) -> dict | None:
+    """One rocprofv3 counter pass over a child `bench.py --profile-pass` (this script, run
+    as a separate process; this process only waits).  Returns {kernel kind: [per-dispatch
+    counter sums]} for the calibration copy ("copy"), the decode stack ("stack") and the
+    lm_head GEMV ("lm_head"), or None when the pass did not produce its CSV."""
+    import csv
+    import subprocess
+    from collections import defaultdict
+
+    cmd = ["rocprofv3", "--pmc", counter, "--kernel-include-regex", "decode_stack|linear_bfp16|copy|Copy",
+           "--output-format", "csv", "-d", str(out_dir), "-o", "run", "--",
+           sys.executable, str(ROOT / "bench.py"), "--profile-pass", "--no-prefill"] + extra_args
+    try:
+        proc = subprocess.run(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.PIPE, timeout=timeout_s)
+    except (OSError, subprocess.TimeoutExpired) as e:
+        log(f"traffic pass {counter}: {type(e).__name__}: {e}")
+        return None
+    csvs = sorted(out_dir.rglob("run_counter_collection.csv"))
+    if not csvs:
+        log(f"traffic pass {counter}: rocprofv3 exited {proc.returncode} without counter output")
+        return None
+    per = defaultdict(float)
+    names = {}
+    with open(csvs[0], newline="") as f:
+        for row in csv.DictReader(f):
+            if row.get("Counter_Name") != counter:
+                continue
+            d = int(row["Dispatch_Id"])
+            per[d] += float(row["Counter_Value"])
+            names[d] = row["Kernel_Name"]
+    out = {"copy": [], "stack": [], "lm_head": []}
+    for d in sorted(per):
+        n = names[d]
+        kind = "stack" if "decode_stack" in n else "lm_head" if "linear_bfp16" in n else "copy"
+        out[kind].append(per[d])
+    # rocprofv3 can end with a fault of its own after a complete run; complete CSVs count.
+    return out if out["copy"] and out["stack"] else None
+
+
+def measure_traffic(args) -> dict | None:
+    """HBM bytes per launch of the decode stack and of the lm_head GEMV, measured in this
+    run: rocprofv3 FETCH_SIZE, then WRITE_SIZE, each over a child `bench.py --profile-pass`
+    (a 512 MiB device copy twice, two decode launches of the 48-layer stack, the lm_head
+    GEMV), each scaled by what the same counter reads for the copy of known size (512 MiB
+    read, 512 MiB written).  None when rocprofv3 is absent or a pass fails."""
+    import shutil
+    import statistics
+    import tempfile
+
+    if shutil.which("rocprofv3") is None:
+        log("traffic: rocprofv3 not found; roofline.traffic falls back to the committed figure")
+        return None
+    extra = ["--seed", str(args.seed), "--layers", str(args.layers)] + (["--no-lm-head"] if args.no_lm_head else [])
+    res = {}
+    with tempfile.TemporaryDirectory(prefix="rmoe_traffic_") as td:
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            r = _counter_pass(counter, Path(td) / counter, extra, 180.0)
+            if r is None:
+                return None
+            # The two calibration copies are the largest "copy" dispatches of the pass
+            # (the stack build's dtype conversions are small ones).
+            copy_bytes = 512 * 1024 * 1024
+            factor = copy_bytes / statistics.median(sorted(r["copy"])[-2:])
+            res[counter] = {k: statistics.median(v) * factor for k, v in r.items() if v}
+            res[counter]["factor_bytes_per_unit"] = factor
+    out = {
+        "stack": res["FETCH_SIZE"]["stack"] + res["WRITE_SIZE"]["stack"],
+        "fetch_factor": res["FETCH_SIZE"]["factor_bytes_per_unit"],
+        "write_factor": res["WRITE_SIZE"]["factor_bytes_per_unit"],
+    }
+    if "lm_head" in res["FETCH_SIZE"] and "lm_head" in res["WRITE_SIZE"]:
+        out["lm_head"] = res["FETCH_SIZE"]["lm_head"] + res["WRITE_SIZE"]["lm_head"]
+    return out
+
+
 # Timeline stamps of the decode stack's timeline build (event index, meaning); the
 # product library has none.  One wave per workgroup stores s_memrealtime (100 MHz).
 TIMELINE_EVENTS = [
@@ -883,6 +960,24 @@ def main() -> int:
     elif configs:
         configs.pop("_config1_bytes", None)
 
+    # HBM traffic per launch, measured in this run by counter passes over child processes
+    # (this process holds its buffers and waits); the committed figures otherwise.
+    traffic, traffic_src = (DECODE_TRAFFIC_BYTES if args.layers == 48 else None), "committed counter profile"
+    if not args.no_traffic and args.layers == 48:
+        torch.cuda.synchronize()
+        t_tr = time.perf_counter()
+        tr = measure_traffic(args)
+        if tr is not None:
+            traffic, traffic_src = int(tr["stack"]), "rocprofv3 FETCH_SIZE + WRITE_SIZE, this run"
+            if lm_head is not None and "lm_head" in tr:
+                lm_head["traffic"] = int(tr["lm_head"])
+                lm_head["traffic_source"] = traffic_src
+            log(f"traffic: decode stack {traffic / 1e9:.4f} GB per launch ({traffic / nbytes:.3f}x the algorithmic "
+                f"bytes), factors {tr['fetch_factor']:.1f} / {tr['write_factor']:.1f} B per counter unit, "
+                f"{time.perf_counter() - t_tr:.0f} s")
+    if lm_head is not None and "traffic_source" not in lm_head:
+        lm_head["traffic_source"] = "committed counter profile"
+
     line = {
         "metric": "MoE decode tokens/s (48-layer q4nx stack, batch 1); prefill grouped-GEMM TFLOP/s in 'prefill'",
         "value": round(tok_s, 2),
@@ -915,7 +1010,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": DECODE_TRAFFIC_BYTES if args.layers == 48 else None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "bytes_per_launch": nbytes,
             "us_per_launch": round(per_launch * 1e6, 3),
         },
