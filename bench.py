@@ -40,7 +40,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 # child `bench.py --profile-pass` runs, calibrated against a 512 MiB copy).  These are the
 # figures of the committed counter profile (profiles/decode_prefill_hbm_counters.txt),
 # reported instead only when rocprofv3 is absent, a pass fails, or --no-traffic is given.
-DECODE_TRAFFIC_BYTES = 1341868544
+DECODE_TRAFFIC_BYTES = 1338292512
 LM_HEAD_TRAFFIC_BYTES = 749777961
 
 

@@ -231,7 +231,11 @@ template <int NKT>
 __global__ __launch_bounds__(64) void linear_lane_kernel(LinearArgs a) {
   constexpr int R = 32 / NKT;
   const int lane = threadIdx.x;
-  const int row0 = blockIdx.x * R;
+  // Workgroups are dealt round robin to the 8 XCDs: XCD x takes a contiguous eighth of the
+  // rows, so the workgroups that share a 128-byte line of a tile (its 16-byte row pieces)
+  // share an L2 (grid = M / R, a multiple of 8).
+  const int wg = blockIdx.x, per_xcd = gridDim.x / 8;
+  const int row0 = ((wg % 8) * per_xcd + wg / 8) * R;
   const int q = lane / R, r = lane % R, kt = q >> 1, hf = q & 1;
   const uint8_t* tile =
       a.tiles + ((size_t)(row0 / kTileRows) * NKT + kt) * kTileBytes + (size_t)(row0 % kTileRows + r) * 16;
