@@ -153,7 +153,7 @@ __global__ __launch_bounds__(256) void linear_bfp16_kernel(B16Args a) {
   const int per = (nkt + a.ksplit - 1) / a.ksplit;
   const int kt0 = ks * per;
   const int nrange = max(0, min(per, nkt - kt0));
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int nwaves = blockDim.x >> 6;
 
   const int xstride = per * 64;

@@ -133,7 +133,7 @@ __device__ void route_select(const RouteArgs& a, int t) {
 __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   __shared__ unsigned last_flag;
   const int t = blockIdx.y;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int e = blockIdx.x * kRouteExpertsPerBlock + wave;
   if (e < a.E) {
     const uint32_t* wr = reinterpret_cast<const uint32_t*>(a.w + (size_t)e * a.H);
@@ -268,7 +268,7 @@ __global__ __launch_bounds__(1024) void decode_gate_up_band_kernel(DecodeArgs a0
   const int groups = a.I / R;
   const int s = blockIdx.x / groups, u0 = (blockIdx.x % groups) * R;
   const int band = u0 / kTileRows, rsub = u0 % kTileRows;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), nwaves = blockDim.x >> 6;
   const int g = lane / R, r = lane % R;
   const int e = slot_expert(a, s);
   const uint8_t* W = a.gu + (size_t)e * a.gu_bytes;
@@ -345,7 +345,7 @@ __global__ __launch_bounds__(1024) void decode_down_band_kernel(DecodeArgs a0) {
   float* ssum = reinterpret_cast<float*>(band_lds + items * tstride);
   float* isum = ssum + items * 4;
   const int row0 = blockIdx.x * R, band = row0 / kTileRows, rsub = row0 % kTileRows;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), nwaves = blockDim.x >> 6;
   const int g = lane / R, r = lane % R;
   constexpr int kTB = kFmt == RMOE_FMT_BFP16 ? kB16TileBytes : kTileBytes;
   using Row = typename std::conditional<kFmt == RMOE_FMT_BFP16, B16Row, Q4Row>::type;

@@ -386,6 +386,8 @@ template <int NC>
 __device__ __forceinline__ void select_rank(const SelectParams a, const float* __restrict__ bias, SelectLds& sl,
                                             bool keys_ready, int stamp_l, int stamp_g) {
   static_assert(NC >= 1 && NC <= kMaxE / 64, "64-expert chunks");
+  // The wave index stays a per-lane value here: as a scalar it measured slower (the rank loop
+  // and the key writes are scheduled differently), unlike in the kernel body.
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int E = a.E, K = a.k;
   const int nc = (E + 63) >> 6;     // 64-key chunks; keys in [E, 64*nc) are 0
@@ -610,7 +612,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
   __shared__ __attribute__((aligned(16))) int dn_d[kMaxDnUnits][2];
   __shared__ uint32_t epoch_s;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int g = blockIdx.x, G = gridDim.x;
   const int Hp = a.H / 2;
   if (tid == 0) {
@@ -701,7 +703,7 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
     // the wave's weight loads.
     int tid_o = (int)threadIdx.x;
     asm volatile("" : "+v"(tid_o));
-    const int tid = tid_o, lane = tid & 63, wave = tid >> 6;
+    const int tid = tid_o, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     unsigned* c_ready = cnt_at(a, l, g % kReadyCopies);
     uint8_t* lay = a.scratch + (size_t)l * a.layer_bytes;
     const uint32_t* xin = reinterpret_cast<const uint32_t*>(lay);

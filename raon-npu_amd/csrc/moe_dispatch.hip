@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256) void dispatch_scatter_kernel(const int32_t* __
                                                                int cap, int shared_rows) {
   __shared__ int slot[4][256];  // per wave: counts, then next output slot per expert
   __shared__ int wsum[4];
-  const int c = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int c = blockIdx.x, tid = threadIdx.x, wave = wave_id(), lane = tid & 63;
   for (int i = tid; i < 4 * 256; i += 256) (&slot[0][0])[i] = 0;
   // This wave's assignments (loaded first, so that their latency overlaps the count reads).
   const int begin = c * kChunk + 256 * wave;

@@ -132,7 +132,7 @@ __device__ __forceinline__ void router_gemm_block(const uint16_t* __restrict__ x
                                                   const uint16_t* __restrict__ w, int E, float* __restrict__ plogits,
                                                   int bx, int by, int bz) {
   __shared__ float part[4][kRouterTok][NFR * 16 + 1];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int l16 = lane & 15, lq = lane >> 4;
   const int q = by, e0 = 16 * NFR * bz;
   const int nsteps = H / 32, sx = 4 * q + wave;
@@ -274,7 +274,7 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
   __shared__ __attribute__((aligned(16))) uint64_t keys[4][256];
   __shared__ float ch[4][16];
   __shared__ int hist[2][256];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int t = blockIdx.x * 4 + wave;
   const int cbase = blockIdx.x * 4 * k / kDispatchChunk;
   if (counts) {
@@ -638,7 +638,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint32_t* __r
   const int e = (int)(te & 511u), row0 = (int)(te >> 9);
   const int rend = group_end(a, e);
   const int nrows = min(kBM, rend - row0);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int l16 = lane & 15, lq = lane >> 4;
   const int nkt = a.K / kTileCols;
   const uint8_t* W = a.wbase + (size_t)e * a.wstride;
@@ -1114,7 +1114,7 @@ __device__ __forceinline__ void gemm_tile_b16(const GemmArgs& a, const uint32_t*
   const int e = (int)(te & 511u), row0 = (int)(te >> 9);
   const int rend = group_end(a, e);
   const int nrows = min(kBM, rend - row0);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int l16 = lane & 15, lq = lane >> 4;
   const int nkt = a.K / kTileCols;
   const uint8_t* W = a.wbase + (size_t)e * a.wstride;

@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256) void linear_kernel(LinearArgs a) {
   const int per = (nkt + a.ksplit - 1) / a.ksplit;
   const int kt0 = ks * per;
   const int nrange = max(0, min(per, nkt - kt0));
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int nwaves = blockDim.x >> 6;
   const int xstride = per * 64;
   uint32_t* xs = lin_lds;
@@ -142,7 +142,7 @@ __global__ __launch_bounds__(1024) void linear_band_kernel(LinearArgs a) {
   const int rsub = row0 % kTileRows;
   const int tok0 = blockIdx.y * kNT;
   const int nt = min(kNT, a.T - tok0);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int nwaves = blockDim.x >> 6;
   const int g = lane / R, r = lane % R;
   const int tstride = 64 + kXPad;

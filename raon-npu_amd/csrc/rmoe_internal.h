@@ -39,6 +39,12 @@ constexpr int kB16MantBytes = 8192;
 inline size_t matrix_bytes_bfp16(int M, int K) { return (size_t)M * (size_t)K * 9 / 8; }
 
 // ------------------------------------------------------------- device helpers --
+// Index of the calling wave in its workgroup as a wave-uniform (scalar) value.  The compiler
+// does not infer that threadIdx.x >> 6 is the same in every lane of a wave, so with the plain
+// expression every per-wave branch becomes an exec-mask region whose saved masks hold scalar
+// registers across it.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
 // float32 -> bf16 bits, round to nearest even, every NaN -> 0x7FC0 (quant/q4nx.py:32-44).
