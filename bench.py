@@ -647,10 +647,21 @@ def _counter_pass(counter: str, out_dir: Path, extra_args: list[str], timeout_s:
     cmd = ["rocprofv3", "--pmc", counter, "--kernel-include-regex", "decode_stack|linear_bfp16|copy|Copy",
            "--output-format", "csv", "-d", str(out_dir), "-o", "run", "--",
            sys.executable, str(ROOT / "bench.py"), "--profile-pass", "--no-prefill"] + extra_args
+    # The pass runs in a process group of its own, so that a pass that overruns is ended
+    # together with the profiled child (rocprofv3 starts the program as its own child).
+    import signal
+
     try:
-        proc = subprocess.run(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.PIPE, timeout=timeout_s)
-    except (OSError, subprocess.TimeoutExpired) as e:
+        proc = subprocess.Popen(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, start_new_session=True)
+    except OSError as e:
         log(f"traffic pass {counter}: {type(e).__name__}: {e}")
+        return None
+    try:
+        proc.wait(timeout=timeout_s)
+    except subprocess.TimeoutExpired:
+        os.killpg(proc.pid, signal.SIGKILL)
+        proc.wait()
+        log(f"traffic pass {counter}: no result within {timeout_s:.0f} s; the pass was ended")
         return None
     csvs = sorted(out_dir.rglob("run_counter_collection.csv"))
     if not csvs:
@@ -691,7 +702,7 @@ def measure_traffic(args) -> dict | None:
     res = {}
     with tempfile.TemporaryDirectory(prefix="rmoe_traffic_") as td:
         for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-            r = _counter_pass(counter, Path(td) / counter, extra, 180.0)
+            r = _counter_pass(counter, Path(td) / counter, extra, 90.0)
             if r is None:
                 return None
             # The two calibration copies are the largest "copy" dispatches of the pass
