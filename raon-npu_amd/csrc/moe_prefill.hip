@@ -77,15 +77,6 @@ __device__ __forceinline__ void split3_bf16(float v, uint32_t& hi, uint32_t& mid
   mid = f32_to_bf16(r);
   lo = f32_to_bf16(r - bf16_to_f32(mid));
 }
-// The same split by truncation (hi = the top 16 bits of v, then of the remainder): each
-// remainder is exact in fp32 and the last part has at most 8 significant bits, so again
-// v = hi + mid + lo exactly; the parts are returned as fp32 values on the bf16 grid.
-__device__ __forceinline__ void split3_trunc(float v, float& hi, float& mid, float& lo) {
-  hi = __uint_as_float(__float_as_uint(v) & 0xffff0000u);
-  const float r = v - hi;
-  mid = __uint_as_float(__float_as_uint(r) & 0xffff0000u);
-  lo = r - mid;
-}
 // bf16 pair (a | b << 16) of two fp32 values on the bf16 grid (their top halves).
 __device__ __forceinline__ uint32_t pack_bf16_top(float a, float b) {
   return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
@@ -755,33 +746,35 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint32_t* __r
   }
   const uint32_t xrow = (uint32_t)l16 * 256u;  // A row 16m + l16: m*4096 + xrow
 
-  // acc += sum_g (min + 8*scale)[r, g] * S[m, g] over one block of 32 groups, both
-  // factors split exactly into 3 bf16 parts; the 6 leading products are kept.  Also
+  // acc += sum_g (min + 8*scale)[r, g] * S[m, g] over one block of 32 groups, as
+  // sum_g min * S + sum_g (8*scale) * S: min and 8*scale are exact bf16 values (a bf16
+  // scale times 8 keeps its 8 significant bits), S is split exactly into 3 bf16 parts, so
+  // the six products are the whole correction and only the fp32 accumulation rounds.  Also
   // tracks the largest scale (as bf16 bits; scales are >= 0) of the lane's weight rows.
   uint32_t smax[2] = {0u, 0u};
   auto corr_block = [&](int blk, const u32x4v (&c)[2][2]) {
     const int gl = 32 * blk + 8 * lq;
-    uint4 bc[2][3];
+    uint4 bmin[2], bsc8[2];
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
       const uint32_t sv[8] = {c[f][0].x, c[f][0].y, c[f][0].z, c[f][0].w, c[f][1].x, c[f][1].y, c[f][1].z, c[f][1].w};
-      float hv[8], mv[8], lv[8];
+      uint32_t w[8];
+      float s8[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const bool live = gl + i < G;
-        const float coef = live ? __uint_as_float(sv[i] & 0xffff0000u) + 8.f * bf16_to_f32(sv[i] & 0xffffu) : 0.f;
-        if (live) smax[f] = max(smax[f], sv[i] & 0x7fffu);
-        split3_trunc(coef, hv[i], mv[i], lv[i]);
+        w[i] = gl + i < G ? sv[i] : 0u;  // groups past G: min 0, scale 0
+        smax[f] = max(smax[f], w[i] & 0x7fffu);
+        s8[i] = 8.f * bf16_to_f32(w[i] & 0xffffu);
       }
-      bc[f][0] = make_uint4(pack_bf16_top(hv[0], hv[1]), pack_bf16_top(hv[2], hv[3]), pack_bf16_top(hv[4], hv[5]),
-                            pack_bf16_top(hv[6], hv[7]));
-      bc[f][1] = make_uint4(pack_bf16_top(mv[0], mv[1]), pack_bf16_top(mv[2], mv[3]), pack_bf16_top(mv[4], mv[5]),
-                            pack_bf16_top(mv[6], mv[7]));
-      bc[f][2] = make_uint4(pack_bf16_top(lv[0], lv[1]), pack_bf16_top(lv[2], lv[3]), pack_bf16_top(lv[4], lv[5]),
-                            pack_bf16_top(lv[6], lv[7]));
+      bmin[f] = make_uint4(pack_bf16_top(__uint_as_float(w[0]), __uint_as_float(w[1])),
+                           pack_bf16_top(__uint_as_float(w[2]), __uint_as_float(w[3])),
+                           pack_bf16_top(__uint_as_float(w[4]), __uint_as_float(w[5])),
+                           pack_bf16_top(__uint_as_float(w[6]), __uint_as_float(w[7])));
+      bsc8[f] = make_uint4(pack_bf16_top(s8[0], s8[1]), pack_bf16_top(s8[2], s8[3]), pack_bf16_top(s8[4], s8[5]),
+                           pack_bf16_top(s8[6], s8[7]));
     }
     const uint8_t* ss = lds + 2 * kStageBytes + (blk & 1) * kSBlock + l16 * kSRow + 16 * lq;
-    // Six products per (m, f), smallest first; consecutive MFMAs go to different
+    // Six products per (m, f), the low part of S first; consecutive MFMAs go to different
     // accumulators (16 independent chains).
 #pragma unroll
     for (int half = 0; half < (MF + 3) / 4; ++half) {
@@ -803,8 +796,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint32_t* __r
           for (int f = 0; f < 2; ++f) {
             const int m = 4 * half + mm;
             if (m >= MF) continue;
-            const uint4 av = p == 0 ? al[mm] : (p == 1 || p == 3) ? am[mm] : ah[mm];
-            const uint4 bv = (p == 0 || p == 3 || p == 5) ? bc[f][0] : (p == 1 || p == 4) ? bc[f][1] : bc[f][2];
+            const uint4 av = p < 2 ? al[mm] : p < 4 ? am[mm] : ah[mm];
+            const uint4 bv = (p & 1) ? bsc8[f] : bmin[f];
             acc[m][f] = mfma16(av, bv, acc[m][f]);
           }
     }
