@@ -255,7 +255,10 @@ int rmoe_moe_decode(rmoe_ctx* ctx, int layer, const uint16_t* x, uint16_t* out, 
  * keeps one workgroup per CU resident; its waits are bounded (a timeout is reported as
  * RMOE_EDEVICE by the next synchronous call).  Every layer must have a router and a
  * shared expert.  rmoe_reserve_decode_stack sizes the hand-off buffers (host call,
- * allocates); the _dev call never allocates. */
+ * allocates); the _dev call never allocates.  The host form rmoe_moe_decode_stack (and
+ * rmoe_moe_decode) first waits for all of this process's work on the device, so that no
+ * kernel queued earlier on another stream holds CUs; with the _dev form that is the
+ * caller's to ensure. */
 int rmoe_reserve_decode_stack(rmoe_ctx* ctx, const int* layers, int n_layers);
 /* Diagnostic, no counterpart in the reference: the number of polls (about a microsecond
  * each) after which a wait of the persistent decode kernel gives up (0 restores the default,

@@ -1015,6 +1015,11 @@ int rmoe_moe_decode_stack(rmoe_ctx* ctx, const int* layers, int n_layers, const 
   const size_t xb = align_up((size_t)L.H * 2, 256), rb = align_up((size_t)n_layers * L.top_k * 4, 256);
   uint8_t* io;
   TRY(io_area(ctx, 2 * xb + 2 * rb, &io));
+  // The persistent kernel needs every CU: the synchronous entry point first waits for all
+  // work this process has queued on the device (any stream), so none of it can still hold
+  // CUs when the stack starts.  (Work of other processes, and the _dev entry points, which
+  // a caller may capture into a graph, are the caller's to keep apart.)
+  HIP_TRY(hipDeviceSynchronize());
   HIP_TRY(hipMemcpyAsync(io, x, (size_t)L.H * 2, hipMemcpyHostToDevice, ctx->stream));
   TRY(rmoe_moe_decode_stack_dev(ctx, layers, n_layers, io, io + xb, residual, act, gate_beta, value_beta,
                                 io + 2 * xb, io + 2 * xb + rb, nullptr));
