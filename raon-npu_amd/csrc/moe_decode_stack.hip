@@ -374,7 +374,8 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 //
 // Keys sit in LDS in quarters of 32 (E <= 128) or 64 keys with 16 bytes between
 // quarters, so the four quarter reads of one instruction fall in different banks.
-__device__ __forceinline__ int key_pos(int e, int qkeys) { return e + 2 * (e / qkeys); }
+// qkeys is 32 or 64: a shift, not an integer division.
+__device__ __forceinline__ int key_pos(int e, int qkeys) { return e + 2 * (e >> (qkeys == 32 ? 5 : 6)); }
 
 __device__ __forceinline__ bool select_fast(const SelectParams a, const float* bias) {
   return a.score == 1 && bias == nullptr;
@@ -783,7 +784,16 @@ __global__ __launch_bounds__(kThreads) void decode_stack_kernel(StackArgs a) {
         if (j1 < nf4) *reinterpret_cast<uint4*>(lrow + r1 * lstride + 4 * (j1 - r1 * rq)) = pv1;
         __syncthreads();
         if (b0 == 0) RMOE_STAMP(l, g, 12, 0);
-        if (pe < a.E) {
+        if (pe < a.E && nb == 8 * P) {
+          // The pass holds exactly eight of the thread's bands (BASELINE: 32 bands, P = 4):
+          // the same reads and sums as the loop below, without its bounds tests.
+          const float* lp = lrow + pp * lstride + pe;
+          const int bs = P * lstride;
+          float v[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[i] = lp[i * bs];
+          lacc += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+        } else if (pe < a.E) {
           // Eight of the thread's bands are read at a time (one LDS round trip, not one
           // per band), then added in band order.
           for (int bb = pp; bb < nb; bb += 8 * P) {
