@@ -555,26 +555,33 @@ __device__ __forceinline__ void ring_wait(int pending) {
     default: asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
   }
 }
-// The same, tying the coefficient registers of gload16() to the wait.
-#define RMOE_WAIT_TIED(N, c)                                                                             \
-  asm volatile("s_waitcnt vmcnt(" #N ") lgkmcnt(0)\n\ts_barrier"                                        \
-               : "+v"(c[0][0]), "+v"(c[0][1]), "+v"(c[1][0]), "+v"(c[1][1])::"memory")
-// RMOE_WAIT_TIED with a count known only at run time, among the values the grouped GEMM
-// uses (they depend on the tile class and the wave).
+// Hands the coefficient registers of gload16() to the compiler: placed after the wait
+// that covers their loads, it is where their values are defined for the code after it.
+__device__ __forceinline__ void tie_coef(u32x4v (&c)[2][2]) {
+  asm volatile("" : "+v"(c[0][0]), "+v"(c[0][1]), "+v"(c[1][0]), "+v"(c[1][1])::"memory");
+}
+#define RMOE_VM_WAIT(N) asm volatile("s_waitcnt vmcnt(" #N ") lgkmcnt(0)\n\ts_barrier" ::: "memory")
+// ring_wait for the counts of the coefficient waits (they depend on the tile class and
+// the wave), then tie_coef().  The branches of the switch hold no register operands: had
+// each branch's wait also tied the registers, the values would merge after the switch
+// and the compiler would copy the loaded registers into the ones it chose for each
+// branch, before that branch's wait -- copies that read a register whose load has not
+// yet landed.
 __device__ __forceinline__ void wait_tied(int pending, u32x4v (&c)[2][2]) {
   switch (pending) {
-    case 17: RMOE_WAIT_TIED(17, c); break;
-    case 15: RMOE_WAIT_TIED(15, c); break;
-    case 14: RMOE_WAIT_TIED(14, c); break;
-    case 13: RMOE_WAIT_TIED(13, c); break;
-    case 12: RMOE_WAIT_TIED(12, c); break;
-    case 11: RMOE_WAIT_TIED(11, c); break;
-    case 10: RMOE_WAIT_TIED(10, c); break;
-    case 9: RMOE_WAIT_TIED(9, c); break;
-    case 8: RMOE_WAIT_TIED(8, c); break;
-    case 6: RMOE_WAIT_TIED(6, c); break;
-    default: RMOE_WAIT_TIED(0, c); break;
+    case 17: RMOE_VM_WAIT(17); break;
+    case 15: RMOE_VM_WAIT(15); break;
+    case 14: RMOE_VM_WAIT(14); break;
+    case 13: RMOE_VM_WAIT(13); break;
+    case 12: RMOE_VM_WAIT(12); break;
+    case 11: RMOE_VM_WAIT(11); break;
+    case 10: RMOE_VM_WAIT(10); break;
+    case 9: RMOE_VM_WAIT(9); break;
+    case 8: RMOE_VM_WAIT(8); break;
+    case 6: RMOE_VM_WAIT(6); break;
+    default: RMOE_VM_WAIT(0); break;
   }
+  tie_coef(c);
 }
 // Largest of v over the 16 lanes of a DPP row, in every lane of the row: quad swaps, then
 // the half-row and row mirrors (VALU moves, no LDS permute).
@@ -814,7 +821,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint32_t* __r
     u32x4v cfb[2][2];
     load_coef(blk, cfb);
     issue_s(blk);
-    RMOE_WAIT_TIED(0, cfb);
+    wait_tied(0, cfb);
     corr_block(blk, cfb);
   }
 

@@ -44,11 +44,18 @@ def _check_dev(t, shape: tuple, dtype_name: str, name: str):
         raise ValueError(f"{name} must be contiguous")
 
 
+_HIP_STREAM_LEGACY = 1  # hipStreamLegacy: the null stream, with its implicit ordering
+
+
 def _stream_ptr(stream) -> int | None:
+    """The HIP stream handle for a ``stream`` argument: None selects the context's own
+    stream (the library's NULL).  A torch stream whose handle is 0 -- torch's default
+    stream, HIP's null stream -- is passed as hipStreamLegacy, since a 0 handle would
+    select the context's stream, which is not ordered with torch's work."""
     if stream is None:
         return None
     if hasattr(stream, "cuda_stream"):
-        return stream.cuda_stream
+        return stream.cuda_stream or _HIP_STREAM_LEGACY
     return int(stream)
 
 

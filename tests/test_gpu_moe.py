@@ -205,6 +205,50 @@ def test_prefill_config3_matches_oracle(baseline):
     np.testing.assert_array_equal(out_r.cpu().numpy().view(np.uint16), f32_to_bf16(bf16_to_f32(xs) + bf16_to_f32(o)))
 
 
+def test_prefill_repeated_calls_identical(baseline):
+    """The grouped GEMM is deterministic: repeated calls on the same input give the same
+    bits.  Config 3's 445 tokens fill all three tile classes (<=32, 33-64 and >64 rows);
+    a register copy taken before a coefficient load landed once corrupted one expert's
+    rows in about one call in twenty, so the calls are many and compared on the device."""
+    import torch
+
+    geom, lyr, _, _ = baseline
+    T = 445
+    xs = random_tokens(T, geom.hidden, 610)
+    xd = torch.from_numpy(xs.view(np.int16)).cuda()
+    stream = torch.cuda.current_stream()
+    first = torch.empty_like(xd)
+    out = torch.empty_like(xd)
+    lyr.moe_prefill_dev(xd, T, first, residual=False, stream=stream)
+    bad = []
+    for i in range(150):
+        out.fill_(0x7777)
+        lyr.moe_prefill_dev(xd, T, out, residual=False, stream=stream)
+        if not torch.equal(out, first):
+            bad.append((i, int((out != first).any(1).sum())))
+    assert not bad, f"calls differing from the first (call, rows): {bad}"
+
+    # The grouped experts entry point, with a hot expert (every token) and cold ones.
+    T = 300
+    rng = np.random.default_rng(631)
+    ids = np.zeros((T, geom.top_k), np.int32)
+    for t in range(T):
+        ids[t] = np.concatenate([[0], rng.choice(np.arange(1, geom.n_routed), geom.top_k - 1, replace=False)])
+    idd = torch.from_numpy(ids).cuda()
+    wd = torch.from_numpy(rng.random((T, geom.top_k), dtype=np.float32)).cuda()
+    xd = torch.from_numpy(random_tokens(T, geom.hidden, 632).view(np.int16)).cuda()
+    sd = torch.from_numpy(random_tokens(T, 2 * geom.inter, 633).view(np.int16)).cuda()
+    r0, s0 = torch.empty_like(xd), torch.empty_like(xd)
+    ro, so = torch.empty_like(xd), torch.empty_like(xd)
+    lyr.moe_experts_grouped_dev(xd, idd, wd, sd, r0, s0, None, None, stream=stream)
+    for i in range(100):
+        ro.fill_(0x7777)
+        lyr.moe_experts_grouped_dev(xd, idd, wd, sd, ro, so, None, None, stream=stream)
+        if not (torch.equal(ro, r0) and torch.equal(so, s0)):
+            bad.append(i)
+    assert not bad, f"grouped calls differing from the first: {bad}"
+
+
 def test_grouped_skewed_routing(baseline):
     """Load-imbalanced groups (hot expert with every token, cold experts with 1-2) and
     ragged tails: grouped routed sums and shared rows vs the token-serial oracle."""
