@@ -40,8 +40,8 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 # child `bench.py --profile-pass` runs, calibrated against a 512 MiB copy).  These are the
 # figures of the committed counter profile (profiles/decode_prefill_hbm_counters.txt),
 # reported instead only when rocprofv3 is absent, a pass fails, or --no-traffic is given.
-DECODE_TRAFFIC_BYTES = 1338292512
-LM_HEAD_TRAFFIC_BYTES = 749777961
+DECODE_TRAFFIC_BYTES = 1338163081
+LM_HEAD_TRAFFIC_BYTES = 749714547
 
 
 def log(msg: str) -> None:
@@ -258,7 +258,7 @@ def roofline(bound: str, work: float, seconds: float, kernel: str, per: str, tra
 # WRITE_SIZE over `bench.py --profile-configs` (calibrated against a 512 MiB copy); the
 # summary and commands are in profiles/configs123_hbm_counters.txt.  Re-measure after
 # changing the kernels.
-CONFIG_TRAFFIC_BYTES = {"config1_gemv": 1142209, "config2_decode_layer": 28710137, "config3_prefill_445": 466973329}
+CONFIG_TRAFFIC_BYTES = {"config1_gemv": 1059270, "config2_decode_layer": 28544825, "config3_prefill_445": 466689316}
 
 
 class ConfigWorkloads:
