@@ -509,12 +509,15 @@ typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
 // 16 bytes per lane from global memory straight into LDS: lane L writes lds + 16 L.
 // Written as inline assembly so that the compiler does not treat every later LDS read
 // as dependent on it (it would wait for all outstanding loads before each one); the
-// kernel's own waits order the copies.  M0 is saved and restored.
+// kernel's own waits order the copies.  M0 is saved and restored.  On gfx9 an LDS copy
+// needs one wait state after an SALU write of M0 (the compiler pads its own copies the
+// same way, but cannot see inside an asm statement): hence the s_nop.
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
   uint32_t saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
       "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
       "global_load_lds_dwordx4 %1, off\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
@@ -529,6 +532,7 @@ __device__ __forceinline__ void dma16_nt(const void* g, uint32_t lds) {
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
       "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
       "global_load_lds_dwordx4 %1, off nt\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)

@@ -9,6 +9,11 @@ the two that reads, copies or spills those registers sees whatever they held bef
 Such a copy once sat before the wait, inside each branch of a switch over the wait
 count, and corrupted one expert's rows in a few percent of calls.  This test compiles
 the file to assembly and checks every such load.
+
+It also checks the LDS copies (``global_load_lds_dwordx4``): on gfx9 one takes M0 as its
+LDS address and needs one wait state after an SALU write of M0.  The compiler pads the
+copies it emits itself; the grouped GEMM's copies are inline assembly that set M0 and
+must pad it themselves.
 """
 
 from __future__ import annotations
@@ -95,18 +100,51 @@ def test_scanner_flags_a_copy_before_the_wait():
     assert uncounted_load_hazards(head + other + wait + copy, "grouped_gemm") == (1, [])
 
 
-def test_grouped_gemm_coefficient_registers_untouched_before_wait(tmp_path):
+def m0_lds_dma_hazards(asm_text: str):
+    """LDS copies whose preceding instruction (in code order) writes M0."""
+    hazards, prev = [], None
+    for i, t, _ in _instructions(asm_text.split("\n")):
+        if re.match(r"^(global|buffer)_load_lds", t) and prev and re.match(r"^s_\w+\s+m0\b", prev[1]):
+            hazards.append((i + 1, prev[1], t))
+        prev = (i, t)
+    return hazards
+
+
+def test_scanner_flags_an_lds_copy_right_after_m0():
+    asm = "\ts_mov_b32 m0, s6\n\tglobal_load_lds_dwordx4 v[4:5], off\n"
+    padded = "\ts_mov_b32 m0, s6\n\ts_nop 0\n\tglobal_load_lds_dwordx4 v[4:5], off\n"
+    assert m0_lds_dma_hazards(asm) and not m0_lds_dma_hazards(padded)
+
+
+def _device_asm(tmp_path, name: str) -> str:
     b = _load_build_module()
     hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not shutil.which(hipcc):
         pytest.skip("hipcc not available")
-    src = b.PKG / "csrc" / "moe_prefill.hip"
-    out = tmp_path / "moe_prefill.s"
+    src = b.PKG / "csrc" / name
+    out = tmp_path / (src.stem + ".s")
     cmd = [hipcc, *b.COMMON, "-I", str(b.PKG.parent / "include"), "--cuda-device-only", "-S", str(src), "-o",
            str(out)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     assert res.returncode == 0, res.stderr[-2000:]
-    loads, hazards = uncounted_load_hazards(out.read_text(), "grouped_gemm_kernel")
+    return out.read_text()
+
+
+@pytest.fixture(scope="module")
+def prefill_asm(tmp_path_factory):
+    return _device_asm(tmp_path_factory.mktemp("asm"), "moe_prefill.hip")
+
+
+def test_grouped_gemm_coefficient_registers_untouched_before_wait(prefill_asm):
+    loads, hazards = uncounted_load_hazards(prefill_asm, "grouped_gemm_kernel")
     # eight coefficient loads ahead of the K loop and four per later block, per tile class
     assert loads >= 36, loads
+    assert not hazards, hazards[:10]
+
+
+@pytest.mark.parametrize("name", ["moe_prefill.hip", "moe_decode_stack.hip"])
+def test_lds_copies_wait_after_m0(prefill_asm, tmp_path, name):
+    text = prefill_asm if name == "moe_prefill.hip" else _device_asm(tmp_path, name)
+    assert text.count("global_load_lds_dwordx4") > 0
+    hazards = m0_lds_dma_hazards(text)
     assert not hazards, hazards[:10]
