@@ -271,6 +271,51 @@ def test_grouped_skewed_routing(baseline):
     _check(sdown, s_ref, "skewed shared_down")
 
 
+def _ids_with_counts(T: int, k: int, E: int, counts: dict[int, int]) -> np.ndarray:
+    """Routing ids [T, k] with k distinct experts per token in which expert e holds exactly
+    counts[e] rows; the remaining rows go to the other experts.  Experts are placed in
+    descending order of count, each on the tokens with the most free slots (ties by token
+    index), which meets every count when max(counts) <= T."""
+    rest = [e for e in range(E) if e not in counts]
+    total_rest = T * k - sum(counts.values())
+    want = dict(counts)
+    for i, e in enumerate(rest):
+        want[e] = total_rest // len(rest) + (1 if i < total_rest % len(rest) else 0)
+    free = np.full(T, k)
+    ids = [[] for _ in range(T)]
+    for e in sorted(want, key=lambda e: (-want[e], e)):
+        toks = np.lexsort((np.arange(T), -free))[: want[e]]
+        assert (free[toks] > 0).all()
+        for t in toks:
+            ids[t].append(e)
+        free[toks] -= 1
+    assert not free.any()
+    out = np.array(ids, np.int64)
+    for e, c in counts.items():
+        assert int((out == e).sum()) == c
+    return out
+
+
+def test_grouped_tile_class_boundaries(baseline):
+    """Experts whose row counts sit on either side of every tile boundary: the fragment
+    classes (16 rows per fragment; tiles of up to 32, 64 and 128 rows) and whole 128-row
+    tiles (127/128/129, 255/256/257 rows), so every class runs full, partly filled and
+    one-row tiles in both GEMMs.  Grouped routed sums and shared rows vs the oracle."""
+    geom, lyr, bank, _ = baseline
+    T = 260
+    counts = {0: 257, 1: 256, 2: 255, 3: 129, 4: 128, 5: 127, 6: 65, 7: 64, 8: 63, 9: 49, 10: 48, 11: 47,
+              12: 33, 13: 32, 14: 31, 15: 17, 16: 16, 17: 15, 18: 1}
+    ids = _ids_with_counts(T, geom.top_k, geom.n_routed, counts)
+    xs = random_tokens(T, geom.hidden, 640)
+    rng = np.random.default_rng(641)
+    w = rng.random((T, geom.top_k), dtype=np.float32)
+    sgu = np.stack([om.shared_gate_up(bank, geom.shared_id, x) for x in xs])
+    routed, sdown = lyr.moe_experts_grouped(xs, ids, w, sgu, None, None)
+    r_ref, s_ref = om.moe_experts_grouped_batched(bank, xs, ids, w, sgu, geom.shared_id, None, None)
+    _check(routed, r_ref, "class-boundary routed")
+    _check(sdown, s_ref, "class-boundary shared_down")
+
+
 def test_reference_model_shape(gpu_ctx):
     """The reference model's shape (host/raon.py:127-142; kernels/moe/pack.py:46-69):
     H=2560, I=1088 (down input padded to 1280), top-6, sigmoid router with selection bias
