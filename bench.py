@@ -254,10 +254,11 @@ def roofline(bound: str, work: float, seconds: float, kernel: str, per: str, tra
             "traffic": traffic}
 
 
-# HBM bytes per launch of the configs 1-3 workloads measured with rocprofv3 FETCH_SIZE and
-# WRITE_SIZE over `bench.py --profile-configs` (calibrated against a 512 MiB copy); the
-# summary and commands are in profiles/configs123_hbm_counters.txt.  Re-measure after
-# changing the kernels.
+# HBM bytes per launch of the configs 1-3 workloads: each default run measures them itself
+# (measure_config_traffic: rocprofv3 FETCH_SIZE and WRITE_SIZE over a child
+# `bench.py --profile-configs`, calibrated against a 512 MiB copy).  These are the figures
+# of the committed counter profile (profiles/configs123_hbm_counters.txt), reported instead
+# only when rocprofv3 is absent, a pass fails, or --no-traffic is given.
 CONFIG_TRAFFIC_BYTES = {"config1_gemv": 1059270, "config2_decode_layer": 28544825, "config3_prefill_445": 466689316}
 
 
@@ -635,18 +636,36 @@ def profile_pass(ctx, layers, geom, args, stream, gen) -> int:
     return 0
 
 
-def _counter_pass(counter: str, out_dir: Path, extra_args: list[str], timeout_s: float) -> dict | None:
-    """One rocprofv3 counter pass over a child `bench.py --profile-pass` (this script, run
+def _kind_profile_pass(name: str) -> str:
+    """Kernel kind of a dispatch of `bench.py --profile-pass`."""
+    return "stack" if "decode_stack" in name else "lm_head" if "linear_bfp16" in name else "copy"
+
+
+# Kernel kinds of a dispatch of `bench.py --profile-configs` (the first match counts;
+# other dispatches, such as the weight synthesis, are left out).
+_CONFIG_KINDS = (("copyBuffer", "copy"), ("CopyBuffer", "copy"), ("linear_lane_kernel", "config1"),
+                 ("decode_stack_kernel", "config2"), ("router_prep_kernel", "c3_router"),
+                 ("topk_kernel", "c3_topk"), ("dispatch_scatter_kernel", "c3_scatter"),
+                 ("grouped_gemm_kernel", "c3_gemm"), ("h_unify_kernel", "c3_unify"), ("combine_kernel", "c3_combine"))
+
+
+def _kind_profile_configs(name: str) -> str | None:
+    return next((k for pat, k in _CONFIG_KINDS if pat in name), None)
+
+
+def _counter_pass(counter: str, out_dir: Path, child_args: list[str], kind_of, timeout_s: float,
+                  regex: str | None = None) -> dict | None:
+    """One rocprofv3 counter pass over a child `bench.py <child_args>` (this script, run
     as a separate process; this process only waits).  Returns {kernel kind: [per-dispatch
-    counter sums]} for the calibration copy ("copy"), the decode stack ("stack") and the
-    lm_head GEMV ("lm_head"), or None when the pass did not produce its CSV."""
+    counter sums, in dispatch order]} with the kinds that kind_of gives the kernel names
+    (None: left out), or None when the pass did not produce its CSV."""
     import csv
     import subprocess
     from collections import defaultdict
 
-    cmd = ["rocprofv3", "--pmc", counter, "--kernel-include-regex", "decode_stack|linear_bfp16|copy|Copy",
-           "--output-format", "csv", "-d", str(out_dir), "-o", "run", "--",
-           sys.executable, str(ROOT / "bench.py"), "--profile-pass", "--no-prefill"] + extra_args
+    cmd = ["rocprofv3", "--pmc", counter] + (["--kernel-include-regex", regex] if regex else []) + [
+        "--output-format", "csv", "-d", str(out_dir), "-o", "run", "--",
+        sys.executable, str(ROOT / "bench.py")] + child_args
     # The pass runs in a process group of its own, so that a pass that overruns is ended
     # together with the profiled child (rocprofv3 starts the program as its own child).
     import signal
@@ -676,13 +695,32 @@ def _counter_pass(counter: str, out_dir: Path, extra_args: list[str], timeout_s:
             d = int(row["Dispatch_Id"])
             per[d] += float(row["Counter_Value"])
             names[d] = row["Kernel_Name"]
-    out = {"copy": [], "stack": [], "lm_head": []}
+    out = defaultdict(list)
     for d in sorted(per):
-        n = names[d]
-        kind = "stack" if "decode_stack" in n else "lm_head" if "linear_bfp16" in n else "copy"
-        out[kind].append(per[d])
+        kind = kind_of(names[d])
+        if kind is not None:
+            out[kind].append(per[d])
     # rocprofv3 can end with a fault of its own after a complete run; complete CSVs count.
-    return out if out["copy"] and out["stack"] else None
+    return dict(out) if out.get("copy") else None
+
+
+def _calibrated_passes(child_args: list[str], kind_of, regex: str | None, tag: str) -> dict | None:
+    """FETCH_SIZE, then WRITE_SIZE over the child, each per-dispatch value scaled to bytes
+    by what the same counter reads for the child's 512 MiB calibration copy (its two
+    largest copy dispatches).  {counter: {kind: [bytes per dispatch]}, counter + "_factor": f}."""
+    import statistics
+    import tempfile
+
+    res = {}
+    with tempfile.TemporaryDirectory(prefix=f"rmoe_traffic_{tag}_") as td:
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            r = _counter_pass(counter, Path(td) / counter, child_args, kind_of, 90.0, regex)
+            if r is None:
+                return None
+            factor = 512 * 1024 * 1024 / statistics.median(sorted(r["copy"])[-2:])
+            res[counter] = {k: [v * factor for v in vals] for k, vals in r.items()}
+            res[counter + "_factor"] = factor
+    return res
 
 
 def measure_traffic(args) -> dict | None:
@@ -693,31 +731,55 @@ def measure_traffic(args) -> dict | None:
     read, 512 MiB written).  None when rocprofv3 is absent or a pass fails."""
     import shutil
     import statistics
-    import tempfile
 
     if shutil.which("rocprofv3") is None:
         log("traffic: rocprofv3 not found; roofline.traffic falls back to the committed figure")
         return None
-    extra = ["--seed", str(args.seed), "--layers", str(args.layers)] + (["--no-lm-head"] if args.no_lm_head else [])
-    res = {}
-    with tempfile.TemporaryDirectory(prefix="rmoe_traffic_") as td:
-        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-            r = _counter_pass(counter, Path(td) / counter, extra, 90.0)
-            if r is None:
-                return None
-            # The two calibration copies are the largest "copy" dispatches of the pass
-            # (the stack build's dtype conversions are small ones).
-            copy_bytes = 512 * 1024 * 1024
-            factor = copy_bytes / statistics.median(sorted(r["copy"])[-2:])
-            res[counter] = {k: statistics.median(v) * factor for k, v in r.items() if v}
-            res[counter]["factor_bytes_per_unit"] = factor
+    child = ["--profile-pass", "--no-prefill", "--seed", str(args.seed), "--layers", str(args.layers)] + (
+        ["--no-lm-head"] if args.no_lm_head else [])
+    res = _calibrated_passes(child, _kind_profile_pass, "decode_stack|linear_bfp16|copy|Copy", "stack")
+    if res is None or "stack" not in res["FETCH_SIZE"] or "stack" not in res["WRITE_SIZE"]:
+        return None
+    med = {c: {k: statistics.median(v) for k, v in res[c].items()} for c in ("FETCH_SIZE", "WRITE_SIZE")}
     out = {
-        "stack": res["FETCH_SIZE"]["stack"] + res["WRITE_SIZE"]["stack"],
-        "fetch_factor": res["FETCH_SIZE"]["factor_bytes_per_unit"],
-        "write_factor": res["WRITE_SIZE"]["factor_bytes_per_unit"],
+        "stack": med["FETCH_SIZE"]["stack"] + med["WRITE_SIZE"]["stack"],
+        "fetch_factor": res["FETCH_SIZE_factor"],
+        "write_factor": res["WRITE_SIZE_factor"],
     }
-    if "lm_head" in res["FETCH_SIZE"] and "lm_head" in res["WRITE_SIZE"]:
-        out["lm_head"] = res["FETCH_SIZE"]["lm_head"] + res["WRITE_SIZE"]["lm_head"]
+    if "lm_head" in med["FETCH_SIZE"] and "lm_head" in med["WRITE_SIZE"]:
+        out["lm_head"] = med["FETCH_SIZE"]["lm_head"] + med["WRITE_SIZE"]["lm_head"]
+    return out
+
+
+def measure_config_traffic(args) -> dict | None:
+    """HBM bytes per launch of configs 1-3, measured in this run like measure_traffic but
+    over a child `bench.py --profile-configs --layers 1` (the calibration copy, then 20
+    config-1 GEMVs, 10 config-2 1-layer decode launches and 5 config-3 prefill layers, one at
+    a time): config 1 and 2 the median dispatch of their kernel, config 3 the sum over its
+    kernels of their median dispatch (the grouped GEMM's gate/up and down dispatches
+    alternate).  None when rocprofv3 is absent or a pass fails."""
+    import shutil
+    import statistics
+
+    if shutil.which("rocprofv3") is None:
+        return None
+    res = _calibrated_passes(["--profile-configs", "--layers", "1", "--seed", str(args.seed)],
+                             _kind_profile_configs, None, "configs")
+    if res is None:
+        return None
+    out = {}
+    c3_kinds = ("c3_router", "c3_topk", "c3_scatter", "c3_unify", "c3_combine")
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        r = res[c]
+        if not all(k in r for k in ("config1", "config2", "c3_gemm") + c3_kinds) or len(r["c3_gemm"]) < 2:
+            log(f"traffic: the configs pass of {c} lacks a kernel; configs keep the committed figures")
+            return None
+        med = {k: statistics.median(v) for k, v in r.items()}
+        gemm = r["c3_gemm"]
+        c3 = sum(med[k] for k in c3_kinds) + statistics.median(gemm[0::2]) + statistics.median(gemm[1::2])
+        for name, v in (("config1_gemv", med["config1"]), ("config2_decode_layer", med["config2"]),
+                        ("config3_prefill_445", c3)):
+            out[name] = out.get(name, 0.0) + v
     return out
 
 
@@ -988,6 +1050,22 @@ def main() -> int:
                 f"{time.perf_counter() - t_tr:.0f} s")
     if lm_head is not None and "traffic_source" not in lm_head:
         lm_head["traffic_source"] = "committed counter profile"
+    if configs:
+        ctr = None
+        if not args.no_traffic:
+            torch.cuda.synchronize()
+            t_tr = time.perf_counter()
+            ctr = measure_config_traffic(args)
+            if ctr is not None:
+                log("traffic: configs 1-3 " + ", ".join(f"{k} {v / 1e6:.2f} MB" for k, v in ctr.items()) +
+                    f" per launch, {time.perf_counter() - t_tr:.0f} s")
+        for name in CONFIG_TRAFFIC_BYTES:
+            if name in configs:
+                rl = configs[name]["roofline"]
+                if ctr is not None:
+                    rl["traffic"] = int(ctr[name])
+                rl["traffic_source"] = ("rocprofv3 FETCH_SIZE + WRITE_SIZE, this run" if ctr is not None
+                                        else "committed counter profile")
 
     line = {
         "metric": "MoE decode tokens/s (48-layer q4nx stack, batch 1); prefill grouped-GEMM TFLOP/s in 'prefill'",
