@@ -624,13 +624,15 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
 //   gate/up: intermediate units 128*nt + 16w..+15: fragment 0 the gate rows, 1 the up
 //            rows, so the activation stays in the lane;
 //   down:    output rows 256*nt + 16w and 256*nt + 128 + 16w.
-// Per group the MFMA runs on the codes as exact bf16 values 16 + n; the group's scale
-// is applied by one fp32 FMA per output:
-//   y = sum_g scale_g * sum_k x_k (16 + n_k) + sum_g (min_g - 16 scale_g) * S_g.
-// The second sum (the correction) runs first, from group sums copied into ring slot 2
-// while the first two K steps' copies are in flight.  K loop: a three-deep LDS ring
-// filled by global->LDS copies; per K step one barrier, then the copy for step kt+2
-// into the slot step kt-1 used.
+// With w = (min + 8 scale) + scale (n - 8) per group g of 32 columns:
+//   y = sum_g sum_k x_k scale_g (n_k - 8) + sum_g (min_g + 8 scale_g) * S_g,
+// S_g the group sums of the row.  The first sum runs on fp16 MFMAs: A the row scaled by
+// its power-of-two exponent, B = scale (n - 8) scaled by the lane's weight-row exponent
+// (exact in fp16: a bf16 scale times an integer of magnitude <= 8), fp32 accumulation.
+// The second sum (the correction) runs first, on bf16 MFMAs with exact operands, from
+// group sums copied into ring slot 2 while the first two K steps' copies are in flight.
+// K loop: a three-deep LDS ring filled by global->LDS copies; per K step one barrier,
+// then the copy for step kt+2 into the slot step kt-1 used.
 // One (m-tile, n-tile) with MF live 16-row fragments; tl is the tile list of its class.
 // lds / rowidx / row_e are the kernel's shared arrays.
 template <int MF>
