@@ -8,13 +8,14 @@
 //   sum_k x[m,k] w[r,k] = sum_k x[m,k] * (scale[r]*(n[r,k] - 8)) + (min[r] + 8*scale[r]) * S[m]
 // with S[m] = sum_k x[m,k].  scale*(n-8) has at most 11 significant bits (8 of the bf16
 // scale times |n-8| <= 8), so it is exact in fp16, and so is every bf16 activation: the
-// first sum is one v_mfma_f32_16x16x32_f16 per group with no per-group fix-up, and the
-// MFMAs of all groups accumulate in place.  Range: activation rows carry a power-of-two
+// first sum runs on v_mfma_f32_16x16x32_f16 with no per-group fix-up, the MFMAs of all
+// groups accumulating in place.  Range: activation rows carry a power-of-two
 // exponent (x rows are normalised to max |x| in [2^14, 2^15); h chunks of 128 units are
 // scaled only when their largest value is outside [2^-6, 2^15)) and each weight row's
 // scales are normalised by a power of two (largest scale in [2^11, 2^12)); the
-// exponents are undone exactly in fp32.  The correction (second sum) is a small GEMM over the groups, done on bf16 MFMA
-// with S and the coefficient split exactly into three bf16 parts (six leading products).
+// exponents are undone exactly in fp32.  The correction (second sum) is a small GEMM over
+// the groups on bf16 MFMA: min and 8*scale are exact bf16 values and S is split exactly
+// into three bf16 parts, so its six products are the whole correction.
 #include "../../include/raon_moe.h"
 #include "rmoe_internal.h"
 
