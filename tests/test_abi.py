@@ -55,3 +55,20 @@ def test_geometry_matches_reference_constants():
 
 def test_package_exports():
     assert raon_npu_amd.BASELINE.top_k == 8
+
+
+def test_stream_argument_mapping():
+    """The wrappers' stream argument: None selects the context's stream (the library's
+    NULL); a torch stream passes its handle, and torch's default stream (handle 0, HIP's
+    null stream) is passed as hipStreamLegacy (1), since a 0 handle would select the
+    context's own stream, which is not ordered with torch's work."""
+    from raon_npu_amd.device import _stream_ptr
+
+    class FakeStream:
+        def __init__(self, handle):
+            self.cuda_stream = handle
+
+    assert _stream_ptr(None) is None
+    assert _stream_ptr(FakeStream(0)) == 1
+    assert _stream_ptr(FakeStream(0x7F00AB00)) == 0x7F00AB00
+    assert _stream_ptr(0x1234) == 0x1234
